@@ -1,0 +1,262 @@
+"""Headline benchmark: triangle attention (ending node) fwd+bwd, N=768, H=4, c=32, bf16, one MI355X.
+
+One "step" = forward + backward (dQ, dK, dV, dBias) of ``oops_amd.triangle_attention`` on
+q, k, v ``randn(1, 768, 768, 4, 32)`` bf16 passed as ``.transpose(1, 2)``
+views (ending node, swapped pair axes, read in place), bias ``randn(1, 1, 4, 768, 768)`` bf16
+shared over rows, no mask, upstream gradient ``randn`` in the output's layout.  Inputs are
+resident in HBM before timing.  Algorithmic FLOPs per step = 14 * H * c * N^3 (flash
+convention).
+
+Prints ONE JSON line with the driver's contract fields plus ``roofline`` (dominant kernel,
+timed live with HIP events on the launch stream) and ``cpu_baseline`` (the numpy oracle on
+a bounded row sample, on this host's cores).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "tri-attn fwd+bwd TFLOP/s & ms/call at N=768 bf16; MFMA util % vs peak"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+N, H, C = 768, 4, 32
+
+
+def flops_step(n=N, h=H, c=C):
+    return 14 * h * c * n**3
+
+
+def _log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_inputs(device, seed=2):
+    import torch
+
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    base = [torch.randn(1, N, N, H, C, generator=g).to(torch.bfloat16).to(device) for _ in range(3)]
+    q, k, v = (b.transpose(1, 2).requires_grad_(True) for b in base)
+    bias = torch.randn(1, 1, H, N, N, generator=g).to(torch.bfloat16).to(device).requires_grad_(True)
+    # upstream gradient in the output's (ending-node) layout
+    dout = torch.randn(1, N, N, H, C, generator=g).to(torch.bfloat16).to(device).transpose(1, 2)
+    return q, k, v, bias, dout
+
+
+def step(q, k, v, bias, dout):
+    import torch
+
+    from oops_amd import triangle_attention
+
+    out = triangle_attention(q, k, v, None, bias)
+    return torch.autograd.grad(out, (q, k, v, bias), dout)
+
+
+def time_events(fn, iters, warmup, stream):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(iters):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        fn()
+        b.record(stream)
+        b.synchronize()
+        times.append(a.elapsed_time(b))
+    return statistics.median(times)
+
+
+def kernel_times(q, k, v, bias, dout, iters=20):
+    """Median ms of each kernel, each launched alone on the current stream (HIP events)."""
+
+    import torch
+
+    from oops_amd import _lib
+    from oops_amd.attention import _core
+
+    stream = torch.cuda.current_stream()
+    out = triangle_attention_out = None
+    from oops_amd import triangle_attention
+
+    with torch.no_grad():
+        out = triangle_attention(q, k, v, None, bias)
+    # rebuild the op-level arguments exactly as the front-end does
+    qd, kd, vd, bd = (t.detach() for t in (q, k, v, bias))
+    table = []
+    for _ in range(1):
+        table += _core.table_row(
+            groups=N, len_q=N, len_k=N,
+            q=(0, qd.stride(1), qd.stride(3), qd.stride(2)),
+            k=(0, kd.stride(1), kd.stride(3), kd.stride(2)),
+            v=(0, vd.stride(1), vd.stride(3), vd.stride(2)),
+            bias=(0, 0, bd.stride(2), bd.stride(3)), dbias=(0, 0, N * N, N), bias_mode=_lib.BIAS_SHARED,
+            lse_off=0,
+        )  # fmt: skip
+    scale = C**-0.5
+    lse_numel = N * H * N
+    fwd = lambda: _core.attention_forward(qd, kd, vd, None, bd, table, H, scale, lse_numel, True)
+    o, o_lo, lse = fwd()
+    res = {"fwd": time_events(fwd, iters, 3, stream)}
+    for name, ph in (("delta", _lib.PHASE_DELTA), ("dq", _lib.PHASE_DQ), ("dkv", _lib.PHASE_DKV),
+                     ("dbias", _lib.PHASE_DBIAS)):  # fmt: skip
+
+        def bwd(ph=ph):
+            with _core.profile_phases(ph):
+                _core.attention_backward(dout, qd, kd, vd, None, bd, o, o_lo, lse, table, H, scale, bd.numel(),
+                                         [True, True, True, True])  # fmt: skip
+
+        res[name] = time_events(bwd, iters, 3, stream)
+    # the isolated backward call also allocates outputs/workspace; measure that overhead with no kernels
+    def empty_bwd():
+        with _core.profile_phases(0x10):
+            _core.attention_backward(dout, qd, kd, vd, None, bd, o, o_lo, lse, table, H, scale, bd.numel(),
+                                     [True, True, True, True])  # fmt: skip
+
+    overhead = time_events(empty_bwd, iters, 3, stream)
+    for name in ("delta", "dq", "dkv", "dbias"):
+        res[name] = max(res[name] - overhead, 1e-6)
+    return res
+
+
+# per-kernel MFMA work in units of 2*H*c*N^3 (one N x N x c GEMM per row and head)
+KERNEL_GEMMS = {"fwd": 2, "dq": 3, "dkv": 4, "dbias": 2, "delta": 0}
+
+
+def cpu_baseline(budget_s=15.0):
+    """The numpy oracle (float32) on a bounded sample of rows of the same workload."""
+
+    import numpy as np
+
+    from oracle import attention as ora
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+    except Exception:  # pragma: no cover
+        threads = 1
+    rng = np.random.default_rng(2)
+    bias = rng.standard_normal((1, 1, H, N, N), dtype=np.float32)
+    rows_done, elapsed, chunk = 0, 0.0, 4
+    while elapsed < budget_s and rows_done < N:
+        q, k, v, do = (rng.standard_normal((1, chunk, N, H, C), dtype=np.float32) for _ in range(4))
+        t0 = time.perf_counter()
+        ora.triangle_attention_forward(q, k, v, None, bias, dtype=np.float32)
+        ora.triangle_attention_backward(q, k, v, do, None, bias, dtype=np.float32)
+        elapsed += time.perf_counter() - t0
+        rows_done += chunk
+    flops = 14 * H * C * N * N * rows_done
+    return {
+        "value": flops / elapsed / 1e12,
+        "unit": "TFLOP/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"numpy float32 oracle fwd+bwd on {rows_done} of {N} rows (N={N}, H={H}, c={C}, shared bias), "
+        f"{elapsed:.1f} s; host os.cpu_count()={os.cpu_count()}",
+        "ms_per_call_extrapolated": elapsed / rows_done * N * 1e3,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(
+            "bench.py measures one GPU only: this build has no multi-GPU path "
+            "(rows shard independently; see DESIGN.md). Run with --gpus 1.",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+
+    import torch
+
+    from oops_amd import _lib
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    q, k, v, bias, dout = make_inputs(dev)
+    torch.cuda.synchronize()
+    _log("bench: warmup")
+    for _ in range(args.warmup):
+        step(q, k, v, bias, dout)
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps):
+        step(q, k, v, bias, dout)
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = start.elapsed_time(end) / args.steps
+    peak_mem = torch.cuda.max_memory_allocated()
+    _log(f"bench: {ms:.3f} ms/step (wall {wall / args.steps * 1e3:.3f} ms)")
+
+    kt = kernel_times(q, k, v, bias, dout)
+    _log("bench: kernel ms " + json.dumps({k_: round(v_, 4) for k_, v_ in kt.items()}))
+    dominant = max(kt, key=kt.get)
+    unit_flops = 2 * H * C * N**3
+    ach = KERNEL_GEMMS[dominant] * unit_flops / (kt[dominant] * 1e-3) / 1e12
+    value = flops_step() / (ms * 1e-3) / 1e12
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded randn, BASELINE config 3)",
+        "config": {
+            "workload": "triangle attention ending node fwd+bwd (config 3)",
+            "N": N,
+            "heads": H,
+            "head_size": C,
+            "bias": "shared [1,1,4,768,768] bf16",
+            "mask": None,
+            "parallelism": "single GPU",
+        },
+        "mfma_util_pct": round(100 * value / PEAK_BF16_TFLOPS, 2),
+        "peak_mem_bytes": int(peak_mem),
+        "kernel_ms": {k_: round(v_, 4) for k_, v_ in kt.items()},
+        "roofline": {
+            "kernel": dominant,
+            "bound": "mfma",
+            "achieved": round(ach, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(ach / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu:
+        _log("bench: cpu baseline")
+        line["cpu_baseline"] = cpu_baseline(args.cpu_budget)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,139 @@
+/*
+ * oops_amd — MI355X (gfx950) pair-biased attention, C ABI.
+ *
+ * One kernel family serves every layout of the reference's attention path:
+ * dense triangle attention in the starting-node (row) and ending-node (column,
+ * swapped pair axes) orientation, ragged NestedTensor batches, and MSA-row
+ * pair-bias attention.  The caller describes each independent "sample" (one
+ * dense batch element, one nested complex, one MSA prefix element) with one row
+ * of an int64 geometry table; every attention problem of a sample is indexed by
+ * (group g, head h) and attends Lq queries over Lk keys:
+ *
+ *   O[g,h,i,:] = sum_j softmax_j(scale * Q[g,h,i,:].K[g,h,j,:] + bias[g,h,i,j]
+ *                                  masked where keep[g,i,j] == 0) * V[g,h,j,:]
+ *
+ * Element (g, h, i, d) of a Q/K/V/O/dO operand lives at
+ *     base + off + g*s_g + h*s_h + i*s_i + d          (elements, d contiguous)
+ * so the ending-node orientation is only a different (s_g, s_i) pair and is
+ * never materialised transposed.  Strides of 0 broadcast.
+ *
+ * Reference interfaces replaced (paths relative to the OOps source tree):
+ *   oops_attn_forward   <- _run_forward / _launch_forward + Triton _forward
+ *                          (oops/attention/triangle/triton/generic.py:173-317,
+ *                           oops/attention/triangle/triton/kernel.py:266) and
+ *                          run_attention_forward
+ *                          (oops/attention/flash/triton/generic.py:233)
+ *   oops_attn_backward  <- _run_backward + Triton _backward_preprocess,
+ *                          _backward_query, _backward_key_value,
+ *                          _backward_shared_bias and the partials.sum(0)
+ *                          (oops/attention/triangle/triton/generic.py:320-536,
+ *                           oops/attention/triangle/triton/kernel.py:375-873) and
+ *                          run_attention_backward
+ *                          (oops/attention/flash/triton/generic.py:324-658)
+ *   oops_attn_backward_workspace_bytes <- the partial-slab sizing of
+ *                          SharedBiasSplit (oops/attention/triangle/triton/schedule.py:124-141)
+ *   the geometry table  <- the int64 sample table of
+ *                          triangle_attention_sample_table / uniform_sample_table
+ *                          (oops/attention/triangle/nested.py:60, triton/ops.py:44)
+ *
+ * Every entry point is stateless and re-entrant; work is enqueued on the HIP
+ * stream passed in (NULL = legacy default stream) and nothing synchronises the
+ * host, so calls are safe under stream capture.  Return value 0 = success,
+ * otherwise an OOPS_E* code; oops_last_error() gives a thread-local message.
+ */
+#ifndef OOPS_AMD_H
+#define OOPS_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types */
+#define OOPS_F32 0
+#define OOPS_BF16 1
+#define OOPS_F16 2
+
+/* status codes */
+#define OOPS_OK 0
+#define OOPS_EINVAL 1     /* malformed geometry or unsupported combination */
+#define OOPS_ELAUNCH 2    /* a HIP launch failed */
+#define OOPS_EWORKSPACE 3 /* workspace missing or too small */
+
+/* bias modes (table column OOPS_T_BIAS_MODE) */
+#define OOPS_BIAS_NONE 0
+#define OOPS_BIAS_FULL 1   /* one bias matrix per group: dBias = dS        */
+#define OOPS_BIAS_SHARED 2 /* one bias matrix for all groups: dBias = sum_g dS */
+
+/* backward phases (oops_attn_geometry.phases); 0 runs all of them */
+#define OOPS_PHASE_DELTA 1 /* delta = rowsum(O * dO)                 */
+#define OOPS_PHASE_DQ 2    /* dQ and per-group dBias               */
+#define OOPS_PHASE_DKV 4   /* dK and dV                            */
+#define OOPS_PHASE_DBIAS 8 /* shared dBias (partials + reduction)  */
+
+/* geometry table: OOPS_TABLE_WIDTH int64 columns per sample */
+enum oops_table_column {
+  OOPS_T_GROUPS = 0, /* G */
+  OOPS_T_LEN_Q,      /* Lq */
+  OOPS_T_LEN_K,      /* Lk */
+  OOPS_T_Q_OFF, OOPS_T_Q_SG, OOPS_T_Q_SH, OOPS_T_Q_SI,     /* also dQ */
+  OOPS_T_K_OFF, OOPS_T_K_SG, OOPS_T_K_SH, OOPS_T_K_SI,     /* also dK */
+  OOPS_T_V_OFF, OOPS_T_V_SG, OOPS_T_V_SH, OOPS_T_V_SI,     /* also dV */
+  OOPS_T_O_OFF, OOPS_T_O_SG, OOPS_T_O_SH, OOPS_T_O_SI,
+  OOPS_T_DO_OFF, OOPS_T_DO_SG, OOPS_T_DO_SH, OOPS_T_DO_SI,
+  OOPS_T_B_OFF, OOPS_T_B_SG, OOPS_T_B_SH, OOPS_T_B_SI,     /* bias, key stride 1 */
+  OOPS_T_M_OFF, OOPS_T_M_SG, OOPS_T_M_SI,                  /* u8 keep-mask, key stride 1; -1 = none */
+  OOPS_T_L_OFF,                                            /* f32 LSE/delta, [G][H][Lq] */
+  OOPS_T_DB_OFF, OOPS_T_DB_SG, OOPS_T_DB_SH, OOPS_T_DB_SI, /* f32 dBias output */
+  OOPS_T_BIAS_MODE,                                        /* OOPS_BIAS_* */
+  OOPS_T_RESERVED0, OOPS_T_RESERVED1, OOPS_T_RESERVED2, OOPS_T_RESERVED3,
+  OOPS_TABLE_WIDTH = 40
+};
+
+typedef struct oops_attn_geometry {
+  int32_t dtype;       /* OOPS_F32 / OOPS_BF16 / OOPS_F16 for Q, K, V, O, dO */
+  int32_t bias_dtype;  /* dtype of the bias: the Q dtype or OOPS_F32 */
+  int32_t num_heads;   /* H */
+  int32_t head_size;   /* D, 1..256 */
+  int32_t num_samples; /* rows of the table */
+  int32_t has_bias;    /* 0/1 */
+  int32_t has_mask;    /* 0/1 */
+  int32_t vec_ok;      /* 1 when every row of Q/K/V/O/dO/bias starts 16-byte aligned */
+  float scale;         /* multiplies Q.K before the bias is added */
+  int32_t phases;      /* backward kernels to run: OR of OOPS_PHASE_*, 0 = all */
+  const int64_t* table_host;   /* host copy, used for grid sizing */
+  const int64_t* table_device; /* device copy, read by the kernels */
+} oops_attn_geometry;
+
+/* Forward: writes O (dtype) and LSE (f32, log2 units, [G][H][Lq] per sample).
+ * out_lo (optional, NULL to skip; 16-bit dtypes) receives O - round(O) with
+ * O's layout, which the backward uses for an exact delta = rowsum(O * dO),
+ * as the reference does with its saved fp32 output (triton/ops.py:369-377). */
+int oops_attn_forward(const oops_attn_geometry* geo, const void* q, const void* k, const void* v,
+                      const uint8_t* mask, const void* bias, void* out, void* out_lo, float* lse,
+                      void* stream);
+
+/* Bytes of device workspace oops_attn_backward needs for this geometry. */
+size_t oops_attn_backward_workspace_bytes(const oops_attn_geometry* geo);
+
+/* Backward: dq/dk/dv in dtype with the Q/K/V strides of the table; dbias f32
+ * at the table's dBias offsets (may be NULL when no bias gradient is wanted;
+ * any of dq/dk/dv may be NULL likewise).  workspace must be device memory of
+ * at least oops_attn_backward_workspace_bytes(geo) bytes, 256-byte aligned. */
+int oops_attn_backward(const oops_attn_geometry* geo, const void* q, const void* k, const void* v,
+                       const uint8_t* mask, const void* bias, const void* out, const void* out_lo,
+                       const float* lse, const void* dout, void* dq, void* dk, void* dv, float* dbias, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/* Thread-local description of the last failure (empty string if none). */
+const char* oops_last_error(void);
+
+/* Library ABI version; bumped on any change to the table or geometry layout. */
+int oops_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* OOPS_AMD_H */

@@ -1,0 +1,10 @@
+"""oops_amd: MI355X-native pair-biased triangle attention with the OOps operator API.
+
+``from oops_amd import triangle_attention, pair_bias_attention, OOpsUnsupportedError``
+is the drop-in for ``from oops import ...`` on the attention path.
+"""
+
+from ._errors import OOpsUnsupportedError
+from .attention import triangle_attention
+
+__all__ = ["OOpsUnsupportedError", "triangle_attention"]

@@ -1,0 +1,109 @@
+"""ctypes binding of the C-ABI library ``oops_amd/lib/liboops_amd.so``.
+
+The library is the product's compute path; nothing here falls back to another
+implementation.  If it is missing or fails to load, every operator raises.
+The structure and constants mirror ``include/oops_amd.h``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "liboops_amd.so"
+
+F32, BF16, F16 = 0, 1, 2
+BIAS_NONE, BIAS_FULL, BIAS_SHARED = 0, 1, 2
+PHASE_DELTA, PHASE_DQ, PHASE_DKV, PHASE_DBIAS = 1, 2, 4, 8
+TABLE_WIDTH = 40
+ABI_VERSION = 1
+
+# geometry table columns (enum oops_table_column)
+(
+    T_GROUPS, T_LEN_Q, T_LEN_K,
+    T_Q_OFF, T_Q_SG, T_Q_SH, T_Q_SI,
+    T_K_OFF, T_K_SG, T_K_SH, T_K_SI,
+    T_V_OFF, T_V_SG, T_V_SH, T_V_SI,
+    T_O_OFF, T_O_SG, T_O_SH, T_O_SI,
+    T_DO_OFF, T_DO_SG, T_DO_SH, T_DO_SI,
+    T_B_OFF, T_B_SG, T_B_SH, T_B_SI,
+    T_M_OFF, T_M_SG, T_M_SI,
+    T_L_OFF,
+    T_DB_OFF, T_DB_SG, T_DB_SH, T_DB_SI,
+    T_BIAS_MODE,
+) = range(36)  # fmt: skip
+
+EXPORTED_SYMBOLS = (
+    "oops_attn_forward",
+    "oops_attn_backward_workspace_bytes",
+    "oops_attn_backward",
+    "oops_last_error",
+    "oops_abi_version",
+)
+
+
+class Geometry(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("bias_dtype", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32),
+        ("head_size", ctypes.c_int32),
+        ("num_samples", ctypes.c_int32),
+        ("has_bias", ctypes.c_int32),
+        ("has_mask", ctypes.c_int32),
+        ("vec_ok", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("phases", ctypes.c_int32),
+        ("table_host", ctypes.c_void_p),
+        ("table_device", ctypes.c_void_p),
+    ]
+
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library; raises ``RuntimeError`` if it is absent."""
+
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"oops_amd native library not built: {LIB_PATH} is missing "
+                "(run `python -m oops_amd.csrc.build` or __graft_entry__.build())"
+            )
+        # torch first: its HIP runtime then serves the library as well
+        import torch  # noqa: F401
+
+        lib = ctypes.CDLL(os.fspath(LIB_PATH))
+        vp, sz, i32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+        geo = ctypes.POINTER(Geometry)
+        lib.oops_attn_forward.argtypes = [geo, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        lib.oops_attn_forward.restype = i32
+        lib.oops_attn_backward_workspace_bytes.argtypes = [geo]
+        lib.oops_attn_backward_workspace_bytes.restype = sz
+        lib.oops_attn_backward.argtypes = [geo, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
+        lib.oops_attn_backward.restype = i32
+        lib.oops_last_error.argtypes = []
+        lib.oops_last_error.restype = ctypes.c_char_p
+        lib.oops_abi_version.argtypes = []
+        lib.oops_abi_version.restype = i32
+        if lib.oops_abi_version() != ABI_VERSION:
+            raise RuntimeError(
+                f"oops_amd native library ABI {lib.oops_abi_version()} does not match the Python side ({ABI_VERSION})"
+            )
+        _lib = lib
+        return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        message = load().oops_last_error().decode(errors="replace")
+        raise RuntimeError(f"oops_amd {what} failed (code {rc}): {message}")

@@ -1,0 +1,342 @@
+"""Custom ops and autograd around the C-ABI attention library.
+
+Every front-end (dense triangle attention, nested triangle attention, MSA-row
+pair-bias attention) lowers its call to the same two operators:
+
+* ``oops_amd::attention_forward(q, k, v, mask, bias, table, ...) -> (out, lse)``
+* ``oops_amd::attention_backward(dout, q, k, v, mask, bias, out, lse, table, ...)``
+
+``table`` is the flattened int64 geometry table of ``include/oops_amd.h``
+(``TABLE_WIDTH`` ints per sample), built from shapes and strides only, so the
+ops are opaque to ``torch.compile`` and traceable under ``FakeTensorMode``.
+The output, dQ, dK and dV are allocated with the strides of Q, K and V, so
+their table columns are those of Q/K/V; dBias is a float32 buffer laid out as
+the contiguous bias values.
+
+This plays the role of the reference's ``triton_triangle_attention`` /
+``_TriangleAttention`` and the ``ooperators::_triangle_attention_*`` custom ops
+(oops/attention/triangle/triton/ops.py:102-423).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from collections import OrderedDict
+from typing import List, Optional, Sequence, Tuple
+
+import torch
+from torch import Tensor
+
+from .. import _lib
+
+_DTYPE_CODE = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
+SUPPORTED_DTYPES = tuple(_DTYPE_CODE)
+MAX_HEAD_SIZE = 256
+
+# Backward kernels to run (OR of _lib.PHASE_*; 0 = all).  Only for profiling
+# single kernels; see ``profile_phases``.
+_PHASES = 0
+
+
+class profile_phases:
+    """Context manager restricting backward calls to a subset of kernels (profiling only)."""
+
+    def __init__(self, phases: int):
+        self.phases = phases
+
+    def __enter__(self):
+        global _PHASES
+        self.saved, _PHASES = _PHASES, self.phases
+        return self
+
+    def __exit__(self, *exc):
+        global _PHASES
+        _PHASES = self.saved
+        return False
+
+
+# ----------------------------------------------------------------- tables
+
+_TABLE_CACHE: "OrderedDict[tuple, tuple[Tensor, Tensor]]" = OrderedDict()
+_TABLE_CACHE_SIZE = 512
+
+
+def device_table(table: Sequence[int], device: torch.device) -> tuple[Tensor, Tensor]:
+    """(pinned host copy, device copy) of a geometry table, cached by value.
+
+    The device copy is filled from pinned memory with an async copy, which is
+    legal under CUDA-graph capture; cached entries are reused unchanged, so a
+    captured graph keeps reading valid memory.
+    """
+
+    key = (device.index, tuple(int(x) for x in table))
+    hit = _TABLE_CACHE.get(key)
+    if hit is not None:
+        _TABLE_CACHE.move_to_end(key)
+        return hit
+    host = torch.tensor(key[1], dtype=torch.int64).pin_memory()
+    dev = torch.empty(host.shape, dtype=torch.int64, device=device)
+    dev.copy_(host, non_blocking=True)
+    _TABLE_CACHE[key] = (host, dev)
+    while len(_TABLE_CACHE) > _TABLE_CACHE_SIZE:
+        _TABLE_CACHE.popitem(last=False)
+    return host, dev
+
+
+def _vec_ok(table: Sequence[int], tensors: Sequence[Optional[Tensor]], bias: Optional[Tensor]) -> bool:
+    """True when every row of every operand starts on a 16-byte boundary."""
+
+    for t in (*tensors, bias):
+        if t is not None and t.data_ptr() % 16:
+            return False
+    width = _lib.TABLE_WIDTH
+    q = tensors[0]
+    ce = 16 // q.element_size()
+    cols = (
+        _lib.T_Q_OFF, _lib.T_Q_SG, _lib.T_Q_SH, _lib.T_Q_SI,
+        _lib.T_K_OFF, _lib.T_K_SG, _lib.T_K_SH, _lib.T_K_SI,
+        _lib.T_V_OFF, _lib.T_V_SG, _lib.T_V_SH, _lib.T_V_SI,
+    )  # fmt: skip
+    bce = 16 // bias.element_size() if bias is not None else 1
+    bcols = (_lib.T_B_OFF, _lib.T_B_SG, _lib.T_B_SH, _lib.T_B_SI)
+    for s in range(len(table) // width):
+        row = table[s * width : (s + 1) * width]
+        if any(int(row[c]) % ce for c in cols):
+            return False
+        if bias is not None and int(row[_lib.T_B_OFF]) >= 0 and any(int(row[c]) % bce for c in bcols):
+            return False
+    return True
+
+
+def _geometry(q: Tensor, bias: Optional[Tensor], mask: Optional[Tensor], table: Sequence[int],
+              num_heads: int, scale: float, vec_ok: bool) -> tuple[_lib.Geometry, tuple]:
+    host, dev = device_table(table, q.device)
+    geo = _lib.Geometry()
+    geo.dtype = _DTYPE_CODE[q.dtype]
+    geo.bias_dtype = _DTYPE_CODE[bias.dtype] if bias is not None else geo.dtype
+    geo.num_heads = num_heads
+    geo.head_size = q.shape[-1]
+    geo.num_samples = len(table) // _lib.TABLE_WIDTH
+    geo.has_bias = int(bias is not None)
+    geo.has_mask = int(mask is not None)
+    geo.vec_ok = int(vec_ok)
+    geo.scale = float(scale)
+    geo.phases = _PHASES
+    geo.table_host = host.data_ptr()
+    geo.table_device = dev.data_ptr()
+    return geo, (host, dev)
+
+
+def _ptr(t: Optional[Tensor]) -> Optional[int]:
+    return None if t is None or t.numel() == 0 else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+# ----------------------------------------------------------------- ops
+
+
+@torch.library.custom_op("oops_amd::attention_forward", mutates_args=(), device_types="cuda")
+def attention_forward(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    mask: Optional[Tensor],
+    bias: Optional[Tensor],
+    table: List[int],
+    num_heads: int,
+    scale: float,
+    lse_numel: int,
+    save_residual: bool,
+) -> Tuple[Tensor, Tensor, Tensor]:
+    lib = _lib.load()
+    out = torch.empty_strided(q.size(), q.stride(), dtype=q.dtype, device=q.device)
+    out_lo = _residual_like(out, save_residual)
+    lse = torch.empty(lse_numel, dtype=torch.float32, device=q.device)
+    vec = _vec_ok(table, (q, k, v, out), bias)
+    geo, keep = _geometry(q, bias, mask, table, num_heads, scale, vec)
+    with torch.cuda.device(q.device):
+        rc = lib.oops_attn_forward(
+            ctypes.byref(geo), _ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(bias), _ptr(out), _ptr(out_lo),
+            _ptr(lse), _stream(q.device),
+        )
+    _lib.check(rc, "attention forward")
+    del keep
+    return out, out_lo, lse
+
+
+def _residual_like(out: Tensor, save: bool) -> Tensor:
+    """Buffer for out - round(out) (16-bit outputs of a differentiable call), else empty."""
+
+    if save and out.dtype != torch.float32:
+        return torch.empty_strided(out.size(), out.stride(), dtype=out.dtype, device=out.device)
+    return out.new_empty(0)
+
+
+@attention_forward.register_fake
+def _(q, k, v, mask, bias, table, num_heads, scale, lse_numel, save_residual):
+    out = torch.empty_strided(q.size(), q.stride(), dtype=q.dtype, device=q.device)
+    return out, _residual_like(out, save_residual), q.new_empty(lse_numel, dtype=torch.float32)
+
+
+@torch.library.custom_op("oops_amd::attention_backward", mutates_args=(), device_types="cuda")
+def attention_backward(
+    dout: Tensor,
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    mask: Optional[Tensor],
+    bias: Optional[Tensor],
+    out: Tensor,
+    out_lo: Tensor,
+    lse: Tensor,
+    table: List[int],
+    num_heads: int,
+    scale: float,
+    dbias_numel: int,
+    needs: List[bool],
+) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    lib = _lib.load()
+    dout = dout.resolve_neg().resolve_conj()
+    if dout.dtype != out.dtype:
+        dout = dout.to(out.dtype)
+    if dout.stride() != out.stride():
+        # the kernels read dO with the output's (= query's) layout
+        dout = torch.empty_strided(out.size(), out.stride(), dtype=out.dtype, device=out.device).copy_(dout)
+    need_q, need_k, need_v, need_b = needs
+
+    def like(t: Tensor, need: bool) -> Tensor:
+        if not need:
+            return t.new_empty(0)
+        return torch.empty_strided(t.size(), t.stride(), dtype=t.dtype, device=t.device)
+
+    dq, dk, dv = like(q, need_q), like(k, need_k), like(v, need_v)
+    dbias = (
+        torch.empty(dbias_numel, dtype=torch.float32, device=q.device)
+        if need_b and bias is not None
+        else q.new_empty(0, dtype=torch.float32)
+    )
+    vec = _vec_ok(table, (q, k, v, out, dout), bias)
+    geo, keep = _geometry(q, bias, mask, table, num_heads, scale, vec)
+    ws_bytes = lib.oops_attn_backward_workspace_bytes(ctypes.byref(geo))
+    if ws_bytes == 0:
+        _lib.check(1, "attention backward workspace sizing")
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    with torch.cuda.device(q.device):
+        rc = lib.oops_attn_backward(
+            ctypes.byref(geo), _ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(bias), _ptr(out), _ptr(out_lo),
+            _ptr(lse), _ptr(dout), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dbias), _ptr(workspace), ws_bytes,
+            _stream(q.device),
+        )
+    _lib.check(rc, "attention backward")
+    del keep
+    return dq, dk, dv, dbias
+
+
+@attention_backward.register_fake
+def _(dout, q, k, v, mask, bias, out, out_lo, lse, table, num_heads, scale, dbias_numel, needs):
+    def like(t, need):
+        return torch.empty_strided(t.size(), t.stride(), dtype=t.dtype, device=t.device) if need else t.new_empty(0)
+
+    need_q, need_k, need_v, need_b = needs
+    dbias = q.new_empty(dbias_numel if (need_b and bias is not None) else 0, dtype=torch.float32)
+    return like(q, need_q), like(k, need_k), like(v, need_v), dbias
+
+
+def _setup_context(ctx, inputs, output):
+    q, k, v, mask, bias, table, num_heads, scale, lse_numel, save_residual = inputs
+    out, out_lo, lse = output
+    ctx.save_for_backward(q, k, v, mask, bias, out, out_lo, lse)
+    ctx.table = table
+    ctx.num_heads = num_heads
+    ctx.scale = scale
+    ctx.bias_shape = None if bias is None else bias.shape
+    ctx.bias_dtype = None if bias is None else bias.dtype
+    ctx.mark_non_differentiable(out_lo, lse)
+
+
+def _backward(ctx, dout, dout_lo, dlse):
+    q, k, v, mask, bias, out, out_lo, lse = ctx.saved_tensors
+    need_q, need_k, need_v, _, need_b = ctx.needs_input_grad[:5]
+    need_b = bool(need_b and bias is not None)
+    if not (need_q or need_k or need_v or need_b):
+        return (None,) * 10
+    dbias_numel = 0 if bias is None else bias.numel()
+    dq, dk, dv, dbias = attention_backward(
+        dout, q, k, v, mask, bias, out, out_lo, lse, ctx.table, ctx.num_heads, ctx.scale, dbias_numel,
+        [bool(need_q), bool(need_k), bool(need_v), need_b],
+    )
+    grad_bias = dbias.view(ctx.bias_shape).to(ctx.bias_dtype) if need_b else None
+    return (
+        dq if need_q else None,
+        dk if need_k else None,
+        dv if need_v else None,
+        None,
+        grad_bias,
+        None,
+        None,
+        None,
+        None,
+        None,
+    )
+
+
+attention_forward.register_autograd(_backward, setup_context=_setup_context)
+
+
+# ----------------------------------------------------------------- table rows
+
+
+def table_row(
+    *,
+    groups: int,
+    len_q: int,
+    len_k: int,
+    q: Sequence[int],
+    k: Sequence[int],
+    v: Sequence[int],
+    bias: Optional[Sequence[int]] = None,
+    dbias: Optional[Sequence[int]] = None,
+    bias_mode: int = _lib.BIAS_NONE,
+    mask: Optional[Sequence[int]] = None,
+    lse_off: int = 0,
+) -> list:
+    """One geometry-table row.  q/k/v/bias/dbias are (off, s_g, s_h, s_i); mask is (off, s_g, s_i).
+
+    The output and dO columns repeat the query's, matching how the ops
+    allocate the output.
+    """
+
+    row = [0] * _lib.TABLE_WIDTH
+    row[_lib.T_GROUPS], row[_lib.T_LEN_Q], row[_lib.T_LEN_K] = groups, len_q, len_k
+    row[_lib.T_Q_OFF : _lib.T_Q_OFF + 4] = list(q)
+    row[_lib.T_K_OFF : _lib.T_K_OFF + 4] = list(k)
+    row[_lib.T_V_OFF : _lib.T_V_OFF + 4] = list(v)
+    row[_lib.T_O_OFF : _lib.T_O_OFF + 4] = list(q)
+    row[_lib.T_DO_OFF : _lib.T_DO_OFF + 4] = list(q)
+    row[_lib.T_B_OFF : _lib.T_B_OFF + 4] = list(bias) if bias is not None else [-1, 0, 0, 0]
+    row[_lib.T_M_OFF : _lib.T_M_OFF + 3] = list(mask) if mask is not None else [-1, 0, 0]
+    row[_lib.T_L_OFF] = lse_off
+    row[_lib.T_DB_OFF : _lib.T_DB_OFF + 4] = list(dbias) if dbias is not None else [0, 0, 0, 0]
+    row[_lib.T_BIAS_MODE] = bias_mode if bias is not None else _lib.BIAS_NONE
+    return row
+
+
+def kernel_operand(tensor: Optional[Tensor]) -> Optional[Tensor]:
+    """Resolve lazy neg/conj view bits; raw pointers cannot observe them."""
+
+    if tensor is None:
+        return None
+    return tensor.resolve_neg().resolve_conj()
+
+
+def attend(q, k, v, mask, bias, table, num_heads, scale, lse_numel) -> Tensor:
+    """Run the forward op (autograd-aware) and return the output tensor."""
+
+    save = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (q, k, v, bias)
+    )
+    out, _, _ = attention_forward(q, k, v, mask, bias, table, num_heads, scale, lse_numel, save)
+    return out

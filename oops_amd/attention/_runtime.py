@@ -1,0 +1,48 @@
+"""Small runtime guards shared by the front-ends.
+
+Restates the contract pieces of the reference's runtime helpers
+(oops/runtime/dispatch.py:529-636): forward-mode AD is rejected with
+``OOpsUnsupportedError``; operands must share one device.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch.autograd import forward_ad
+
+from .._errors import unsupported
+
+
+def is_nested(x) -> bool:
+    """Duck-typed DanLing ``NestedTensor`` test (packed ``.concat`` + ``.packed_like``)."""
+
+    return x is not None and not isinstance(x, torch.Tensor) and hasattr(x, "concat") and hasattr(x, "packed_like")
+
+
+def forward_mode_active(*tensors) -> bool:
+    if forward_ad._current_level < 0:
+        return False
+    try:
+        if torch._C._are_functorch_transforms_active():
+            return True
+    except AttributeError:  # pragma: no cover
+        pass
+    for t in tensors:
+        if isinstance(t, torch.Tensor) and forward_ad.unpack_dual(t).tangent is not None:
+            return True
+    return False
+
+
+def require_no_forward_mode(operator: str, *tensors) -> None:
+    if forward_mode_active(*tensors):
+        raise unsupported(
+            operator,
+            "does not support forward-mode AD",
+            hint="use reverse-mode autograd or the equivalent Torch operation for a Jacobian-vector product",
+        )
+
+
+def require_same_device(operator: str, *tensors) -> None:
+    devices = {t.device for t in tensors if isinstance(t, torch.Tensor)}
+    if len(devices) > 1:
+        raise ValueError(f"{operator} operands must share one device, got {sorted(map(str, devices))}")

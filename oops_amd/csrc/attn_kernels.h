@@ -1,0 +1,130 @@
+// Kernel argument blocks and the instantiated (dtype, bias dtype, padded
+// head size) configurations.
+#pragma once
+
+#include "attn_common.h"
+
+namespace oops {
+
+template <typename T, typename BT>
+struct FwdArgsT {
+  const T* q;
+  const T* k;
+  const T* v;
+  const BT* bias;
+  const uint8_t* mask;
+  T* out;
+  T* out_lo;  // optional: out - round(out), for an exact backward delta
+  float* lse;
+  const int64_t* table;
+  int64_t uniform_tiles;
+  int num_samples;
+  int num_heads;
+  int head_size;
+  int vec_ok;
+  float scale;
+};
+
+template <typename T, typename BT>
+struct BwdArgsT {
+  const T* q;
+  const T* k;
+  const T* v;
+  const T* out;
+  const T* out_lo;
+  const T* dout;
+  const BT* bias;
+  const uint8_t* mask;
+  const float* lse;
+  float* delta;
+  T* dq;
+  T* dk;
+  T* dv;
+  float* dbias;        // final dBias (f32)
+  float* dbias_part;   // [parts][dbias_extent] partial slabs (shared-bias mode)
+  const int64_t* table;
+  int64_t uniform_tiles;
+  int64_t dbias_extent;
+  int num_samples;
+  int num_heads;
+  int head_size;
+  int vec_ok;
+  int parts;
+  float scale;
+};
+
+}  // namespace oops
+
+// The kernels name their argument block FwdArgs / BwdArgs; each kernel
+// template defines them for its own (T, BT).
+#define FwdArgs FwdArgsT<T, BT>
+#define BwdArgs BwdArgsT<T, BT>
+
+#define OOPS_FOR_EACH_DP(X, T, BT) X(T, BT, 32) X(T, BT, 64) X(T, BT, 128) X(T, BT, 256)
+#define OOPS_FOR_EACH_CONFIG(X)           \
+  OOPS_FOR_EACH_DP(X, float, float)       \
+  OOPS_FOR_EACH_DP(X, __bf16, __bf16)     \
+  OOPS_FOR_EACH_DP(X, __bf16, float)      \
+  OOPS_FOR_EACH_DP(X, _Float16, _Float16) \
+  OOPS_FOR_EACH_DP(X, _Float16, float)
+
+#include <type_traits>
+
+namespace oops {
+
+template <typename T>
+struct Tag {
+  using type = T;
+};
+
+// Call f(Tag<T>, Tag<BT>, integral_constant<DP>) for the instantiated
+// configuration; returns false when the combination is not built.
+template <typename F>
+inline bool dispatch_config(int dtype, int bias_dtype, int dp, F&& f) {
+  auto by_dp = [&](auto t, auto bt) {
+    switch (dp) {
+      case 32: f(t, bt, std::integral_constant<int, 32>{}); return true;
+      case 64: f(t, bt, std::integral_constant<int, 64>{}); return true;
+      case 128: f(t, bt, std::integral_constant<int, 128>{}); return true;
+      case 256: f(t, bt, std::integral_constant<int, 256>{}); return true;
+    }
+    return false;
+  };
+  if (dtype == OOPS_F32) return bias_dtype == OOPS_F32 && by_dp(Tag<float>{}, Tag<float>{});
+  if (dtype == OOPS_BF16) {
+    if (bias_dtype == OOPS_BF16) return by_dp(Tag<__bf16>{}, Tag<__bf16>{});
+    if (bias_dtype == OOPS_F32) return by_dp(Tag<__bf16>{}, Tag<float>{});
+    return false;
+  }
+  if (dtype == OOPS_F16) {
+    if (bias_dtype == OOPS_F16) return by_dp(Tag<_Float16>{}, Tag<_Float16>{});
+    if (bias_dtype == OOPS_F32) return by_dp(Tag<_Float16>{}, Tag<float>{});
+    return false;
+  }
+  return false;
+}
+
+// Host-side launch plan derived from the geometry table.
+struct Plan {
+  int dp = 0;
+  int64_t fwd_tiles = 0, fwd_uniform = 0;        // 128-query blocks
+  int64_t delta_tiles = 0, delta_uniform = 0;    // 64-query blocks
+  int64_t dkv_tiles = 0, dkv_uniform = 0;        // 128-key blocks
+  int64_t sbias_tiles = 0, sbias_uniform = 0;    // shared dBias blocks (incl. parts)
+  int64_t sred_tiles = 0, sred_uniform = 0;      // shared dBias reduction blocks
+  int64_t lse_extent = 0;                        // floats
+  int64_t dbias_extent = 0;                      // floats
+  int parts = 1;
+  bool any_full = false, any_shared = false;
+};
+
+hipError_t launch_forward(const oops_attn_geometry& geo, const Plan& plan, const void* q, const void* k,
+                          const void* v, const uint8_t* mask, const void* bias, void* out, void* out_lo,
+                          float* lse, hipStream_t stream);
+
+hipError_t launch_backward(const oops_attn_geometry& geo, const Plan& plan, const void* q, const void* k,
+                           const void* v, const uint8_t* mask, const void* bias, const void* out,
+                           const void* out_lo, const float* lse, const void* dout, void* dq, void* dk, void* dv, float* dbias,
+                           float* delta, float* dbias_part, hipStream_t stream);
+
+}  // namespace oops

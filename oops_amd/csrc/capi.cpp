@@ -1,0 +1,203 @@
+// C entry points: validate the geometry table, derive the launch plan and
+// enqueue the kernels.  No device memory is allocated here; the backward
+// pass takes a caller-provided workspace.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "attn_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, long long a = 0, long long b = 0) {
+  char buf[512];
+  std::snprintf(buf, sizeof(buf), fmt, a, b);
+  g_last_error = buf;
+  return code;
+}
+
+constexpr int64_t kMaxGrid = (int64_t(1) << 31) - 1;
+constexpr int64_t kTargetSharedBiasBlocks = 2048;  // 8 workgroups per CU on 256 CUs
+constexpr int kMaxParts = 64;
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+int padded_head(int d) {
+  if (d <= 32) return 32;
+  if (d <= 64) return 64;
+  if (d <= 128) return 128;
+  return 256;
+}
+
+// Highest element index touched (+1) by an operand with the given strides.
+int64_t extent(int64_t off, int64_t G, int64_t sg, int64_t H, int64_t sh, int64_t L, int64_t si, int64_t inner) {
+  return off + (G - 1) * sg + (H - 1) * sh + (L - 1) * si + inner;
+}
+
+// Returns 0 and fills `plan`, or an error code.
+int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
+  using oops::Sample;
+  if (geo == nullptr) return fail(OOPS_EINVAL, "geometry is NULL");
+  if (geo->table_host == nullptr || geo->table_device == nullptr)
+    return fail(OOPS_EINVAL, "geometry table pointers must be set (host and device copies)");
+  if (geo->num_samples <= 0) return fail(OOPS_EINVAL, "num_samples must be positive, got %lld", geo->num_samples);
+  if (geo->num_heads <= 0) return fail(OOPS_EINVAL, "num_heads must be positive, got %lld", geo->num_heads);
+  if (geo->head_size <= 0 || geo->head_size > 256)
+    return fail(OOPS_EINVAL, "head_size must be in 1..256, got %lld", geo->head_size);
+  if (geo->dtype < OOPS_F32 || geo->dtype > OOPS_F16) return fail(OOPS_EINVAL, "unknown dtype %lld", geo->dtype);
+  if (geo->has_bias && geo->bias_dtype != geo->dtype && geo->bias_dtype != OOPS_F32)
+    return fail(OOPS_EINVAL, "bias dtype must equal the q/k/v dtype or be float32");
+  plan = oops::Plan{};
+  plan.dp = padded_head(geo->head_size);
+  const int64_t H = geo->num_heads;
+  const Sample* tab = reinterpret_cast<const Sample*>(geo->table_host);
+  int64_t c_fwd = -1, c_delta = -1, c_dkv = -1, c_sb = -1;
+  bool u_fwd = true, u_delta = true, u_dkv = true, u_sb = true;
+  int64_t min_shared_groups = INT64_MAX, sbias_base = 0;
+  auto track = [](int64_t c, int64_t& first, bool& uniform) {
+    if (first < 0) first = c;
+    else if (first != c) uniform = false;
+  };
+  for (int s = 0; s < geo->num_samples; ++s) {
+    const Sample& S = tab[s];
+    if (S.G <= 0 || S.Lq <= 0 || S.Lk <= 0)
+      return fail(OOPS_EINVAL, "sample %lld has an empty axis (G, Lq or Lk <= 0)", s);
+    if (S.Lq > INT32_MAX || S.Lk > INT32_MAX) return fail(OOPS_EINVAL, "sample %lld is too long", s);
+    const int64_t q_off_min = std::min({S.q_off, S.k_off, S.v_off, S.o_off, S.do_off});
+    if (q_off_min < 0 || S.l_off < 0) return fail(OOPS_EINVAL, "sample %lld has a negative offset", s);
+    if (S.q_sg < 0 || S.q_sh < 0 || S.q_si < 0 || S.k_sg < 0 || S.k_sh < 0 || S.k_si < 0 || S.v_sg < 0 ||
+        S.v_sh < 0 || S.v_si < 0 || S.o_sg < 0 || S.o_sh < 0 || S.o_si < 0 || S.do_sg < 0 || S.do_sh < 0 ||
+        S.do_si < 0)
+      return fail(OOPS_EINVAL, "sample %lld has a negative stride", s);
+    if (S.bias_mode < OOPS_BIAS_NONE || S.bias_mode > OOPS_BIAS_SHARED)
+      return fail(OOPS_EINVAL, "sample %lld has unknown bias mode %lld", s, S.bias_mode);
+    if (geo->has_bias && S.b_off >= 0 && S.bias_mode == OOPS_BIAS_SHARED && S.b_sg != 0)
+      return fail(OOPS_EINVAL, "sample %lld: a shared bias must have group stride 0", s);
+    const int64_t c1 = S.G * H * cdiv(S.Lq, 128);
+    const int64_t c2 = S.G * H * cdiv(S.Lq, 64);
+    const int64_t c3 = S.G * H * cdiv(S.Lk, 128);
+    const int64_t cs = S.bias_mode == OOPS_BIAS_SHARED ? H * cdiv(S.Lq, 128) * cdiv(S.Lk, 32) : 0;
+    plan.fwd_tiles += c1;
+    plan.delta_tiles += c2;
+    plan.dkv_tiles += c3;
+    sbias_base += cs;
+    track(c1, c_fwd, u_fwd);
+    track(c2, c_delta, u_delta);
+    track(c3, c_dkv, u_dkv);
+    track(cs, c_sb, u_sb);
+    plan.lse_extent = std::max(plan.lse_extent, S.l_off + S.G * H * S.Lq);
+    if (geo->has_bias && S.b_off >= 0) {
+      if (S.bias_mode == OOPS_BIAS_FULL) plan.any_full = true;
+      if (S.bias_mode == OOPS_BIAS_SHARED) {
+        plan.any_shared = true;
+        min_shared_groups = std::min(min_shared_groups, S.G);
+      }
+      if (S.bias_mode != OOPS_BIAS_NONE) {
+        const int64_t gspan = S.bias_mode == OOPS_BIAS_SHARED ? 1 : S.G;
+        plan.dbias_extent =
+            std::max(plan.dbias_extent, extent(S.db_off, gspan, S.db_sg, H, S.db_sh, S.Lq, S.db_si, S.Lk));
+      }
+    }
+  }
+  if (plan.fwd_tiles > kMaxGrid || plan.delta_tiles > kMaxGrid || plan.dkv_tiles > kMaxGrid)
+    return fail(OOPS_EINVAL, "launch grid exceeds 2^31-1 workgroups");
+  plan.fwd_uniform = u_fwd ? c_fwd : 0;
+  plan.delta_uniform = u_delta ? c_delta : 0;
+  plan.dkv_uniform = u_dkv ? c_dkv : 0;
+  if (plan.any_shared) {
+    int64_t parts = cdiv(kTargetSharedBiasBlocks, std::max<int64_t>(sbias_base, 1));
+    parts = std::min<int64_t>({parts, kMaxParts, min_shared_groups});
+    plan.parts = (int)std::max<int64_t>(parts, 1);
+    plan.sbias_tiles = sbias_base * plan.parts;
+    plan.sbias_uniform = u_sb && c_sb > 0 ? c_sb * plan.parts : 0;
+    int64_t c_red = -1;
+    bool u_red = true;
+    for (int s = 0; s < geo->num_samples; ++s) {
+      const Sample& S = tab[s];
+      const int64_t c = S.bias_mode == OOPS_BIAS_SHARED ? cdiv(H * S.Lq * S.Lk, 256) : 0;
+      plan.sred_tiles += c;
+      track(c, c_red, u_red);
+    }
+    plan.sred_uniform = u_red && c_red > 0 ? c_red : 0;
+    if (plan.sbias_tiles > kMaxGrid || plan.sred_tiles > kMaxGrid)
+      return fail(OOPS_EINVAL, "dBias launch grid exceeds 2^31-1 workgroups");
+  }
+  return OOPS_OK;
+}
+
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+size_t workspace_bytes(const oops::Plan& plan) {
+  size_t bytes = align256(sizeof(float) * (size_t)plan.lse_extent);
+  if (plan.any_shared && plan.parts > 1) bytes += align256(sizeof(float) * (size_t)plan.parts * plan.dbias_extent);
+  return bytes;
+}
+
+}  // namespace
+
+extern "C" {
+
+int oops_abi_version(void) { return 1; }
+
+const char* oops_last_error(void) { return g_last_error.c_str(); }
+
+int oops_attn_forward(const oops_attn_geometry* geo, const void* q, const void* k, const void* v,
+                      const uint8_t* mask, const void* bias, void* out, void* out_lo, float* lse,
+                      void* stream) {
+  g_last_error.clear();
+  oops::Plan plan;
+  if (int rc = make_plan(geo, plan)) return rc;
+  if (!q || !k || !v || !out) return fail(OOPS_EINVAL, "q, k, v and out must be non-NULL");
+  if (geo->has_bias && !bias) return fail(OOPS_EINVAL, "has_bias is set but bias is NULL");
+  if (geo->has_mask && !mask) return fail(OOPS_EINVAL, "has_mask is set but mask is NULL");
+  const hipError_t err = oops::launch_forward(*geo, plan, q, k, v, mask, bias, out, out_lo, lse,
+                                              static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) {
+    g_last_error = std::string("forward launch failed: ") + hipGetErrorString(err);
+    return OOPS_ELAUNCH;
+  }
+  return OOPS_OK;
+}
+
+size_t oops_attn_backward_workspace_bytes(const oops_attn_geometry* geo) {
+  oops::Plan plan;
+  if (make_plan(geo, plan)) return 0;
+  return workspace_bytes(plan);
+}
+
+int oops_attn_backward(const oops_attn_geometry* geo, const void* q, const void* k, const void* v,
+                       const uint8_t* mask, const void* bias, const void* out, const void* out_lo,
+                       const float* lse, const void* dout, void* dq, void* dk, void* dv, float* dbias, void* workspace,
+                       size_t ws_bytes, void* stream) {
+  g_last_error.clear();
+  oops::Plan plan;
+  if (int rc = make_plan(geo, plan)) return rc;
+  if (!q || !k || !v || !out || !lse || !dout) return fail(OOPS_EINVAL, "q, k, v, out, lse and dout must be non-NULL");
+  if (geo->has_bias && !bias) return fail(OOPS_EINVAL, "has_bias is set but bias is NULL");
+  if (geo->has_mask && !mask) return fail(OOPS_EINVAL, "has_mask is set but mask is NULL");
+  const size_t need = workspace_bytes(plan);
+  if (workspace == nullptr || ws_bytes < need)
+    return fail(OOPS_EWORKSPACE, "workspace of %lld bytes required, %lld given", (long long)need,
+                (long long)(workspace ? ws_bytes : 0));
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return fail(OOPS_EWORKSPACE, "workspace must be 256-byte aligned");
+  float* delta = static_cast<float*>(workspace);
+  float* parts = plan.any_shared && plan.parts > 1
+                     ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                                align256(sizeof(float) * (size_t)plan.lse_extent))
+                     : nullptr;
+  const hipError_t err = oops::launch_backward(*geo, plan, q, k, v, mask, bias, out, out_lo, lse, dout, dq, dk, dv,
+                                               geo->has_bias ? dbias : nullptr, delta, parts,
+                                               static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) {
+    g_last_error = std::string("backward launch failed: ") + hipGetErrorString(err);
+    return OOPS_ELAUNCH;
+  }
+  return OOPS_OK;
+}
+
+}  // extern "C"

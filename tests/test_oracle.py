@@ -1,0 +1,165 @@
+"""Pins the numpy oracle (oracle/attention.py) against independent routes.
+
+* torch.nn.functional.scaled_dot_product_attention (library routine), forward
+  and autograd, with the bias passed as a float attn_mask (so dBias is pinned);
+* a pure-Python brute-force loop (index / transposition mistakes);
+* central finite differences of the oracle forward (the analytic backward);
+* invariants: ending node == starting node on transposed tensors, shared
+  dBias == row-sum of full dBias, probabilities sum to one, fully masked rows
+  give zero output and zero gradients even with non-finite inputs.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attention as ora
+
+
+def _rand(rng, *shape):
+    return rng.standard_normal(shape)
+
+
+def _sdpa_triangle(q, k, v, mask, bias, scale):
+    """Triangle attention through SDPA on (B, R, H, C, D) tensors; float attn_mask carries bias and mask."""
+
+    qt, kt, vt = (x.transpose(-2, -3) for x in (q, k, v))
+    B, R, H, C, D = qt.shape
+    attn = torch.zeros(B, R, H, C, C, dtype=q.dtype)
+    if bias is not None:
+        attn = attn + bias
+    if mask is not None:
+        attn = attn.masked_fill(~mask[:, :, None, None, :], float("-inf"))
+    out = F.scaled_dot_product_attention(qt, kt, vt, attn_mask=attn, scale=scale)
+    return out.transpose(-2, -3)
+
+
+@pytest.mark.parametrize("bias_kind", ["none", "shared", "full"])
+@pytest.mark.parametrize("masked", [False, True])
+def test_forward_backward_vs_sdpa(bias_kind, masked):
+    rng = np.random.default_rng(7)
+    B, R, C, H, D = 2, 5, 9, 3, 8
+    q, k, v, do = (_rand(rng, B, R, C, H, D) for _ in range(4))
+    bias = None if bias_kind == "none" else _rand(rng, B, 1 if bias_kind == "shared" else R, H, C, C)
+    mask = None
+    if masked:
+        mask = rng.random((B, R, C)) > 0.3
+        mask[..., 0] = True  # SDPA returns NaN on fully masked rows; those are pinned separately
+    scale = 0.37
+    out, _ = ora.triangle_attention_forward(q, k, v, mask, bias, scale)
+    dq, dk, dv, db = ora.triangle_attention_backward(q, k, v, do, mask, bias, scale)
+
+    tq, tk, tv = (torch.tensor(x, requires_grad=True) for x in (q, k, v))
+    tb = None if bias is None else torch.tensor(bias, requires_grad=True)
+    tm = None if mask is None else torch.tensor(mask)
+    ref = _sdpa_triangle(tq, tk, tv, tm, tb, scale)
+    np.testing.assert_allclose(out, ref.detach().numpy(), atol=1e-12, rtol=1e-10)
+    leaves = [tq, tk, tv] + ([tb] if tb is not None else [])
+    grads = torch.autograd.grad(ref, leaves, torch.tensor(do))
+    for mine, theirs in zip((dq, dk, dv, db), grads):
+        np.testing.assert_allclose(mine, theirs.numpy(), atol=1e-11, rtol=1e-9)
+
+
+def test_bruteforce_loops():
+    rng = np.random.default_rng(3)
+    q, k, v = (_rand(rng, 1, 3, 4, 2, 3) for _ in range(3))
+    bias = _rand(rng, 1, 3, 2, 4, 4)
+    mask = np.array([[[1, 0, 1, 1], [0, 0, 0, 0], [1, 1, 0, 1]]], dtype=bool)
+    out, _ = ora.triangle_attention_forward(q, k, v, mask, bias)
+    brute = ora.triangle_attention_bruteforce(q, k, v, mask, bias)
+    np.testing.assert_allclose(out, brute, atol=1e-13)
+    assert np.all(out[0, 1] == 0.0)  # row 1 has no kept key
+
+
+def test_finite_differences():
+    rng = np.random.default_rng(11)
+    q, k, v, do = (_rand(rng, 1, 2, 4, 2, 3) for _ in range(4))
+    bias = _rand(rng, 1, 1, 2, 4, 4)
+    mask = np.array([[[1, 1, 0, 1], [1, 0, 1, 1]]], dtype=bool)
+    grads = ora.triangle_attention_backward(q, k, v, do, mask, bias)
+    args = [q, k, v, bias]
+    eps = 1e-6
+    for idx, g in enumerate(grads):
+        x = args[idx]
+        num = np.zeros_like(x)
+        it = np.nditer(x, flags=["multi_index"])
+        for _ in it:
+            i = it.multi_index
+            saved = x[i]
+            x[i] = saved + eps
+            fp = (ora.triangle_attention_forward(*args[:3], mask, args[3])[0] * do).sum()
+            x[i] = saved - eps
+            fm = (ora.triangle_attention_forward(*args[:3], mask, args[3])[0] * do).sum()
+            x[i] = saved
+            num[i] = (fp - fm) / (2 * eps)
+        np.testing.assert_allclose(g, num, atol=1e-7, rtol=1e-6)
+
+
+def test_invariants():
+    rng = np.random.default_rng(5)
+    B, R, C, H, D = 1, 4, 6, 2, 5
+    q, k, v, do = (_rand(rng, B, R, C, H, D) for _ in range(4))
+    # ending node == starting node on swapped pair axes
+    out, _ = ora.triangle_attention_forward(q, k, v)
+    sw = [np.swapaxes(x, 1, 2) for x in (q, k, v)]
+    out_sw, _ = ora.triangle_attention_forward(*sw)
+    direct = ora.triangle_attention_bruteforce(*sw)
+    np.testing.assert_allclose(out_sw, direct, atol=1e-12)
+    assert not np.allclose(out, np.swapaxes(out_sw, 1, 2))  # orientation matters
+    # shared-bias gradient == sum over rows of the full-bias gradient
+    shared = _rand(rng, B, 1, H, C, C)
+    full = np.broadcast_to(shared, (B, R, H, C, C)).copy()
+    db_shared = ora.triangle_attention_backward(q, k, v, do, None, shared)[3]
+    db_full = ora.triangle_attention_backward(q, k, v, do, None, full)[3]
+    np.testing.assert_allclose(db_shared, db_full.sum(axis=1, keepdims=True), atol=1e-12)
+    # dV == P^T dO with P rows summing to 1
+    s = np.einsum("brihd,brjhd->brhij", q, k) * D**-0.5
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    np.testing.assert_allclose(p.sum(-1), 1.0, atol=1e-12)
+    dv = ora.triangle_attention_backward(q, k, v, do)[2]
+    np.testing.assert_allclose(dv, np.einsum("brhij,brihd->brjhd", p, do), atol=1e-12)
+    # LSE == logsumexp of the scores
+    _, lse = ora.triangle_attention_forward(q, k, v)
+    np.testing.assert_allclose(lse, np.log(np.exp(s).sum(-1)), atol=1e-12)
+
+
+def test_fully_masked_nonfinite():
+    q = np.full((1, 3, 3, 1, 4), np.inf)
+    bias = np.full((1, 1, 1, 3, 3), np.nan)
+    mask = np.zeros((1, 3, 3), dtype=bool)
+    with np.errstate(invalid="ignore"):
+        out, lse = ora.triangle_attention_forward(q, q, q, mask, bias)
+        grads = ora.triangle_attention_backward(q, q, q, np.ones_like(q), mask, bias)
+    assert np.all(out == 0) and np.all(lse == 0)
+    for g in grads:
+        assert np.all(g == 0)
+
+
+@pytest.mark.parametrize("mask_kind", ["none", "key", "pair"])
+def test_pair_bias_vs_sdpa(mask_kind):
+    rng = np.random.default_rng(13)
+    S, H, Q, D = 3, 2, 7, 4
+    q, k, v, do = (_rand(rng, S, H, Q, D) for _ in range(4))
+    bias = _rand(rng, 1, H, Q, Q)
+    mask = None
+    if mask_kind == "key":
+        mask = rng.random((S, Q)) > 0.3
+        mask[:, 0] = True
+    elif mask_kind == "pair":
+        mask = rng.random((S, Q, Q)) > 0.3
+        mask[..., 0] = True
+    out = ora.pair_bias_attention_forward(q, k, v, mask, bias)
+    grads = ora.pair_bias_attention_backward(q, k, v, do, mask, bias)
+    tq, tk, tv, tb = (torch.tensor(x, requires_grad=True) for x in (q, k, v, bias))
+    attn = tb.expand(S, H, Q, Q)
+    if mask is not None:
+        keep = torch.tensor(mask)
+        keep = keep[:, None, None, :] if mask_kind == "key" else keep[:, None]
+        attn = attn.masked_fill(~keep, float("-inf"))
+    ref = F.scaled_dot_product_attention(tq, tk, tv, attn_mask=attn)
+    np.testing.assert_allclose(out, ref.detach().numpy(), atol=1e-12)
+    tgrads = torch.autograd.grad(ref, (tq, tk, tv, tb), torch.tensor(do))
+    for mine, theirs in zip(grads, tgrads):
+        np.testing.assert_allclose(mine, theirs.numpy(), atol=1e-11)

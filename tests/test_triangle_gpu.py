@@ -1,0 +1,182 @@
+"""GPU parity of dense triangle attention against the numpy oracle.
+
+Cases follow the reference's test matrix (tests/attention/triangle/
+test_triangle_attention.py:226-419): dtypes, starting/ending-node
+("swapped") layouts, prefix axes, shared/full/no bias, fp32 bias over half
+inputs, masks, odd head sizes, neg-bit views and aliasing.  Tolerances are
+those of BASELINE.json, read as max-abs error divided by max(1, |ref|)
+(absolute for unit-scale values, relative for larger ones, whose 16-bit
+output rounding alone would exceed 2e-2): fp32 <= 1e-5; 16-bit <= 2e-2 and
+mean-relative <= 1e-2, against the float64 oracle on the same (rounded)
+inputs.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as ora
+from oops_amd import OOpsUnsupportedError, triangle_attention
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _np(t):
+    return None if t is None else t.detach().double().cpu().numpy()
+
+
+def assert_close(actual, expected, dtype, what=""):
+    actual = actual.detach().double().cpu().numpy()
+    err = np.abs(actual - expected)
+    if dtype == torch.float32:
+        # 1e-5 absolute on unit-scale values, relative beyond |ref| > 1
+        scaled = err / np.maximum(1.0, np.abs(expected))
+        assert scaled.max() <= 1e-5, f"{what}: scaled max-abs {scaled.max():.3g} (max-abs {err.max():.3g})"
+    else:
+        # 2e-2 absolute on unit-scale values; relative beyond |ref| > 1, where the
+        # 16-bit result's own rounding (up to 2^-9 relative) would exceed 2e-2
+        scaled = err / np.maximum(1.0, np.abs(expected))
+        denom = np.abs(expected).mean() + 1e-12
+        assert scaled.max() <= 2e-2, f"{what}: scaled max-abs {scaled.max():.3g}"
+        assert err.mean() / denom <= 1e-2, f"{what}: mean-rel {err.mean() / denom:.3g}"
+
+
+def make_case(dtype, *, prefix=(2,), rows=4, cols=33, heads=2, head=24, bias_kind="shared", masked=True,
+              layout="dense", bias_dtype=None, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    shape = (*prefix, rows, cols, heads, head)
+    if layout == "swapped":
+        base = [torch.randn((*prefix, cols, rows, heads, head), generator=g).to(dtype) for _ in range(3)]
+        q, k, v = (b.transpose(-4, -3) for b in base)
+    else:
+        q, k, v = (torch.randn(shape, generator=g).to(dtype) for _ in range(3))
+    mask = None
+    if masked:
+        mask = torch.rand((*prefix, rows, cols), generator=g) > 0.2
+        mask[..., 0] = True
+    bias = None
+    if bias_kind != "none":
+        bshape = (*prefix, 1 if bias_kind == "shared" else rows, heads, cols, cols)
+        bias = torch.randn(bshape, generator=g).to(bias_dtype or dtype)
+    dout = torch.randn(shape, generator=g).to(dtype)
+    return q, k, v, mask, bias, dout
+
+
+def run_and_check(q, k, v, mask, bias, dout, dtype, grads=True, scale=None):
+    to = lambda t: None if t is None else t.to(DEV)
+    leaves = []
+    dq, dk, dv, db = (to(t) for t in (q, k, v, bias))
+    if q.dim() >= 5 and not q.is_contiguous():  # keep the swapped layout on device
+        dq, dk, dv = (torch.empty_strided(t.shape, t.stride(), dtype=t.dtype, device=DEV).copy_(t) for t in (q, k, v))
+    tensors = []
+    for t in (dq, dk, dv, db):
+        if t is not None and grads:
+            t.requires_grad_(True)
+            leaves.append(t)
+        tensors.append(t)
+    out = triangle_attention(tensors[0], tensors[1], tensors[2], to(mask), tensors[3], scale=scale)
+    assert out.shape == q.shape and out.dtype == q.dtype
+    m = _np(mask)
+    exp_out, _ = ora.triangle_attention_forward(_np(q), _np(k), _np(v), m, _np(bias), scale)
+    assert_close(out, exp_out, dtype, "out")
+    if not grads:
+        return
+    got = torch.autograd.grad(out, leaves, to(dout))
+    want = ora.triangle_attention_backward(_np(q), _np(k), _np(v), _np(dout), m, _np(bias), scale)
+    names = ("dq", "dk", "dv", "dbias")
+    for g_, w, leaf, name in zip(got, want, leaves, names):
+        assert g_.dtype == leaf.dtype and g_.shape == leaf.shape
+        assert_close(g_, w, dtype if name != "dbias" or leaf.dtype != torch.float32 else dtype, name)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("bias_kind", ["none", "shared", "full"])
+@pytest.mark.parametrize("layout", ["dense", "swapped"])
+def test_forward_backward(dtype, bias_kind, layout):
+    case = make_case(dtype, bias_kind=bias_kind, layout=layout)
+    run_and_check(*case, dtype)
+
+
+@pytest.mark.parametrize("head", [16, 32, 64, 128, 129, 255])
+def test_head_sizes_fp32(head):
+    case = make_case(torch.float32, rows=3, cols=17, head=head, seed=117)
+    run_and_check(*case, torch.float32)
+
+
+@pytest.mark.parametrize("head", [16, 24, 32, 64, 128, 129])
+def test_head_sizes_bf16(head):
+    case = make_case(torch.bfloat16, rows=3, cols=41, head=head, seed=3)
+    run_and_check(*case, torch.bfloat16)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fp32_bias_over_half(dtype):
+    case = make_case(dtype, bias_kind="full", bias_dtype=torch.float32)
+    run_and_check(*case, dtype)
+
+
+def test_prefixed_and_batchless():
+    case = make_case(torch.float32, prefix=(2, 3), rows=3, cols=19, head=16)
+    run_and_check(*case, torch.float32)
+    case = make_case(torch.float32, prefix=(), rows=5, cols=37, head=32, bias_kind="none")
+    q, k, v, mask, bias, dout = case
+    run_and_check(q, k, v, mask, None, dout, torch.float32)
+
+
+def test_scale_and_long_rows():
+    case = make_case(torch.bfloat16, prefix=(1,), rows=3, cols=300, heads=4, head=32, seed=5)
+    run_and_check(*case, torch.bfloat16, scale=0.3)
+
+
+def test_negative_view_and_alias():
+    q, k, v, mask, bias, dout = make_case(torch.float32, cols=21, head=16)
+    qd = q.to(DEV).requires_grad_(True)
+    out = triangle_attention(torch._neg_view(qd), torch._neg_view(qd), torch._neg_view(qd), mask.to(DEV))
+    exp, _ = ora.triangle_attention_forward(-_np(q), -_np(q), -_np(q), _np(mask))
+    assert_close(out, exp, torch.float32, "neg out")
+    (gq,) = torch.autograd.grad(out, (qd,), dout.to(DEV))
+    want = ora.triangle_attention_backward(-_np(q), -_np(q), -_np(q), _np(dout), _np(mask))
+    assert_close(gq, -(want[0] + want[1] + want[2]), torch.float32, "alias grad")
+
+
+def test_fully_masked_nonfinite():
+    q, k, v = (torch.full((1, 17, 17, 2, 129), float("inf"), device=DEV, requires_grad=True) for _ in range(3))
+    mask = torch.zeros(1, 17, 17, device=DEV, dtype=torch.bool)
+    bias = torch.full((1, 1, 2, 17, 17), float("nan"), device=DEV, requires_grad=True)
+    out = triangle_attention(q, k, v, mask, bias)
+    torch.testing.assert_close(out, torch.zeros_like(out))
+    for grad, leaf in zip(torch.autograd.grad(out.sum(), (q, k, v, bias)), (q, k, v, bias)):
+        torch.testing.assert_close(grad, torch.zeros_like(leaf))
+
+
+def test_rows_fully_masked_partially():
+    q, k, v, mask, bias, dout = make_case(torch.bfloat16, rows=6, cols=40, head=32, seed=9)
+    mask[:, 2] = False
+    run_and_check(q, k, v, mask, bias, dout, torch.bfloat16)
+
+
+def test_config_c2_key_padding():
+    """BASELINE config 2 at full size: N=384, H=4, c=32, bf16, last 10-30% keys padded (seed 1)."""
+
+    torch.manual_seed(1)
+    n, h, c = 384, 4, 32
+    q, k, v, dout = (torch.randn(1, n, n, h, c).to(torch.bfloat16) for _ in range(4))
+    bias = torch.randn(1, 1, h, n, n).to(torch.bfloat16)
+    frac = float(torch.empty(1).uniform_(0.10, 0.30, generator=torch.Generator().manual_seed(1)))
+    keep_len = n - round(n * frac)
+    mask = torch.ones(1, n, n, dtype=torch.bool)
+    mask[..., keep_len:] = False
+    mask[:, keep_len:, :] = False
+    run_and_check(q, k, v, mask, bias, dout, torch.bfloat16)
+
+
+def test_errors():
+    q = torch.randn(1, 3, 5, 2, 8, device=DEV)
+    with pytest.raises(ValueError):
+        triangle_attention(q, q, q[..., :-1])
+    with pytest.raises(OOpsUnsupportedError):
+        triangle_attention(q.double(), q.double(), q.double())
+    with pytest.raises(OOpsUnsupportedError):
+        triangle_attention(q, q, q, torch.ones(1, 3, 5, device=DEV))  # non-bool mask
