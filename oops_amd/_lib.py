@@ -12,7 +12,7 @@ import os
 import threading
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "lib" / "liboops_amd.so"
+LIB_PATH = Path(os.environ.get("OOPS_AMD_LIB") or Path(__file__).resolve().parent / "lib" / "liboops_amd.so")
 
 F32, BF16, F16 = 0, 1, 2
 BIAS_NONE, BIAS_FULL, BIAS_SHARED = 0, 1, 2
@@ -56,6 +56,7 @@ class Geometry(ctypes.Structure):
         ("vec_ok", ctypes.c_int32),
         ("scale", ctypes.c_float),
         ("phases", ctypes.c_int32),
+        ("force_generic", ctypes.c_int32),
         ("table_host", ctypes.c_void_p),
         ("table_device", ctypes.c_void_p),
     ]

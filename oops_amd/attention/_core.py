@@ -55,6 +55,23 @@ class profile_phases:
         return False
 
 
+_FORCE_GENERIC = 0
+
+
+class force_generic:
+    """Context manager routing calls to the generic kernels instead of the fast paths (testing)."""
+
+    def __enter__(self):
+        global _FORCE_GENERIC
+        self.saved, _FORCE_GENERIC = _FORCE_GENERIC, 1
+        return self
+
+    def __exit__(self, *exc):
+        global _FORCE_GENERIC
+        _FORCE_GENERIC = self.saved
+        return False
+
+
 # ----------------------------------------------------------------- tables
 
 _TABLE_CACHE: "OrderedDict[tuple, tuple[Tensor, Tensor]]" = OrderedDict()
@@ -122,6 +139,7 @@ def _geometry(q: Tensor, bias: Optional[Tensor], mask: Optional[Tensor], table: 
     geo.vec_ok = int(vec_ok)
     geo.scale = float(scale)
     geo.phases = _PHASES
+    geo.force_generic = _FORCE_GENERIC
     geo.table_host = host.data_ptr()
     geo.table_device = dev.data_ptr()
     return geo, (host, dev)

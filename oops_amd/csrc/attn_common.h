@@ -104,6 +104,56 @@ __device__ __forceinline__ void store_elems(T* dst, uint4 u) {
   for (int i = 0; i < (int)(16 / sizeof(T)); ++i) dst[i] = e[i];
 }
 
+// Buffer resource over `bytes` bytes at `base`: raw buffer loads through it
+// return zeros for offsets at or past `bytes` instead of faulting.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+
+// s_waitcnt vmcnt(0): wait for every outstanding vector-memory load.
+__device__ __forceinline__ void vmem_wait_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Workgroup barrier for LDS producer/consumer hand-off only: waits for this
+// wave's LDS operations (lgkmcnt(0)) but, unlike __syncthreads(), not for
+// its outstanding global loads, so prefetches stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// gfx950 LDS transpose read (ds_read_b64_tr_b16).  Within each group of 16
+// lanes, lane i receives in slot k element i % 4 of the 8-byte chunk addressed
+// by lane 4k + i / 4 of its group.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+__device__ __forceinline__ s16x4 lds_read_tr4(const void* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+}
+
+// 32x32x16 MFMA k-operand of X^T from a row-major LDS tile X[row][col]
+// (16-bit elements, row stride ld): lane (c = lane % 32, g = lane / 32) gets
+// X[r][c0 + c] for the 8 rows r of k-slots g*8 .. g*8+7, where k-slot j maps
+// to row r0 + kappa(g, j) (the accumulator row order, so accumulators feed
+// the other operand directly).  Two transpose reads of four rows each.
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::Frag lds_read_tr_frag(const T* tile, int ld, int r0, int c0, int lane) {
+  const int j = lane & 15;                 // lane within its 16-lane group
+  const int grp = lane >> 4;               // 0..3: (column half, k half g)
+  const int col = c0 + ((grp & 1) << 4) + ((j & 3) << 2);
+  const int g = grp >> 1;
+  const int row = r0 + (g << 2) + (j >> 2);  // kappa(g, 0..3) + (j>>2) over 4 consecutive rows
+  const s16x4 lo = lds_read_tr4(tile + row * ld + col);
+  const s16x4 hi = lds_read_tr4(tile + (row + 8) * ld + col);
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(typename Elem<T>::Frag, v);
+}
+
 // ---------------------------------------------------------------- geometry
 struct Sample {
   int64_t G, Lq, Lk;
@@ -140,5 +190,23 @@ __device__ __forceinline__ int find_sample(int64_t& tile, const Sample* table, i
 }
 
 __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// MI355X has 8 XCDs, each with its own L2; workgroup b of a launch runs on XCD
+// b % 8.  With a grid padded to a multiple of 8, xcd_tile maps b to a logical
+// tile so that each XCD processes one contiguous range of logical tiles.
+constexpr int kNumXcds = 8;
+__host__ __device__ __forceinline__ int64_t xcd_grid(int64_t tiles) {
+  return (tiles + kNumXcds - 1) / kNumXcds * kNumXcds;
+}
+__device__ __forceinline__ int64_t xcd_tile(int64_t block, int64_t grid) {
+  return (block % kNumXcds) * (grid / kNumXcds) + block / kNumXcds;
+}
+// Heads whose D-element rows together fill one 128-byte line.
+__host__ __forceinline__ int head_group(const oops_attn_geometry& geo) {
+  const int bytes = geo.head_size * (geo.dtype == OOPS_F32 ? 4 : 2);
+  int hg = 1;
+  while (hg * 2 <= geo.num_heads && geo.num_heads % (hg * 2) == 0 && hg * 2 * bytes <= 128) hg *= 2;
+  return hg;
+}
 
 }  // namespace oops

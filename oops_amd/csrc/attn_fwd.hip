@@ -278,6 +278,9 @@ hipError_t launch_forward(const oops_attn_geometry& geo, const Plan& plan, const
                           const void* v, const uint8_t* mask, const void* bias, void* out, void* out_lo, float* lse,
                           hipStream_t stream) {
   hipError_t err = hipSuccess;
+  if (!geo.force_generic &&
+      launch_forward_fast(geo, plan, q, k, v, mask, bias, out, out_lo, lse, stream, &err))
+    return err;
   const bool ok = dispatch_config(geo.dtype, geo.bias_dtype, plan.dp, [&](auto t, auto bt, auto dpc) {
     using T = typename decltype(t)::type;
     using BT = typename decltype(bt)::type;

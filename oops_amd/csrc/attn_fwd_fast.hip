@@ -1,0 +1,443 @@
+// Forward fast path for 16-bit Q/K/V (bias in the same dtype or absent),
+// head size <= 64 and a multiple of 8: the configuration of the headline
+// workload.
+//
+// At head size 32 every score costs only 128 MFMA flops, so the per-score
+// vector work (scale, bias, exponent, row statistics, conversion) bounds the
+// kernel, not the matrix cores.  The kernel therefore
+//   * adds the bias on the matrix core: acc += I(1/scale) x bias, with a
+//     constant identity A-fragment and the bias rows (natural layout, one
+//     16-byte load per fragment) as the B-fragment, so a logit costs one FMA
+//     (x = acc * scale * log2 e - m) before its exponent;
+//   * raises the running max lazily (only when it grows by more than 2^8),
+//     so the O rescale is skipped on almost every step;
+//   * sums the row with v_dot2 on the packed probabilities that also feed
+//     the PV MFMA;
+//   * resolves masks per 64-key tile from a bitmap built once per
+//     workgroup: fully kept tiles do no mask work, fully masked tiles are
+//     skipped, only mixed tiles select per score;
+//   * software-pipelines inside each wave: the QK^T MFMAs of tile i+1 are
+//     issued before the softmax of tile i, so the matrix core works while
+//     the vector ALU computes exponents.
+// Work split: 4 wavefronts x 32 queries per workgroup, 64 keys per step.
+// K (row-major) and V (transposed, key-permuted) go through a 3-buffer LDS
+// ring (one barrier per step, written two steps ahead); bias fragments are
+// loaded from global memory straight into registers two steps ahead.  All
+// loads use range-checked buffer resources whose per-thread offsets are
+// fixed; the per-step part rides in the scalar offset.
+//
+// Semantics are those of the generic forward (attn_fwd.hip), i.e. of the
+// reference's _attend (oops/attention/triangle/triton/kernel.py:151-262):
+// masked keys read as -inf logits with zero K/V, fully masked rows give
+// O = 0 and LSE = 0.  The bias weight 1/scale is rounded to the input dtype
+// (relative error <= 2^-9 for bf16), below the rounding of P itself.
+#include "attn_kernels.h"
+
+namespace oops {
+
+namespace {
+
+template <typename T> struct Pair;
+template <> struct Pair<__bf16> {
+  typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ float dot(v2 a, v2 b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
+  }
+};
+template <> struct Pair<_Float16> {
+  typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ float dot(v2 a, v2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
+};
+
+constexpr int kMaxKeyTiles = 256;  // Lk <= 16384 on this path
+constexpr float kLazyRescale = 8.0f;
+constexpr uint32_t kOut = 0x80000000u;  // a buffer offset past every resource
+
+// max / sum of x over both 32-lane halves, in every lane
+__device__ __forceinline__ float max_halves(float x) {
+  const int xi = __builtin_bit_cast(int, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(xi, xi, false, false);
+  return fmaxf(__builtin_bit_cast(float, (int)r[0]), __builtin_bit_cast(float, (int)r[1]));
+}
+__device__ __forceinline__ float sum_halves(float x) {
+  const int xi = __builtin_bit_cast(int, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(xi, xi, false, false);
+  return __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+}
+
+__device__ __forceinline__ uint4 buffer_load16_s(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+}  // namespace
+
+template <typename T, int DP, bool HAS_BIAS>
+__global__ __launch_bounds__(256, 2) void attn_fwd_fast_kernel(FwdArgsT<T, T> a) {
+  using E = Elem<T>;
+  using Frag = typename E::Frag;
+  using P2 = typename Pair<T>::v2;
+  constexpr int KLD = DP + 8;        // K tile row (elements)
+  constexpr int VLD = DP + 8;        // V tile row (elements), natural layout
+  constexpr int NDT = DP / 32;
+  constexpr int NQF = DP / 16;
+  constexpr int NCH = DP / 32;       // 16-byte K (and V) chunks per thread per step
+  constexpr int KBUF = 64 * KLD;     // elements per K buffer
+  constexpr int VBUF = 64 * VLD;
+
+  __shared__ __attribute__((aligned(16))) T k_lds[3 * KBUF];
+  __shared__ __attribute__((aligned(16))) T v_lds[3 * VBUF];
+  __shared__ uint64_t keep_lds[kMaxKeyTiles];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int lq = lane & 31;
+  const int g2 = lane >> 5;
+
+  // XCD-aware order: the dispatcher deals workgroups round-robin to the 8
+  // XCDs, so workgroup b runs on XCD b % 8; each XCD gets one contiguous
+  // range of logical tiles.  Within a sample the logical order is
+  // (head group, group g, head in group, query block): the query blocks of
+  // one (g, head group) share K/V in one L2, and each XCD sees the bias of
+  // only its head group.
+  int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
+  if (tile >= a.total_tiles) return;
+  const Sample* tab = reinterpret_cast<const Sample*>(a.table);
+  const int H = a.num_heads;
+  const int s_idx = find_sample(tile, tab, a.num_samples, a.uniform_tiles,
+                                [&](const Sample& s) { return s.G * H * cdiv(s.Lq, 128); });
+  if (s_idx < 0) return;
+  const Sample& S = tab[__builtin_amdgcn_readfirstlane(s_idx)];
+  const int64_t G = S.G;
+  const int Lq = (int)S.Lq, Lk = (int)S.Lk;
+  const int nqb = (int)cdiv(Lq, 128);
+  const int HG = a.head_group;
+  const int qb = (int)(tile % nqb);
+  int64_t rest = tile / nqb;
+  const int hh = (int)(rest % HG);
+  rest /= HG;
+  const int g = (int)(rest % G);
+  const int h = (int)(rest / G) * HG + hh;
+  const int D = a.head_size;
+  const int ntiles = (Lk + 63) >> 6;
+  const int k_si = (int)S.k_si, v_si = (int)S.v_si, b_si = (int)S.b_si;
+
+  const T* kbase = a.k + S.k_off + g * S.k_sg + h * S.k_sh;
+  const T* vbase = a.v + S.v_off + g * S.v_sg + h * S.v_sh;
+  const bool has_mask = a.mask != nullptr && S.m_off >= 0;
+  const uint8_t* mbase = has_mask ? a.mask + S.m_off + g * S.m_sg : nullptr;
+
+  // ---- per 64-key tile keep bitmaps (bit i: key 64t+i in range and kept)
+  for (int t = wave; t < ntiles; t += 4) {
+    const int key = t * 64 + lane;
+    bool keep = key < Lk;
+    if (keep && has_mask) keep = mbase[key] != 0;
+    const uint64_t bits = __ballot(keep);
+    if (lane == 0) keep_lds[t] = bits;
+  }
+
+  const int q_lane = qb * 128 + wave * 32 + lq;
+  const bool qv = q_lane < Lq;
+  Frag qf[NQF];
+  {
+    const T* qrow = a.q + S.q_off + g * S.q_sg + h * S.q_sh + (int64_t)q_lane * S.q_si;
+#pragma unroll
+    for (int s = 0; s < NQF; ++s) {
+      const int col = s * 16 + g2 * 8;
+      qf[s] = __builtin_bit_cast(
+          Frag, qv && col < D ? *reinterpret_cast<const uint4*>(qrow + col) : make_uint4(0, 0, 0, 0));
+    }
+  }
+  // identity A-fragments carrying the bias weight 1/scale: MFMA c adds bias keys 16c..16c+15
+  Frag ident[2];
+  {
+    const T w = (T)(1.0f / a.scale);
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ident[c][j] = (lq == 16 * c + g2 * 8 + j) ? w : (T)0.0f;
+  }
+
+  // ---- fixed per-thread load offsets (bytes); the step adds k0 * stride via soffset
+  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kbase, (uint32_t)(((int64_t)(Lk - 1) * k_si + D) * 2));
+  const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vbase, (uint32_t)(((int64_t)(Lk - 1) * v_si + D) * 2));
+  uint32_t kv_row[NCH], k_off[NCH], v_off[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int c = tid + 256 * i;
+    const int r = c / (DP / 8);
+    const int col = (c % (DP / 8)) * 8;
+    kv_row[i] = r;
+    k_off[i] = col < D ? (uint32_t)((r * k_si + col) * 2) : kOut;
+    v_off[i] = col < D ? (uint32_t)((r * v_si + col) * 2) : kOut;
+  }
+  const T* bbase = HAS_BIAS ? a.bias + S.b_off + g * S.b_sg + h * S.b_sh : a.q;
+  const __amdgpu_buffer_rsrc_t b_rsrc =
+      make_rsrc(bbase, HAS_BIAS ? (uint32_t)(((int64_t)(Lq - 1) * b_si + Lk) * 2) : 0u);
+  uint32_t b_off[2][2];
+#pragma unroll
+  for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+      b_off[t2][c] = qv ? (uint32_t)((q_lane * b_si + 32 * t2 + 16 * c + g2 * 8) * 2) : kOut;
+
+  // tile -> registers (K, V chunks of this thread; masked keys read zeros)
+  auto load_kv = [&](int t, uint4 (&ku)[NCH], uint4 (&vu)[NCH]) {
+    const uint64_t bits = keep_lds[t];
+    const uint32_t ks = (uint32_t)(t * 64 * k_si * 2), vs = (uint32_t)(t * 64 * v_si * 2);
+    const bool full = bits == ~uint64_t(0);
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const bool ok = full || ((bits >> kv_row[i]) & 1);
+      ku[i] = buffer_load16_s(k_rsrc, ok ? k_off[i] : kOut, ks);
+      vu[i] = buffer_load16_s(v_rsrc, ok ? v_off[i] : kOut, vs);
+    }
+  };
+  auto store_kv = [&](int buf, const uint4 (&ku)[NCH], const uint4 (&vu)[NCH]) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int c = tid + 256 * i;
+      const int r = c / (DP / 8);
+      const int col = (c % (DP / 8)) * 8;
+      *reinterpret_cast<uint4*>(&k_lds[buf * KBUF + r * KLD + col]) = ku[i];
+      *reinterpret_cast<uint4*>(&v_lds[buf * VBUF + r * VLD + col]) = vu[i];
+    }
+  };
+  // bias B-fragments of a tile: keys past Lk fall in the next row or past the
+  // resource; both are masked (mixed tile) or read as zero
+  // (the tile offset goes into the vector offset: the hardware range check
+  // covers the vector offset, which keeps the last row's tail in bounds)
+  auto load_bias = [&](int t, uint4 (&bf)[2][2]) {
+    const uint32_t s = (uint32_t)(t * 64 * 2);
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) bf[t2][c] = buffer_load16_s(b_rsrc, b_off[t2][c] + s, 0);
+  };
+  // S^T of a tile (bias by identity MFMA, then Q K^T) from LDS buffer buf
+  auto scores = [&](int buf, const uint4 (&bf)[2][2], f32x16 (&sacc)[2]) {
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) {
+      if constexpr (HAS_BIAS) {
+        sacc[t2] = E::mma(ident[0], __builtin_bit_cast(Frag, bf[t2][0]), f32x16{});
+        sacc[t2] = E::mma(ident[1], __builtin_bit_cast(Frag, bf[t2][1]), sacc[t2]);
+      } else {
+        sacc[t2] = f32x16{};
+      }
+#pragma unroll
+      for (int s = 0; s < NQF; ++s) {
+        const Frag kf = __builtin_bit_cast(
+            Frag, *reinterpret_cast<const uint4*>(&k_lds[buf * KBUF + (32 * t2 + lq) * KLD + s * 16 + g2 * 8]));
+        sacc[t2] = E::mma(kf, qf[s], sacc[t2]);
+      }
+    }
+  };
+
+  __syncthreads();  // keep bitmaps visible
+  auto next_tile = [&](int t) {
+    if (t >= ntiles) return ntiles;
+    ++t;
+    while (t < ntiles && keep_lds[t] == 0) ++t;
+    return t;
+  };
+
+  const float c1 = a.scale * kLog2e;
+  float m_run = kNegInf;  // reference max (log2 units), raised lazily
+  float l_run = 0.0f;     // this lane's partial row sum
+  f32x16 oacc[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) oacc[t] = f32x16{};
+  P2 ones;
+  ones[0] = (T)1.0f;
+  ones[1] = (T)1.0f;
+
+  // softmax of one tile's scores + O^T += V^T P^T from LDS buffer buf
+  auto attend = [&](int buf, uint64_t bits, f32x16 (&sacc)[2]) {
+    if (bits != ~uint64_t(0)) {
+      // mixed tile: masked / out-of-range keys get -inf
+      const uint64_t lb = bits >> (g2 * 4);
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int kk = 32 * t2 + ((j >> 2) << 3) + (j & 3);
+          sacc[t2][j] = ((lb >> kk) & 1) ? sacc[t2][j] : kNegInf;
+        }
+    }
+    float mx = sacc[0][0];
+#pragma unroll
+    for (int j = 1; j < 16; ++j) mx = fmaxf(mx, sacc[0][j]);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) mx = fmaxf(mx, sacc[1][j]);
+    mx = max_halves(mx) * c1;
+    const bool grow = mx > m_run + kLazyRescale;
+    if (__any(grow)) {
+      const float m_new = grow ? mx : m_run;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) oacc[t] *= alpha;
+    }
+    const float neg_m = m_run == kNegInf ? 0.0f : -m_run;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        Frag pf;
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          P2 pr;
+          pr[0] = (T)__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t2][8 * m + e], c1, neg_m));
+          pr[1] = (T)__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t2][8 * m + e + 1], c1, neg_m));
+          l_run = Pair<T>::dot(pr, ones, l_run);
+          pf[e] = pr[0];
+          pf[e + 1] = pr[1];
+        }
+#pragma unroll
+        for (int t = 0; t < NDT; ++t) {
+          const Frag vf = lds_read_tr_frag<T>(&v_lds[buf * VBUF], VLD, 32 * t2 + 16 * m, t * 32, lane);
+          oacc[t] = E::mma(vf, pf, oacc[t]);
+        }
+      }
+  };
+
+  // ---- pipeline.  Step i (tile t0, LDS buffer i % 3):
+  //   store K/V of t2 (loaded during step i-1) into buffer (i+2) % 3,
+  //   issue K/V loads of t3, issue QK^T of t1 (its buffer was filled in
+  //   step i-1), issue bias loads of t3 (into the stage t1 just freed), softmax + PV of t0, barrier.
+  uint4 ku[NCH], vu[NCH];
+  uint4 bias_a[2][2], bias_b[2][2];
+  f32x16 sacc_a[2], sacc_b[2];
+  int t0 = next_tile(-1);
+  int t1 = next_tile(t0);
+  int t2 = next_tile(t1);
+  if (t0 < ntiles) {
+    load_kv(t0, ku, vu);
+    if constexpr (HAS_BIAS) load_bias(t0, bias_a);
+    store_kv(0, ku, vu);
+  }
+  if (t1 < ntiles) {
+    load_kv(t1, ku, vu);
+    if constexpr (HAS_BIAS) load_bias(t1, bias_b);
+    store_kv(1, ku, vu);
+  }
+  if (t2 < ntiles) load_kv(t2, ku, vu);
+  // drain every prologue load (Q included) so the wait counters are clean
+  // at loop entry and only the loads issued in a step are ever in flight
+  vmem_wait_all();
+  __syncthreads();
+  if (t0 < ntiles) scores(0, bias_a, sacc_a);
+  if constexpr (HAS_BIAS)
+    if (t2 < ntiles) load_bias(t2, bias_a);
+
+  int buf = 0;
+  // bias_nxt holds bias(t1); once scores(t1) has consumed it, it receives bias(t3)
+  auto step = [&](auto& sacc_cur, auto& sacc_nxt, auto& bias_nxt) {
+    const int t3 = next_tile(t2);
+    const uint64_t bits = keep_lds[t0];
+    const int b1 = buf == 2 ? 0 : buf + 1;
+    const int b2 = b1 == 2 ? 0 : b1 + 1;
+    if (t2 < ntiles) store_kv(b2, ku, vu);
+    if (t3 < ntiles) load_kv(t3, ku, vu);
+    if (t1 < ntiles) scores(b1, bias_nxt, sacc_nxt);
+    if constexpr (HAS_BIAS)
+      if (t3 < ntiles) load_bias(t3, bias_nxt);
+    attend(buf, bits, sacc_cur);
+    lds_barrier();
+    buf = b1;
+    t0 = t1;
+    t1 = t2;
+    t2 = t3;
+  };
+  while (t0 < ntiles) {
+    step(sacc_a, sacc_b, bias_b);
+    if (t0 >= ntiles) break;
+    step(sacc_b, sacc_a, bias_a);
+  }
+
+  // ---- epilogue
+  const float l_tot = sum_halves(l_run);
+  const float inv = 1.0f / (l_tot == 0.0f ? 1.0f : l_tot);
+  if (qv) {
+    const int64_t o_row = S.o_off + g * S.o_sg + h * S.o_sh + (int64_t)q_lane * S.o_si;
+    T* orow = a.out + o_row;
+    T* lrow = a.out_lo != nullptr ? a.out_lo + o_row : nullptr;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int d = t * 32 + kappa(g2, i);
+        if (d < D) {
+          const float o = oacc[t][i] * inv;
+          const T hi = E::from_f(o);
+          orow[d] = hi;
+          if (lrow) lrow[d] = E::from_f(o - E::to_f(hi));
+        }
+      }
+    }
+    if (g2 == 0 && a.lse != nullptr) {
+      const float m_use = m_run == kNegInf ? 0.0f : m_run;
+      a.lse[S.l_off + ((int64_t)g * H + h) * Lq + q_lane] = l_tot == 0.0f ? 0.0f : m_use + __log2f(l_tot);
+    }
+  }
+}
+
+#define OOPS_FWD_FAST_INST(T, DP)                                                \
+  template __global__ void attn_fwd_fast_kernel<T, DP, true>(FwdArgsT<T, T>);  \
+  template __global__ void attn_fwd_fast_kernel<T, DP, false>(FwdArgsT<T, T>);
+OOPS_FWD_FAST_INST(__bf16, 32)
+OOPS_FWD_FAST_INST(__bf16, 64)
+OOPS_FWD_FAST_INST(_Float16, 32)
+OOPS_FWD_FAST_INST(_Float16, 64)
+
+bool launch_forward_fast(const oops_attn_geometry& geo, const Plan& plan, const void* q, const void* k,
+                         const void* v, const uint8_t* mask, const void* bias, void* out, void* out_lo,
+                         float* lse, hipStream_t stream, hipError_t* err) {
+  if (geo.dtype == OOPS_F32 || plan.dp > 64 || plan.max_len_k > 64 * kMaxKeyTiles || plan.any_pair_mask ||
+      !geo.vec_ok || geo.head_size % 8 != 0 || !plan.offsets_32bit)
+    return false;
+  if (geo.has_bias && geo.bias_dtype != geo.dtype) return false;
+  auto go = [&](auto tag, auto dpc) {
+    using T = typename decltype(tag)::type;
+    constexpr int DP = decltype(dpc)::value;
+    FwdArgsT<T, T> a;
+    a.q = static_cast<const T*>(q);
+    a.k = static_cast<const T*>(k);
+    a.v = static_cast<const T*>(v);
+    a.bias = geo.has_bias ? static_cast<const T*>(bias) : nullptr;
+    a.mask = geo.has_mask ? mask : nullptr;
+    a.out = static_cast<T*>(out);
+    a.out_lo = static_cast<T*>(out_lo);
+    a.lse = lse;
+    a.table = geo.table_device;
+    a.uniform_tiles = plan.fwd_uniform;
+    a.num_samples = geo.num_samples;
+    a.num_heads = geo.num_heads;
+    a.head_size = geo.head_size;
+    a.vec_ok = geo.vec_ok;
+    a.scale = geo.scale;
+    a.total_tiles = plan.fwd_tiles;
+    a.head_group = head_group(geo);
+    const dim3 grid((unsigned)xcd_grid(plan.fwd_tiles));
+    if (a.bias != nullptr)
+      hipLaunchKernelGGL((attn_fwd_fast_kernel<T, DP, true>), grid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((attn_fwd_fast_kernel<T, DP, false>), grid, dim3(256), 0, stream, a);
+    *err = hipGetLastError();
+  };
+  if (plan.fwd_tiles == 0) {
+    *err = hipSuccess;
+    return true;
+  }
+  if (geo.dtype == OOPS_BF16) {
+    if (plan.dp == 32) go(Tag<__bf16>{}, std::integral_constant<int, 32>{});
+    else go(Tag<__bf16>{}, std::integral_constant<int, 64>{});
+  } else {
+    if (plan.dp == 32) go(Tag<_Float16>{}, std::integral_constant<int, 32>{});
+    else go(Tag<_Float16>{}, std::integral_constant<int, 64>{});
+  }
+  return true;
+}
+
+}  // namespace oops

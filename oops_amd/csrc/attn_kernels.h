@@ -18,6 +18,8 @@ struct FwdArgsT {
   float* lse;
   const int64_t* table;
   int64_t uniform_tiles;
+  int64_t total_tiles;  // logical tiles (the grid may be padded for the XCD order)
+  int head_group;       // heads whose rows share a 128-byte line, scheduled together
   int num_samples;
   int num_heads;
   int head_size;
@@ -116,7 +118,15 @@ struct Plan {
   int64_t dbias_extent = 0;                      // floats
   int parts = 1;
   bool any_full = false, any_shared = false;
+  bool any_pair_mask = false;                    // a mask that depends on the query
+  bool offsets_32bit = true;                     // every per-(group, head) K/V/bias block < 2 GiB
+  int64_t max_len_q = 0, max_len_k = 0;
 };
+
+// Fast paths (16-bit, head size <= 64); return false when the geometry is not covered.
+bool launch_forward_fast(const oops_attn_geometry& geo, const Plan& plan, const void* q, const void* k,
+                         const void* v, const uint8_t* mask, const void* bias, void* out, void* out_lo,
+                         float* lse, hipStream_t stream, hipError_t* err);
 
 hipError_t launch_forward(const oops_attn_geometry& geo, const Plan& plan, const void* q, const void* k,
                           const void* v, const uint8_t* mask, const void* bias, void* out, void* out_lo,

@@ -26,7 +26,8 @@ LIB_DIR = PKG / "lib"
 OBJ_DIR = REPO / "_build" / "oops_amd"
 LIB_NAME = "liboops_amd.so"
 
-SOURCES = ("attn_fwd.hip", "attn_bwd.hip", "capi.cpp")
+SOURCES = ("attn_fwd.hip", "attn_fwd_fast.hip", "attn_bwd.hip", "capi.cpp")
+FAST_MATH_SOURCES = ("attn_fwd_fast.hip",)
 ARCH = "gfx950"
 
 
@@ -74,6 +75,10 @@ def _compile(src: str, hipcc: str, extra: list[str]) -> Path:
     ]
     if src.endswith(".cpp"):
         cmd[1:1] = ["-x", "hip"]
+    if src in FAST_MATH_SOURCES:
+        # min/max without NaN canonicalisation (the kernels select masked
+        # scores explicitly and never test for NaN)
+        cmd[1:1] = ["-mno-amdgpu-ieee", "-fno-honor-nans"]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{proc.stderr[-8000:]}")

@@ -91,6 +91,16 @@ int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
     track(c3, c_dkv, u_dkv);
     track(cs, c_sb, u_sb);
     plan.lse_extent = std::max(plan.lse_extent, S.l_off + S.G * H * S.Lq);
+    plan.max_len_q = std::max(plan.max_len_q, S.Lq);
+    plan.max_len_k = std::max(plan.max_len_k, S.Lk);
+    if (geo->has_mask && S.m_off >= 0 && S.m_si != 0) plan.any_pair_mask = true;
+    {
+      const int64_t elt = geo->dtype == OOPS_F32 ? 4 : 2;
+      const int64_t lim = int64_t(1) << 31;
+      const int64_t kspan = (S.Lk * std::max(S.k_si, S.v_si) + geo->head_size) * elt;
+      const int64_t bspan = (S.Lq * std::max<int64_t>(S.b_si, 0) + S.Lk) * elt;
+      if (kspan >= lim || bspan >= lim) plan.offsets_32bit = false;
+    }
     if (geo->has_bias && S.b_off >= 0) {
       if (S.bias_mode == OOPS_BIAS_FULL) plan.any_full = true;
       if (S.bias_mode == OOPS_BIAS_SHARED) {
