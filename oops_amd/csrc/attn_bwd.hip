@@ -721,39 +721,21 @@ OOPS_FOR_EACH_CONFIG(OOPS_BWD_INST)
 
 namespace oops {
 
+int head_group_of(const oops_attn_geometry& geo) { return head_group(geo); }
+
 hipError_t launch_backward(const oops_attn_geometry& geo, const Plan& plan, const void* q, const void* k,
                            const void* v, const uint8_t* mask, const void* bias, const void* out,
-                           const void* out_lo, const float* lse, const void* dout, void* dq, void* dk, void* dv, float* dbias,
-                           float* delta, float* dbias_part, hipStream_t stream) {
+                           const void* out_lo, const float* lse, const void* dout, void* dq, void* dk, void* dv,
+                           float* dbias, float* delta, float* dbias_part, hipStream_t stream) {
+  const BwdLaunch L{q, k, v, out, out_lo, dout, bias, mask, lse, delta, dq, dk, dv, dbias, dbias_part};
+  const bool fast = backward_fast_ok(geo, plan);
   hipError_t err = hipSuccess;
   const bool ok = dispatch_config(geo.dtype, geo.bias_dtype, plan.dp, [&](auto t, auto bt, auto dpc) {
     using T = typename decltype(t)::type;
     using BT = typename decltype(bt)::type;
     constexpr int DP = decltype(dpc)::value;
     BwdArgsT<T, BT> a;
-    a.q = static_cast<const T*>(q);
-    a.k = static_cast<const T*>(k);
-    a.v = static_cast<const T*>(v);
-    a.out = static_cast<const T*>(out);
-    a.out_lo = static_cast<const T*>(out_lo);
-    a.dout = static_cast<const T*>(dout);
-    a.bias = geo.has_bias ? static_cast<const BT*>(bias) : nullptr;
-    a.mask = geo.has_mask ? mask : nullptr;
-    a.lse = lse;
-    a.delta = delta;
-    a.dq = static_cast<T*>(dq);
-    a.dk = static_cast<T*>(dk);
-    a.dv = static_cast<T*>(dv);
-    a.dbias = geo.has_bias ? dbias : nullptr;
-    a.dbias_part = dbias_part;
-    a.table = geo.table_device;
-    a.dbias_extent = plan.dbias_extent;
-    a.num_samples = geo.num_samples;
-    a.num_heads = geo.num_heads;
-    a.head_size = geo.head_size;
-    a.vec_ok = geo.vec_ok;
-    a.parts = plan.parts;
-    a.scale = geo.scale;
+    fill_bwd_args(a, geo, plan, L);
     const dim3 block(256);
     auto check = [&]() {
       if (err == hipSuccess) err = hipGetLastError();
@@ -771,9 +753,13 @@ hipError_t launch_backward(const oops_attn_geometry& geo, const Plan& plan, cons
       check();
     }
     if ((phases & OOPS_PHASE_DKV) && (dk != nullptr || dv != nullptr) && plan.dkv_tiles > 0) {
-      a.uniform_tiles = plan.dkv_uniform;
-      hipLaunchKernelGGL((attn_dkv_kernel<T, BT, DP>), dim3((unsigned)plan.dkv_tiles), block, 0, stream, a);
-      check();
+      if (fast) {
+        if (err == hipSuccess) err = launch_dkv_fast(geo, plan, L, stream);
+      } else {
+        a.uniform_tiles = plan.dkv_uniform;
+        hipLaunchKernelGGL((attn_dkv_kernel<T, BT, DP>), dim3((unsigned)plan.dkv_tiles), block, 0, stream, a);
+        check();
+      }
     }
     if ((phases & OOPS_PHASE_DBIAS) && a.dbias != nullptr && plan.any_shared && plan.sbias_tiles > 0) {
       a.uniform_tiles = plan.sbias_uniform;

@@ -31,45 +31,16 @@
 // masked keys read as -inf logits with zero K/V, fully masked rows give
 // O = 0 and LSE = 0.  The bias weight 1/scale is rounded to the input dtype
 // (relative error <= 2^-9 for bf16), below the rounding of P itself.
-#include "attn_kernels.h"
+#include "attn_fast_common.h"
+
+#ifndef OOPS_FWD_PIPE
+#define OOPS_FWD_PIPE 0
+#endif
 
 namespace oops {
 
-namespace {
+using namespace fast;
 
-template <typename T> struct Pair;
-template <> struct Pair<__bf16> {
-  typedef __bf16 v2 __attribute__((ext_vector_type(2)));
-  static __device__ __forceinline__ float dot(v2 a, v2 b, float c) {
-    return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
-  }
-};
-template <> struct Pair<_Float16> {
-  typedef _Float16 v2 __attribute__((ext_vector_type(2)));
-  static __device__ __forceinline__ float dot(v2 a, v2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
-};
-
-constexpr int kMaxKeyTiles = 256;  // Lk <= 16384 on this path
-constexpr float kLazyRescale = 8.0f;
-constexpr uint32_t kOut = 0x80000000u;  // a buffer offset past every resource
-
-// max / sum of x over both 32-lane halves, in every lane
-__device__ __forceinline__ float max_halves(float x) {
-  const int xi = __builtin_bit_cast(int, x);
-  const auto r = __builtin_amdgcn_permlane32_swap(xi, xi, false, false);
-  return fmaxf(__builtin_bit_cast(float, (int)r[0]), __builtin_bit_cast(float, (int)r[1]));
-}
-__device__ __forceinline__ float sum_halves(float x) {
-  const int xi = __builtin_bit_cast(int, x);
-  const auto r = __builtin_amdgcn_permlane32_swap(xi, xi, false, false);
-  return __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
-}
-
-__device__ __forceinline__ uint4 buffer_load16_s(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-}
-
-}  // namespace
 
 template <typename T, int DP, bool HAS_BIAS>
 __global__ __launch_bounds__(256, 2) void attn_fwd_fast_kernel(FwdArgsT<T, T> a) {
@@ -327,23 +298,32 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fast_kernel(FwdArgsT<T, T> a)
   // at loop entry and only the loads issued in a step are ever in flight
   vmem_wait_all();
   __syncthreads();
+#if OOPS_FWD_PIPE
   if (t0 < ntiles) scores(0, bias_a, sacc_a);
   if constexpr (HAS_BIAS)
     if (t2 < ntiles) load_bias(t2, bias_a);
+#endif
 
   int buf = 0;
   // bias_nxt holds bias(t1); once scores(t1) has consumed it, it receives bias(t3)
-  auto step = [&](auto& sacc_cur, auto& sacc_nxt, auto& bias_nxt) {
+  auto step = [&](auto& sacc_cur, auto& sacc_nxt, auto& bias_nxt, auto& bias_cur) {
     const int t3 = next_tile(t2);
     const uint64_t bits = keep_lds[t0];
     const int b1 = buf == 2 ? 0 : buf + 1;
     const int b2 = b1 == 2 ? 0 : b1 + 1;
     if (t2 < ntiles) store_kv(b2, ku, vu);
     if (t3 < ntiles) load_kv(t3, ku, vu);
+#if OOPS_FWD_PIPE
     if (t1 < ntiles) scores(b1, bias_nxt, sacc_nxt);
     if constexpr (HAS_BIAS)
       if (t3 < ntiles) load_bias(t3, bias_nxt);
     attend(buf, bits, sacc_cur);
+#else
+    scores(buf, bias_cur, sacc_cur);
+    if constexpr (HAS_BIAS)
+      if (t2 < ntiles) load_bias(t2, bias_cur);
+    attend(buf, bits, sacc_cur);
+#endif
     lds_barrier();
     buf = b1;
     t0 = t1;
@@ -351,9 +331,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fast_kernel(FwdArgsT<T, T> a)
     t2 = t3;
   };
   while (t0 < ntiles) {
-    step(sacc_a, sacc_b, bias_b);
+    step(sacc_a, sacc_b, bias_b, bias_a);
     if (t0 >= ntiles) break;
-    step(sacc_b, sacc_a, bias_a);
+    step(sacc_b, sacc_a, bias_a, bias_b);
   }
 
   // ---- epilogue
@@ -366,13 +346,17 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fast_kernel(FwdArgsT<T, T> a)
 #pragma unroll
     for (int t = 0; t < NDT; ++t) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int d = t * 32 + kappa(g2, i);
+      for (int i = 0; i < 16; i += 4) {
+        const int d = t * 32 + kappa(g2, i);  // d .. d+3 contiguous; D % 8 == 0
         if (d < D) {
-          const float o = oacc[t][i] * inv;
-          const T hi = E::from_f(o);
-          orow[d] = hi;
-          if (lrow) lrow[d] = E::from_f(o - E::to_f(hi));
+          float o[4], r[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            o[e] = oacc[t][i + e] * inv;
+            r[e] = o[e] - E::to_f(E::from_f(o[e]));  // rounding residual of the output
+          }
+          store4<T>(orow, d, o[0], o[1], o[2], o[3]);
+          if (lrow) store4<T>(lrow, d, r[0], r[1], r[2], r[3]);
         }
       }
     }

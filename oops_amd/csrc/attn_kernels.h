@@ -46,12 +46,14 @@ struct BwdArgsT {
   float* dbias_part;   // [parts][dbias_extent] partial slabs (shared-bias mode)
   const int64_t* table;
   int64_t uniform_tiles;
+  int64_t total_tiles;  // logical tiles of the launch (fast paths; grid padded to 8)
   int64_t dbias_extent;
   int num_samples;
   int num_heads;
   int head_size;
   int vec_ok;
   int parts;
+  int head_group;
   float scale;
 };
 
@@ -131,6 +133,51 @@ bool launch_forward_fast(const oops_attn_geometry& geo, const Plan& plan, const 
 hipError_t launch_forward(const oops_attn_geometry& geo, const Plan& plan, const void* q, const void* k,
                           const void* v, const uint8_t* mask, const void* bias, void* out, void* out_lo,
                           float* lse, hipStream_t stream);
+
+// Device pointers of one backward call.
+struct BwdLaunch {
+  const void *q, *k, *v, *out, *out_lo, *dout, *bias;
+  const uint8_t* mask;
+  const float* lse;
+  float* delta;
+  void *dq, *dk, *dv;
+  float *dbias, *dbias_part;
+};
+
+int head_group_of(const oops_attn_geometry& geo);
+
+template <typename T, typename BT>
+inline void fill_bwd_args(BwdArgsT<T, BT>& a, const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L) {
+  a.q = static_cast<const T*>(L.q);
+  a.k = static_cast<const T*>(L.k);
+  a.v = static_cast<const T*>(L.v);
+  a.out = static_cast<const T*>(L.out);
+  a.out_lo = static_cast<const T*>(L.out_lo);
+  a.dout = static_cast<const T*>(L.dout);
+  a.bias = geo.has_bias ? static_cast<const BT*>(L.bias) : nullptr;
+  a.mask = geo.has_mask ? L.mask : nullptr;
+  a.lse = L.lse;
+  a.delta = L.delta;
+  a.dq = static_cast<T*>(L.dq);
+  a.dk = static_cast<T*>(L.dk);
+  a.dv = static_cast<T*>(L.dv);
+  a.dbias = geo.has_bias ? L.dbias : nullptr;
+  a.dbias_part = L.dbias_part;
+  a.table = geo.table_device;
+  a.uniform_tiles = 0;
+  a.total_tiles = 0;
+  a.dbias_extent = plan.dbias_extent;
+  a.num_samples = geo.num_samples;
+  a.num_heads = geo.num_heads;
+  a.head_size = geo.head_size;
+  a.vec_ok = geo.vec_ok;
+  a.parts = plan.parts;
+  a.head_group = head_group_of(geo);
+  a.scale = geo.scale;
+}
+
+bool backward_fast_ok(const oops_attn_geometry& geo, const Plan& plan);
+hipError_t launch_dkv_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L, hipStream_t stream);
 
 hipError_t launch_backward(const oops_attn_geometry& geo, const Plan& plan, const void* q, const void* k,
                            const void* v, const uint8_t* mask, const void* bias, const void* out,
