@@ -748,9 +748,13 @@ hipError_t launch_backward(const oops_attn_geometry& geo, const Plan& plan, cons
     }
     const bool need_dq = dq != nullptr || (a.dbias != nullptr && plan.any_full);
     if ((phases & OOPS_PHASE_DQ) && need_dq && plan.fwd_tiles > 0) {
-      a.uniform_tiles = plan.fwd_uniform;
-      hipLaunchKernelGGL((attn_dq_kernel<T, BT, DP>), dim3((unsigned)plan.fwd_tiles), block, 0, stream, a);
-      check();
+      if (fast) {
+        if (err == hipSuccess) err = launch_dq_fast(geo, plan, L, stream);
+      } else {
+        a.uniform_tiles = plan.fwd_uniform;
+        hipLaunchKernelGGL((attn_dq_kernel<T, BT, DP>), dim3((unsigned)plan.fwd_tiles), block, 0, stream, a);
+        check();
+      }
     }
     if ((phases & OOPS_PHASE_DKV) && (dk != nullptr || dv != nullptr) && plan.dkv_tiles > 0) {
       if (fast) {
@@ -762,11 +766,16 @@ hipError_t launch_backward(const oops_attn_geometry& geo, const Plan& plan, cons
       }
     }
     if ((phases & OOPS_PHASE_DBIAS) && a.dbias != nullptr && plan.any_shared && plan.sbias_tiles > 0) {
-      a.uniform_tiles = plan.sbias_uniform;
-      hipLaunchKernelGGL((attn_dbias_shared_kernel<T, BT, DP>), dim3((unsigned)plan.sbias_tiles), block, 0,
-                         stream, a);
-      check();
-      if (plan.parts > 1) {
+      if (fast) {
+        if (err == hipSuccess) err = launch_dbias_fast(geo, plan, L, stream);
+        a.parts = plan.fast_parts;
+      } else {
+        a.uniform_tiles = plan.sbias_uniform;
+        hipLaunchKernelGGL((attn_dbias_shared_kernel<T, BT, DP>), dim3((unsigned)plan.sbias_tiles), block, 0,
+                           stream, a);
+        check();
+      }
+      if (a.parts > 1) {
         a.uniform_tiles = plan.sred_uniform;
         hipLaunchKernelGGL((attn_dbias_reduce_kernel<T, BT, DP>), dim3((unsigned)plan.sred_tiles), block, 0,
                            stream, a);

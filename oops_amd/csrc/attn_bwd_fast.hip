@@ -260,9 +260,487 @@ __global__ __launch_bounds__(256, 2) void attn_dkv_fast_kernel(BwdArgsT<T, T> a)
   }
 }
 
+// attn_dq_fast_kernel: one workgroup = 4 wavefronts x 32 queries of one
+// (sample, group, head), the query as MFMA column (as in the forward).  Per
+// 64-key step: S^T = bias (identity MFMA) + K Q^T, dP^T = V dO^T - delta
+// (-delta is a constant accumulator input), P = exp2(S * scale * log2 e -
+// LSE), dS = P dP, dQ^T += K^T dS^T (K^T by LDS transpose reads).  A
+// per-group ("full") bias gets dBias = dS written from registers.
+// Reference: _backward_query (oops/attention/triangle/triton/kernel.py:428-565).
+template <typename T, int DP, bool HAS_BIAS>
+__global__ __launch_bounds__(256, 2) void attn_dq_fast_kernel(BwdArgsT<T, T> a) {
+  using E = Elem<T>;
+  using Frag = typename E::Frag;
+  constexpr int LD = DP + 8;
+  constexpr int TBUF = 64 * LD;
+  constexpr int NDT = DP / 32;
+  constexpr int NQF = DP / 16;
+  constexpr int NCH = DP / 32;
+
+  __shared__ __attribute__((aligned(16))) T k_lds[3 * TBUF];
+  __shared__ __attribute__((aligned(16))) T v_lds[3 * TBUF];
+  __shared__ uint64_t keep_lds[kMaxKeyTiles];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int lq = lane & 31;
+  const int g2 = lane >> 5;
+
+  int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
+  if (tile >= a.total_tiles) return;
+  const Sample* tab = reinterpret_cast<const Sample*>(a.table);
+  const int H = a.num_heads;
+  const int s_idx = find_sample(tile, tab, a.num_samples, a.uniform_tiles,
+                                [&](const Sample& s) { return s.G * H * cdiv(s.Lq, 128); });
+  if (s_idx < 0) return;
+  const Sample& S = tab[__builtin_amdgcn_readfirstlane(s_idx)];
+  const int64_t G = S.G;
+  const int Lq = (int)S.Lq, Lk = (int)S.Lk;
+  const int nqb = (int)cdiv(Lq, 128);
+  const int HG = a.head_group;
+  const int qb = (int)(tile % nqb);
+  int64_t rest = tile / nqb;
+  const int hh = (int)(rest % HG);
+  rest /= HG;
+  const int g = (int)(rest % G);
+  const int h = (int)(rest / G) * HG + hh;
+  const int D = a.head_size;
+  const int ntiles = (Lk + 63) >> 6;
+  const int k_si = (int)S.k_si, v_si = (int)S.v_si, b_si = (int)S.b_si;
+  const bool has_mask = a.mask != nullptr && S.m_off >= 0;
+  const uint8_t* mbase = has_mask ? a.mask + S.m_off + g * S.m_sg : nullptr;
+  const bool write_dbias = a.dbias != nullptr && S.bias_mode == OOPS_BIAS_FULL;
+
+  for (int t = wave; t < ntiles; t += 4) {
+    const int key = t * 64 + lane;
+    bool keep = key < Lk;
+    if (keep && has_mask) keep = mbase[key] != 0;
+    const uint64_t bits = __ballot(keep);
+    if (lane == 0) keep_lds[t] = bits;
+  }
+
+  const int q_lane = qb * 128 + wave * 32 + lq;
+  const bool qv = q_lane < Lq;
+  Frag qf[NQF], df[NQF];
+  {
+    const T* qrow = a.q + S.q_off + g * S.q_sg + h * S.q_sh + (int64_t)q_lane * S.q_si;
+    const T* drow = a.dout + S.do_off + g * S.do_sg + h * S.do_sh + (int64_t)q_lane * S.do_si;
+#pragma unroll
+    for (int s = 0; s < NQF; ++s) {
+      const int col = s * 16 + g2 * 8;
+      const bool ok = qv && col < D;
+      qf[s] = __builtin_bit_cast(Frag, ok ? *reinterpret_cast<const uint4*>(qrow + col) : make_uint4(0, 0, 0, 0));
+      df[s] = __builtin_bit_cast(Frag, ok ? *reinterpret_cast<const uint4*>(drow + col) : make_uint4(0, 0, 0, 0));
+    }
+  }
+  const int64_t lidx = S.l_off + ((int64_t)g * H + h) * Lq + q_lane;
+  const float neg_lse = qv ? -a.lse[lidx] : 0.0f;
+  f32x16 ndelta;
+  {
+    const float nd = qv ? -a.delta[lidx] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) ndelta[j] = nd;
+  }
+  Frag ident[2];
+  identity_frags<T>(ident, 1.0f / a.scale, lane);
+
+  const T* kbase = a.k + S.k_off + g * S.k_sg + h * S.k_sh;
+  const T* vbase = a.v + S.v_off + g * S.v_sg + h * S.v_sh;
+  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kbase, (uint32_t)(((int64_t)(Lk - 1) * k_si + D) * 2));
+  const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vbase, (uint32_t)(((int64_t)(Lk - 1) * v_si + D) * 2));
+  uint32_t kv_row[NCH], k_off[NCH], v_off[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int c = tid + 256 * i;
+    const int r = c / (DP / 8);
+    const int col = (c % (DP / 8)) * 8;
+    kv_row[i] = r;
+    k_off[i] = col < D ? (uint32_t)((r * k_si + col) * 2) : kOut;
+    v_off[i] = col < D ? (uint32_t)((r * v_si + col) * 2) : kOut;
+  }
+  const T* bbase = HAS_BIAS ? a.bias + S.b_off + g * S.b_sg + h * S.b_sh : a.q;
+  const __amdgpu_buffer_rsrc_t b_rsrc =
+      make_rsrc(bbase, HAS_BIAS ? (uint32_t)(((int64_t)(Lq - 1) * b_si + Lk) * 2) : 0u);
+  uint32_t b_off[2][2];
+#pragma unroll
+  for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+      b_off[t2][c] = qv ? (uint32_t)((q_lane * b_si + 32 * t2 + 16 * c + g2 * 8) * 2) : kOut;
+  float* dbrow = write_dbias && qv ? a.dbias + S.db_off + g * S.db_sg + h * S.db_sh + (int64_t)q_lane * S.db_si
+                                   : nullptr;
+
+  auto load_kv = [&](int t, uint4 (&ku)[NCH], uint4 (&vu)[NCH]) {
+    const uint64_t bits = keep_lds[t];
+    const uint32_t ks = (uint32_t)(t * 64 * k_si * 2), vs = (uint32_t)(t * 64 * v_si * 2);
+    const bool full = bits == ~uint64_t(0);
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const bool ok = full || ((bits >> kv_row[i]) & 1);
+      ku[i] = buffer_load16_s(k_rsrc, ok ? k_off[i] : kOut, ks);
+      vu[i] = buffer_load16_s(v_rsrc, ok ? v_off[i] : kOut, vs);
+    }
+  };
+  auto store_kv = [&](int buf, const uint4 (&ku)[NCH], const uint4 (&vu)[NCH]) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int c = tid + 256 * i;
+      const int r = c / (DP / 8);
+      const int col = (c % (DP / 8)) * 8;
+      *reinterpret_cast<uint4*>(&k_lds[buf * TBUF + r * LD + col]) = ku[i];
+      *reinterpret_cast<uint4*>(&v_lds[buf * TBUF + r * LD + col]) = vu[i];
+    }
+  };
+  auto load_bias = [&](int t, uint4 (&bf)[2][2]) {
+    const uint32_t s = (uint32_t)(t * 64 * 2);
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) bf[t2][c] = buffer_load16_s(b_rsrc, b_off[t2][c] + s, 0);
+  };
+
+  __syncthreads();
+  auto next_tile = [&](int t) {
+    if (t >= ntiles) return ntiles;
+    ++t;
+    while (t < ntiles && keep_lds[t] == 0) ++t;
+    return t;
+  };
+
+  const float c1 = a.scale * kLog2e;
+  f32x16 acc[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) acc[t] = f32x16{};
+
+  auto compute = [&](int buf, int t, uint64_t bits, const uint4 (&bf)[2][2]) {
+    const T* kt = &k_lds[buf * TBUF];
+    const T* vt = &v_lds[buf * TBUF];
+    const uint64_t lb = bits >> (g2 * 4);
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) {
+      f32x16 sacc;
+      if constexpr (HAS_BIAS) {
+        sacc = E::mma(ident[0], __builtin_bit_cast(Frag, bf[t2][0]), f32x16{});
+        sacc = E::mma(ident[1], __builtin_bit_cast(Frag, bf[t2][1]), sacc);
+      } else {
+        sacc = f32x16{};
+      }
+      f32x16 pacc = ndelta;
+#pragma unroll
+      for (int s = 0; s < NQF; ++s) {
+        sacc = E::mma(lds_frag<T>(kt + (32 * t2 + lq) * LD + s * 16 + g2 * 8), qf[s], sacc);
+        pacc = E::mma(lds_frag<T>(vt + (32 * t2 + lq) * LD + s * 16 + g2 * 8), df[s], pacc);
+      }
+      float ds[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j], c1, neg_lse));
+        if (bits != ~uint64_t(0)) {
+          const int kk = 32 * t2 + ((j >> 2) << 3) + (j & 3);
+          p = ((lb >> kk) & 1) ? p : 0.0f;
+        }
+        ds[j] = p * pacc[j];
+      }
+      if (dbrow) {
+        const int k0 = t * 64 + 32 * t2;
+#pragma unroll
+        for (int j = 0; j < 16; j += 4) {
+          const int key = k0 + kappa(g2, j);
+          if (key + 3 < Lk) {
+            *reinterpret_cast<float4*>(dbrow + key) = make_float4(ds[j], ds[j + 1], ds[j + 2], ds[j + 3]);
+          } else {
+            for (int e = 0; e < 4; ++e)
+              if (key + e < Lk) dbrow[key + e] = ds[j + e];
+          }
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const Frag sf = pack8<T>(&ds[8 * m]);
+#pragma unroll
+        for (int d = 0; d < NDT; ++d)
+          acc[d] = E::mma(lds_read_tr_frag<T>(kt, LD, 32 * t2 + 16 * m, 32 * d, lane), sf, acc[d]);
+      }
+    }
+  };
+
+  uint4 ku[NCH], vu[NCH];
+  uint4 bias_a[2][2], bias_b[2][2];
+  int t0 = next_tile(-1);
+  int t1 = next_tile(t0);
+  int t2 = next_tile(t1);
+  if (t0 < ntiles) {
+    load_kv(t0, ku, vu);
+    if constexpr (HAS_BIAS) load_bias(t0, bias_a);
+    store_kv(0, ku, vu);
+  }
+  if (t1 < ntiles) {
+    load_kv(t1, ku, vu);
+    if constexpr (HAS_BIAS) load_bias(t1, bias_b);
+    store_kv(1, ku, vu);
+  }
+  if (t2 < ntiles) load_kv(t2, ku, vu);
+  vmem_wait_all();
+  __syncthreads();
+  int buf = 0;
+  auto step = [&](uint4 (&bias_cur)[2][2]) {
+    const int t3 = next_tile(t2);
+    const uint64_t bits = keep_lds[t0];
+    const int b1 = buf == 2 ? 0 : buf + 1;
+    const int b2 = b1 == 2 ? 0 : b1 + 1;
+    if (t2 < ntiles) store_kv(b2, ku, vu);
+    if (t3 < ntiles) load_kv(t3, ku, vu);
+    compute(buf, t0, bits, bias_cur);
+    if constexpr (HAS_BIAS)
+      if (t2 < ntiles) load_bias(t2, bias_cur);
+    lds_barrier();
+    buf = b1;
+    t0 = t1;
+    t1 = t2;
+    t2 = t3;
+  };
+  while (t0 < ntiles) {
+    step(bias_a);
+    if (t0 >= ntiles) break;
+    step(bias_b);
+  }
+
+  if (qv && a.dq != nullptr) {
+    T* row = a.dq + S.q_off + g * S.q_sg + h * S.q_sh + (int64_t)q_lane * S.q_si;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int i = 0; i < 16; i += 4) {
+        const int d = t * 32 + kappa(g2, i);
+        if (d < D)
+          store4<T>(row, d, acc[t][i] * a.scale, acc[t][i + 1] * a.scale, acc[t][i + 2] * a.scale,
+                    acc[t][i + 3] * a.scale);
+      }
+  }
+}
+
+// attn_dbias_fast_kernel: dBias[h, q, k] = sum over groups g of dS for a
+// bias shared by all groups.  One workgroup = 4 waves x 32 queries and 64
+// keys of one head, walking the groups g of one part.  The bias block's MFMA
+// contribution is computed once and is the accumulator input of every
+// group's S^T; K/V tiles of each group go through a 3-buffer LDS ring; the
+// dS block accumulates in registers (no atomics).  Partial sums per part are
+// added by attn_dbias_reduce_kernel.
+// Reference: _backward_shared_bias (oops/attention/triangle/triton/kernel.py:721-873).
+template <typename T, int DP>
+__global__ __launch_bounds__(256, 2) void attn_dbias_fast_kernel(BwdArgsT<T, T> a) {
+  using E = Elem<T>;
+  using Frag = typename E::Frag;
+  constexpr int LD = DP + 8;
+  constexpr int TBUF = 64 * LD;
+  constexpr int NQF = DP / 16;
+  constexpr int NCH = DP / 32;
+
+  __shared__ __attribute__((aligned(16))) T k_lds[3 * TBUF];
+  __shared__ __attribute__((aligned(16))) T v_lds[3 * TBUF];
+  __shared__ uint64_t keep_lds[3];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int lq = lane & 31;
+  const int g2 = lane >> 5;
+  const int P = a.parts;
+
+  int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
+  if (tile >= a.total_tiles) return;
+  const Sample* tab = reinterpret_cast<const Sample*>(a.table);
+  const int H = a.num_heads;
+  const int s_idx = find_sample(tile, tab, a.num_samples, a.uniform_tiles, [&](const Sample& s) {
+    return s.bias_mode == OOPS_BIAS_SHARED ? H * cdiv(s.Lq, 128) * cdiv(s.Lk, 64) * P : (int64_t)0;
+  });
+  if (s_idx < 0) return;
+  const Sample& S = tab[__builtin_amdgcn_readfirstlane(s_idx)];
+  const int64_t G = S.G;
+  const int Lq = (int)S.Lq, Lk = (int)S.Lk;
+  const int nkb = (int)cdiv(Lk, 64);
+  const int nqb = (int)cdiv(Lq, 128);
+  // logical order (head, part, q block, key block): neighbours share the bias block rows
+  const int kb = (int)(tile % nkb);
+  int64_t rest = tile / nkb;
+  const int qb = (int)(rest % nqb);
+  rest /= nqb;
+  const int part = (int)(rest % P);
+  const int h = (int)(rest / P);
+  const int64_t g_begin = G * part / P, g_end = G * (part + 1) / P;
+  const int D = a.head_size;
+  const int k0 = kb * 64;
+  const int k_si = (int)S.k_si, v_si = (int)S.v_si;
+  const bool has_mask = a.mask != nullptr && S.m_off >= 0;
+
+  const int q_lane = qb * 128 + wave * 32 + lq;
+  const bool qv = q_lane < Lq;
+  const float c1 = a.scale * kLog2e;
+
+  // bias contribution of this (query, key) block, shared by every group
+  f32x16 bacc[2];
+  {
+    Frag ident[2];
+    identity_frags<T>(ident, 1.0f / a.scale, lane);
+    const T* brow = a.bias + S.b_off + h * S.b_sh + (int64_t)q_lane * S.b_si;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) {
+      bacc[t2] = f32x16{};
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int key = k0 + 32 * t2 + 16 * c + g2 * 8;
+        uint4 u = make_uint4(0, 0, 0, 0);
+        if (qv) {
+          if (key + 8 <= Lk) u = *reinterpret_cast<const uint4*>(brow + key);
+          else u = load16(brow, key, Lk, false);
+        }
+        bacc[t2] = E::mma(ident[c], __builtin_bit_cast(Frag, u), bacc[t2]);
+      }
+    }
+  }
+  f32x16 acc[2];
+  acc[0] = acc[1] = f32x16{};
+
+  // per-group K/V tile of the block (64 keys), LDS ring like the other kernels
+  uint32_t kv_row[NCH], k_col[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int c = tid + 256 * i;
+    kv_row[i] = c / (DP / 8);
+    k_col[i] = (c % (DP / 8)) * 8;
+  }
+  struct Stage {
+    uint4 k[NCH], v[NCH];
+    uint64_t bits;
+  };
+  auto load_stage = [&](int64_t g, Stage& st) {
+    const T* kbase = a.k + S.k_off + g * S.k_sg + h * S.k_sh;
+    const T* vbase = a.v + S.v_off + g * S.v_sg + h * S.v_sh;
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(kbase, (uint32_t)(((int64_t)(Lk - 1) * k_si + D) * 2));
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(vbase, (uint32_t)(((int64_t)(Lk - 1) * v_si + D) * 2));
+    const int key = k0 + lane;
+    bool keep = key < Lk;
+    if (keep && has_mask) keep = a.mask[S.m_off + g * S.m_sg + key] != 0;
+    st.bits = __ballot(keep);
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const bool ok = ((st.bits >> kv_row[i]) & 1) && (int)k_col[i] < D;
+      const int kk = k0 + kv_row[i];
+      st.k[i] = buffer_load16(kr, ok ? (uint32_t)((kk * k_si + k_col[i]) * 2) : kOut);
+      st.v[i] = buffer_load16(vr, ok ? (uint32_t)((kk * v_si + k_col[i]) * 2) : kOut);
+    }
+  };
+  auto store_stage = [&](int buf, const Stage& st) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      *reinterpret_cast<uint4*>(&k_lds[buf * TBUF + kv_row[i] * LD + k_col[i]]) = st.k[i];
+      *reinterpret_cast<uint4*>(&v_lds[buf * TBUF + kv_row[i] * LD + k_col[i]]) = st.v[i];
+    }
+    if (tid == 0) keep_lds[buf] = st.bits;
+  };
+  // per-group query-side operands of this lane (registers)
+  struct QStage {
+    Frag q[NQF], d[NQF];
+    float nlse, ndlt;
+  };
+  auto load_q = [&](int64_t g, QStage& qs) {
+    const T* qrow = a.q + S.q_off + g * S.q_sg + h * S.q_sh + (int64_t)q_lane * S.q_si;
+    const T* drow = a.dout + S.do_off + g * S.do_sg + h * S.do_sh + (int64_t)q_lane * S.do_si;
+#pragma unroll
+    for (int s = 0; s < NQF; ++s) {
+      const int col = s * 16 + g2 * 8;
+      const bool ok = qv && col < D;
+      qs.q[s] = __builtin_bit_cast(Frag, ok ? *reinterpret_cast<const uint4*>(qrow + col) : make_uint4(0, 0, 0, 0));
+      qs.d[s] = __builtin_bit_cast(Frag, ok ? *reinterpret_cast<const uint4*>(drow + col) : make_uint4(0, 0, 0, 0));
+    }
+    const int64_t lidx = S.l_off + (g * H + h) * Lq + q_lane;
+    qs.nlse = qv ? -a.lse[lidx] : -__builtin_huge_valf();
+    qs.ndlt = qv ? -a.delta[lidx] : 0.0f;
+  };
+
+  const int64_t ng = g_end - g_begin;
+  Stage stg;
+  QStage qa, qb2;
+  if (ng > 0) {
+    load_stage(g_begin, stg);
+    store_stage(0, stg);
+    load_q(g_begin, qa);
+  }
+  if (ng > 1) {
+    load_stage(g_begin + 1, stg);
+    store_stage(1, stg);
+    load_q(g_begin + 1, qb2);
+  }
+  if (ng > 2) load_stage(g_begin + 2, stg);
+  vmem_wait_all();
+  __syncthreads();
+  int buf = 0;
+  auto step = [&](int64_t i, QStage& qc) {
+    const int b1 = buf == 2 ? 0 : buf + 1;
+    const int b2 = b1 == 2 ? 0 : b1 + 1;
+    if (i + 2 < ng) store_stage(b2, stg);
+    if (i + 3 < ng) load_stage(g_begin + i + 3, stg);
+    const T* kt = &k_lds[buf * TBUF];
+    const T* vt = &v_lds[buf * TBUF];
+    const uint64_t bits = keep_lds[buf];
+    const uint64_t lb = bits >> (g2 * 4);
+    f32x16 nd;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) nd[j] = qc.ndlt;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) {
+      f32x16 sacc = bacc[t2];
+      f32x16 pacc = nd;
+#pragma unroll
+      for (int s = 0; s < NQF; ++s) {
+        sacc = E::mma(lds_frag<T>(kt + (32 * t2 + lq) * LD + s * 16 + g2 * 8), qc.q[s], sacc);
+        pacc = E::mma(lds_frag<T>(vt + (32 * t2 + lq) * LD + s * 16 + g2 * 8), qc.d[s], pacc);
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j], c1, qc.nlse));
+        if (bits != ~uint64_t(0)) {
+          const int kk = 32 * t2 + ((j >> 2) << 3) + (j & 3);
+          p = ((lb >> kk) & 1) ? p : 0.0f;
+        }
+        acc[t2][j] = __builtin_fmaf(p, pacc[j], acc[t2][j]);
+      }
+    }
+    if (i + 2 < ng) load_q(g_begin + i + 2, qc);
+    lds_barrier();
+    buf = b1;
+  };
+  for (int64_t i = 0; i < ng; i += 2) {
+    step(i, qa);
+    if (i + 1 >= ng) break;
+    step(i + 1, qb2);
+  }
+
+  if (qv) {
+    float* dst = P == 1 ? a.dbias : a.dbias_part + (int64_t)part * a.dbias_extent;
+    float* row = dst + S.db_off + h * S.db_sh + (int64_t)q_lane * S.db_si;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+      for (int j = 0; j < 16; j += 4) {
+        const int key = k0 + 32 * t2 + kappa(g2, j);
+        if (key + 3 < Lk) {
+          *reinterpret_cast<float4*>(row + key) = make_float4(acc[t2][j], acc[t2][j + 1], acc[t2][j + 2], acc[t2][j + 3]);
+        } else {
+          for (int e = 0; e < 4; ++e)
+            if (key + e < Lk) row[key + e] = acc[t2][j + e];
+        }
+      }
+  }
+}
+
 #define OOPS_BWD_FAST_INST(T, DP)                                                \
   template __global__ void attn_dkv_fast_kernel<T, DP, true>(BwdArgsT<T, T>);  \
-  template __global__ void attn_dkv_fast_kernel<T, DP, false>(BwdArgsT<T, T>);
+  template __global__ void attn_dkv_fast_kernel<T, DP, false>(BwdArgsT<T, T>); \
+  template __global__ void attn_dq_fast_kernel<T, DP, true>(BwdArgsT<T, T>);   \
+  template __global__ void attn_dq_fast_kernel<T, DP, false>(BwdArgsT<T, T>);  \
+  template __global__ void attn_dbias_fast_kernel<T, DP>(BwdArgsT<T, T>);
 OOPS_BWD_FAST_INST(__bf16, 32)
 OOPS_BWD_FAST_INST(__bf16, 64)
 OOPS_BWD_FAST_INST(_Float16, 32)
@@ -276,9 +754,22 @@ bool backward_fast_ok(const oops_attn_geometry& geo, const Plan& plan) {
   return !(geo.has_bias && geo.bias_dtype != geo.dtype);
 }
 
-hipError_t launch_dkv_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L, hipStream_t stream) {
+template <typename F>
+hipError_t dispatch_fast(const oops_attn_geometry& geo, const Plan& plan, F&& f) {
   hipError_t err = hipSuccess;
-  auto go = [&](auto tag, auto dpc) {
+  auto go = [&](auto tag, auto dpc) { err = f(tag, dpc); };
+  if (geo.dtype == OOPS_BF16) {
+    if (plan.dp == 32) go(Tag<__bf16>{}, std::integral_constant<int, 32>{});
+    else go(Tag<__bf16>{}, std::integral_constant<int, 64>{});
+  } else {
+    if (plan.dp == 32) go(Tag<_Float16>{}, std::integral_constant<int, 32>{});
+    else go(Tag<_Float16>{}, std::integral_constant<int, 64>{});
+  }
+  return err;
+}
+
+hipError_t launch_dkv_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L, hipStream_t stream) {
+  return dispatch_fast(geo, plan, [&](auto tag, auto dpc) {
     using T = typename decltype(tag)::type;
     constexpr int DP = decltype(dpc)::value;
     BwdArgsT<T, T> a;
@@ -290,16 +781,41 @@ hipError_t launch_dkv_fast(const oops_attn_geometry& geo, const Plan& plan, cons
       hipLaunchKernelGGL((attn_dkv_fast_kernel<T, DP, true>), grid, dim3(256), 0, stream, a);
     else
       hipLaunchKernelGGL((attn_dkv_fast_kernel<T, DP, false>), grid, dim3(256), 0, stream, a);
-    err = hipGetLastError();
-  };
-  if (geo.dtype == OOPS_BF16) {
-    if (plan.dp == 32) go(Tag<__bf16>{}, std::integral_constant<int, 32>{});
-    else go(Tag<__bf16>{}, std::integral_constant<int, 64>{});
-  } else {
-    if (plan.dp == 32) go(Tag<_Float16>{}, std::integral_constant<int, 32>{});
-    else go(Tag<_Float16>{}, std::integral_constant<int, 64>{});
-  }
-  return err;
+    return hipGetLastError();
+  });
+}
+
+hipError_t launch_dq_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L, hipStream_t stream) {
+  return dispatch_fast(geo, plan, [&](auto tag, auto dpc) {
+    using T = typename decltype(tag)::type;
+    constexpr int DP = decltype(dpc)::value;
+    BwdArgsT<T, T> a;
+    fill_bwd_args(a, geo, plan, L);
+    a.uniform_tiles = plan.fwd_uniform;
+    a.total_tiles = plan.fwd_tiles;
+    const dim3 grid((unsigned)xcd_grid(plan.fwd_tiles));
+    if (a.bias != nullptr)
+      hipLaunchKernelGGL((attn_dq_fast_kernel<T, DP, true>), grid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((attn_dq_fast_kernel<T, DP, false>), grid, dim3(256), 0, stream, a);
+    return hipGetLastError();
+  });
+}
+
+hipError_t launch_dbias_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L,
+                             hipStream_t stream) {
+  return dispatch_fast(geo, plan, [&](auto tag, auto dpc) {
+    using T = typename decltype(tag)::type;
+    constexpr int DP = decltype(dpc)::value;
+    BwdArgsT<T, T> a;
+    fill_bwd_args(a, geo, plan, L);
+    a.parts = plan.fast_parts;
+    a.uniform_tiles = plan.fast_sbias_uniform;
+    a.total_tiles = plan.fast_sbias_tiles;
+    hipLaunchKernelGGL((attn_dbias_fast_kernel<T, DP>), dim3((unsigned)xcd_grid(plan.fast_sbias_tiles)), dim3(256),
+                       0, stream, a);
+    return hipGetLastError();
+  });
 }
 
 }  // namespace oops

@@ -118,7 +118,9 @@ struct Plan {
   int64_t sred_tiles = 0, sred_uniform = 0;      // shared dBias reduction blocks
   int64_t lse_extent = 0;                        // floats
   int64_t dbias_extent = 0;                      // floats
-  int parts = 1;
+  int parts = 1;                                 // group ranges of the shared dBias reduction
+  int64_t fast_sbias_tiles = 0, fast_sbias_uniform = 0;  // same, 64-key blocks (fast path)
+  int fast_parts = 1;
   bool any_full = false, any_shared = false;
   bool any_pair_mask = false;                    // a mask that depends on the query
   bool offsets_32bit = true;                     // every per-(group, head) K/V/bias block < 2 GiB
@@ -178,6 +180,9 @@ inline void fill_bwd_args(BwdArgsT<T, BT>& a, const oops_attn_geometry& geo, con
 
 bool backward_fast_ok(const oops_attn_geometry& geo, const Plan& plan);
 hipError_t launch_dkv_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L, hipStream_t stream);
+hipError_t launch_dq_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L, hipStream_t stream);
+hipError_t launch_dbias_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L,
+                             hipStream_t stream);
 
 hipError_t launch_backward(const oops_attn_geometry& geo, const Plan& plan, const void* q, const void* k,
                            const void* v, const uint8_t* mask, const void* bias, const void* out,

@@ -58,7 +58,8 @@ int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
   const Sample* tab = reinterpret_cast<const Sample*>(geo->table_host);
   int64_t c_fwd = -1, c_delta = -1, c_dkv = -1, c_sb = -1;
   bool u_fwd = true, u_delta = true, u_dkv = true, u_sb = true;
-  int64_t min_shared_groups = INT64_MAX, sbias_base = 0;
+  int64_t min_shared_groups = INT64_MAX, sbias_base = 0, sbias_base64 = 0, c_sb64 = -1;
+  bool u_sb64 = true;
   auto track = [](int64_t c, int64_t& first, bool& uniform) {
     if (first < 0) first = c;
     else if (first != c) uniform = false;
@@ -86,6 +87,9 @@ int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
     plan.delta_tiles += c2;
     plan.dkv_tiles += c3;
     sbias_base += cs;
+    const int64_t cs64 = S.bias_mode == OOPS_BIAS_SHARED ? H * cdiv(S.Lq, 128) * cdiv(S.Lk, 64) : 0;
+    sbias_base64 += cs64;
+    track(cs64, c_sb64, u_sb64);
     track(c1, c_fwd, u_fwd);
     track(c2, c_delta, u_delta);
     track(c3, c_dkv, u_dkv);
@@ -125,6 +129,11 @@ int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
     plan.parts = (int)std::max<int64_t>(parts, 1);
     plan.sbias_tiles = sbias_base * plan.parts;
     plan.sbias_uniform = u_sb && c_sb > 0 ? c_sb * plan.parts : 0;
+    int64_t fparts = cdiv(kTargetSharedBiasBlocks, std::max<int64_t>(sbias_base64, 1));
+    fparts = std::min<int64_t>({fparts, kMaxParts, min_shared_groups});
+    plan.fast_parts = (int)std::max<int64_t>(fparts, 1);
+    plan.fast_sbias_tiles = sbias_base64 * plan.fast_parts;
+    plan.fast_sbias_uniform = u_sb64 && c_sb64 > 0 ? c_sb64 * plan.fast_parts : 0;
     int64_t c_red = -1;
     bool u_red = true;
     for (int s = 0; s < geo->num_samples; ++s) {
@@ -144,7 +153,8 @@ size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
 size_t workspace_bytes(const oops::Plan& plan) {
   size_t bytes = align256(sizeof(float) * (size_t)plan.lse_extent);
-  if (plan.any_shared && plan.parts > 1) bytes += align256(sizeof(float) * (size_t)plan.parts * plan.dbias_extent);
+  const int parts = std::max(plan.parts, plan.fast_parts);
+  if (plan.any_shared && parts > 1) bytes += align256(sizeof(float) * (size_t)parts * plan.dbias_extent);
   return bytes;
 }
 
@@ -196,7 +206,7 @@ int oops_attn_backward(const oops_attn_geometry* geo, const void* q, const void*
                 (long long)(workspace ? ws_bytes : 0));
   if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return fail(OOPS_EWORKSPACE, "workspace must be 256-byte aligned");
   float* delta = static_cast<float*>(workspace);
-  float* parts = plan.any_shared && plan.parts > 1
+  float* parts = plan.any_shared && std::max(plan.parts, plan.fast_parts) > 1
                      ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
                                                 align256(sizeof(float) * (size_t)plan.lse_extent))
                      : nullptr;
