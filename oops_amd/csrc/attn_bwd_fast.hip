@@ -107,8 +107,11 @@ __global__ __launch_bounds__(256, 2) void attn_dkv_fast_kernel(BwdArgsT<T, T> a)
     q_off[i] = col < D ? (uint32_t)((r * q_si + col) * 2) : kOut;
     do_off[i] = col < D ? (uint32_t)((r * do_si + col) * 2) : kOut;
   }
-  const float* lse_row = a.lse + S.l_off + ((int64_t)g * H + h) * Lq;
-  const float* dlt_row = a.delta + S.l_off + ((int64_t)g * H + h) * Lq;
+  // LSE / delta rows: rows past Lq read 0; they contribute nothing because
+  // their dO (and Q) rows read as zero, so dS = P * (0 - 0) = 0
+  const __amdgpu_buffer_rsrc_t l_rsrc = make_rsrc(a.lse + S.l_off + ((int64_t)g * H + h) * Lq, (uint32_t)(Lq * 4));
+  const __amdgpu_buffer_rsrc_t d_rsrc =
+      make_rsrc(a.delta + S.l_off + ((int64_t)g * H + h) * Lq, (uint32_t)(Lq * 4));
   // bias rows of this wave's keys: A fragments (lane = query, 8 consecutive keys)
   const T* bbase = HAS_BIAS ? a.bias + S.b_off + g * S.b_sg + h * S.b_sh : a.q;
   const __amdgpu_buffer_rsrc_t b_rsrc =
@@ -129,10 +132,9 @@ __global__ __launch_bounds__(256, 2) void attn_dkv_fast_kernel(BwdArgsT<T, T> a)
       st.d[i] = buffer_load16_s(do_rsrc, ok ? do_off[i] : kOut, ds);
     }
     if (tid < 64) {
-      const int q = q0 + tid;
-      // rows past Lq: P = exp2(x - inf) = 0 and delta = 0
-      st.lse = q < Lq ? lse_row[q] : __builtin_huge_valf();
-      st.dlt = q < Lq ? dlt_row[q] : 0.0f;
+      const uint32_t off = (uint32_t)((q0 + tid) * 4);  // range-checked: rows past Lq read 0
+      st.lse = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(l_rsrc, off, 0, 0));
+      st.dlt = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(d_rsrc, off, 0, 0));
     }
   };
   auto store_stage = [&](int buf, const Stage& st) {
@@ -220,7 +222,7 @@ __global__ __launch_bounds__(256, 2) void attn_dkv_fast_kernel(BwdArgsT<T, T> a)
     if constexpr (HAS_BIAS) load_bias(1, bias_b);
     store_stage(1, stg);
   }
-  if (nsteps > 2) load_stage(2, stg);
+  load_stage(2, stg);
   vmem_wait_all();
   __syncthreads();
   int buf = 0;
@@ -228,10 +230,10 @@ __global__ __launch_bounds__(256, 2) void attn_dkv_fast_kernel(BwdArgsT<T, T> a)
     const int b1 = buf == 2 ? 0 : buf + 1;
     const int b2 = b1 == 2 ? 0 : b1 + 1;
     if (i + 2 < nsteps) store_stage(b2, stg);
-    if (i + 3 < nsteps) load_stage(i + 3, stg);
+    load_stage(i + 3, stg);
     compute(buf, i * 64, bias_cur);
     if constexpr (HAS_BIAS)
-      if (i + 2 < nsteps) load_bias(i + 2, bias_cur);
+      load_bias(i + 2, bias_cur);
     lds_barrier();
     buf = b1;
   };
@@ -371,8 +373,11 @@ __global__ __launch_bounds__(256, 2) void attn_dq_fast_kernel(BwdArgsT<T, T> a) 
   float* dbrow = write_dbias && qv ? a.dbias + S.db_off + g * S.db_sg + h * S.db_sh + (int64_t)q_lane * S.db_si
                                    : nullptr;
 
+  // An absent tile (t >= ntiles) issues its loads with out-of-range offsets:
+  // no memory traffic, and no branch, so the compiler can count outstanding
+  // loads exactly and never has to wait for all of them.
   auto load_kv = [&](int t, uint4 (&ku)[NCH], uint4 (&vu)[NCH]) {
-    const uint64_t bits = keep_lds[t];
+    const uint64_t bits = t < ntiles ? keep_lds[t < ntiles ? t : 0] : 0;
     const uint32_t ks = (uint32_t)(t * 64 * k_si * 2), vs = (uint32_t)(t * 64 * v_si * 2);
     const bool full = bits == ~uint64_t(0);
 #pragma unroll
@@ -397,7 +402,7 @@ __global__ __launch_bounds__(256, 2) void attn_dq_fast_kernel(BwdArgsT<T, T> a) 
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
-      for (int c = 0; c < 2; ++c) bf[t2][c] = buffer_load16_s(b_rsrc, b_off[t2][c] + s, 0);
+      for (int c = 0; c < 2; ++c) bf[t2][c] = buffer_load16_s(b_rsrc, t < ntiles ? b_off[t2][c] + s : kOut, 0);
   };
 
   __syncthreads();
@@ -480,7 +485,7 @@ __global__ __launch_bounds__(256, 2) void attn_dq_fast_kernel(BwdArgsT<T, T> a) 
     if constexpr (HAS_BIAS) load_bias(t1, bias_b);
     store_kv(1, ku, vu);
   }
-  if (t2 < ntiles) load_kv(t2, ku, vu);
+  load_kv(t2, ku, vu);
   vmem_wait_all();
   __syncthreads();
   int buf = 0;
@@ -490,10 +495,10 @@ __global__ __launch_bounds__(256, 2) void attn_dq_fast_kernel(BwdArgsT<T, T> a) 
     const int b1 = buf == 2 ? 0 : buf + 1;
     const int b2 = b1 == 2 ? 0 : b1 + 1;
     if (t2 < ntiles) store_kv(b2, ku, vu);
-    if (t3 < ntiles) load_kv(t3, ku, vu);
+    load_kv(t3, ku, vu);
     compute(buf, t0, bits, bias_cur);
     if constexpr (HAS_BIAS)
-      if (t2 < ntiles) load_bias(t2, bias_cur);
+      load_bias(t2, bias_cur);
     lds_barrier();
     buf = b1;
     t0 = t1;
@@ -614,14 +619,32 @@ __global__ __launch_bounds__(256, 2) void attn_dbias_fast_kernel(BwdArgsT<T, T> 
     uint4 k[NCH], v[NCH];
     uint64_t bits;
   };
+  // row-invariant bases: group g adds g * (group stride)
+  const T* k_h = a.k + S.k_off + h * S.k_sh;
+  const T* v_h = a.v + S.v_off + h * S.v_sh;
+  // (buffer resources must be wave-uniform: lane-dependent parts go in the offsets)
+  const T* q_h = a.q + S.q_off + h * S.q_sh;
+  const T* do_h = a.dout + S.do_off + h * S.do_sh;
+  const uint32_t q_bytes_all = (uint32_t)(((int64_t)(Lq - 1) * S.q_si + D) * 2);
+  const uint32_t do_bytes_all = (uint32_t)(((int64_t)(Lq - 1) * S.do_si + D) * 2);
+  const uint32_t q_lane_off = (uint32_t)(q_lane * (int)S.q_si * 2);
+  const uint32_t do_lane_off = (uint32_t)(q_lane * (int)S.do_si * 2);
+  const int64_t k_sg = S.k_sg, v_sg = S.v_sg, q_sg = S.q_sg, do_sg = S.do_sg;
+  const float* l_h = a.lse + S.l_off + (int64_t)h * Lq;
+  const float* d_h = a.delta + S.l_off + (int64_t)h * Lq;
+  const int64_t l_sg = (int64_t)H * Lq;
+  const uint8_t* m_h = has_mask ? a.mask + S.m_off : nullptr;
+  const int64_t m_sg = S.m_sg;
+  const uint32_t kv_bytes_k = (uint32_t)(((int64_t)(Lk - 1) * k_si + D) * 2);
+  const uint32_t kv_bytes_v = (uint32_t)(((int64_t)(Lk - 1) * v_si + D) * 2);
   auto load_stage = [&](int64_t g, Stage& st) {
-    const T* kbase = a.k + S.k_off + g * S.k_sg + h * S.k_sh;
-    const T* vbase = a.v + S.v_off + g * S.v_sg + h * S.v_sh;
-    const __amdgpu_buffer_rsrc_t kr = make_rsrc(kbase, (uint32_t)(((int64_t)(Lk - 1) * k_si + D) * 2));
-    const __amdgpu_buffer_rsrc_t vr = make_rsrc(vbase, (uint32_t)(((int64_t)(Lk - 1) * v_si + D) * 2));
+    const bool live = g < g_end;  // past the part: zero-traffic loads, no branch
+    const int64_t gg = live ? g : g_begin;
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(k_h + gg * k_sg, kv_bytes_k);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(v_h + gg * v_sg, kv_bytes_v);
     const int key = k0 + lane;
-    bool keep = key < Lk;
-    if (keep && has_mask) keep = a.mask[S.m_off + g * S.m_sg + key] != 0;
+    bool keep = live && key < Lk;
+    if (keep && m_h) keep = m_h[gg * m_sg + key] != 0;
     st.bits = __ballot(keep);
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
@@ -640,24 +663,33 @@ __global__ __launch_bounds__(256, 2) void attn_dbias_fast_kernel(BwdArgsT<T, T> 
     if (tid == 0) keep_lds[buf] = st.bits;
   };
   // per-group query-side operands of this lane (registers)
+  // Raw loads only: any arithmetic on a loaded value here would make the
+  // wave wait for the load at once.  Queries past Lq read zeros (their
+  // scores then contribute P * (0 - 0) = 0 and are never written).
   struct QStage {
     Frag q[NQF], d[NQF];
-    float nlse, ndlt;
+    float lse, dlt;
   };
+  const uint32_t q_bytes = qv ? 16u * NQF : 0u;
   auto load_q = [&](int64_t g, QStage& qs) {
-    const T* qrow = a.q + S.q_off + g * S.q_sg + h * S.q_sh + (int64_t)q_lane * S.q_si;
-    const T* drow = a.dout + S.do_off + g * S.do_sg + h * S.do_sh + (int64_t)q_lane * S.do_si;
+    const bool live = qv && g < g_end;
+    const int64_t gg = g < g_end ? g : g_begin;
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(q_h + gg * q_sg, q_bytes_all);
+    const __amdgpu_buffer_rsrc_t dr = make_rsrc(do_h + gg * do_sg, do_bytes_all);
 #pragma unroll
     for (int s = 0; s < NQF; ++s) {
       const int col = s * 16 + g2 * 8;
-      const bool ok = qv && col < D;
-      qs.q[s] = __builtin_bit_cast(Frag, ok ? *reinterpret_cast<const uint4*>(qrow + col) : make_uint4(0, 0, 0, 0));
-      qs.d[s] = __builtin_bit_cast(Frag, ok ? *reinterpret_cast<const uint4*>(drow + col) : make_uint4(0, 0, 0, 0));
+      const bool ok = live && col < D;
+      qs.q[s] = __builtin_bit_cast(Frag, buffer_load16(qr, ok ? q_lane_off + col * 2 : kOut));
+      qs.d[s] = __builtin_bit_cast(Frag, buffer_load16(dr, ok ? do_lane_off + col * 2 : kOut));
     }
-    const int64_t lidx = S.l_off + (g * H + h) * Lq + q_lane;
-    qs.nlse = qv ? -a.lse[lidx] : -__builtin_huge_valf();
-    qs.ndlt = qv ? -a.delta[lidx] : 0.0f;
+    const __amdgpu_buffer_rsrc_t lr = make_rsrc(l_h + gg * l_sg, (uint32_t)(Lq * 4));
+    const __amdgpu_buffer_rsrc_t drr = make_rsrc(d_h + gg * l_sg, (uint32_t)(Lq * 4));
+    const uint32_t loff = live ? (uint32_t)(q_lane * 4) : kOut;
+    qs.lse = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(lr, loff, 0, 0));
+    qs.dlt = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(drr, loff, 0, 0));
   };
+  (void)q_bytes;
 
   const int64_t ng = g_end - g_begin;
   Stage stg;
@@ -672,7 +704,7 @@ __global__ __launch_bounds__(256, 2) void attn_dbias_fast_kernel(BwdArgsT<T, T> 
     store_stage(1, stg);
     load_q(g_begin + 1, qb2);
   }
-  if (ng > 2) load_stage(g_begin + 2, stg);
+  load_stage(g_begin + 2, stg);
   vmem_wait_all();
   __syncthreads();
   int buf = 0;
@@ -680,14 +712,15 @@ __global__ __launch_bounds__(256, 2) void attn_dbias_fast_kernel(BwdArgsT<T, T> 
     const int b1 = buf == 2 ? 0 : buf + 1;
     const int b2 = b1 == 2 ? 0 : b1 + 1;
     if (i + 2 < ng) store_stage(b2, stg);
-    if (i + 3 < ng) load_stage(g_begin + i + 3, stg);
+    load_stage(g_begin + i + 3, stg);
     const T* kt = &k_lds[buf * TBUF];
     const T* vt = &v_lds[buf * TBUF];
     const uint64_t bits = keep_lds[buf];
     const uint64_t lb = bits >> (g2 * 4);
     f32x16 nd;
+    const float ndlt = -qc.dlt, nlse = -qc.lse;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) nd[j] = qc.ndlt;
+    for (int j = 0; j < 16; ++j) nd[j] = ndlt;
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
       f32x16 sacc = bacc[t2];
@@ -699,7 +732,7 @@ __global__ __launch_bounds__(256, 2) void attn_dbias_fast_kernel(BwdArgsT<T, T> 
       }
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j], c1, qc.nlse));
+        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j], c1, nlse));
         if (bits != ~uint64_t(0)) {
           const int kk = 32 * t2 + ((j >> 2) << 3) + (j & 3);
           p = ((lb >> kk) & 1) ? p : 0.0f;
@@ -707,7 +740,7 @@ __global__ __launch_bounds__(256, 2) void attn_dbias_fast_kernel(BwdArgsT<T, T> 
         acc[t2][j] = __builtin_fmaf(p, pacc[j], acc[t2][j]);
       }
     }
-    if (i + 2 < ng) load_q(g_begin + i + 2, qc);
+    load_q(g_begin + i + 2, qc);
     lds_barrier();
     buf = b1;
   };

@@ -105,9 +105,16 @@ __device__ __forceinline__ void store_elems(T* dst, uint4 u) {
 }
 
 // Buffer resource over `bytes` bytes at `base`: raw buffer loads through it
-// return zeros for offsets at or past `bytes` instead of faulting.
+// return zeros for offsets at or past `bytes` instead of faulting.  Callers
+// pass wave-uniform values only; they are moved to scalar registers here
+// (the compiler cannot always prove uniformity of values derived from the
+// geometry table and would otherwise wrap every load in a waterfall loop).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  void* up = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(up, (short)0, (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
 }
 __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));

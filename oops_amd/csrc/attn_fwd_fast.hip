@@ -153,8 +153,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fast_kernel(FwdArgsT<T, T> a)
       b_off[t2][c] = qv ? (uint32_t)((q_lane * b_si + 32 * t2 + 16 * c + g2 * 8) * 2) : kOut;
 
   // tile -> registers (K, V chunks of this thread; masked keys read zeros)
+  // An absent tile (t >= ntiles) issues its loads with out-of-range offsets:
+  // no memory traffic, and no branch, so the compiler can count outstanding
+  // loads exactly and never has to wait for all of them.
   auto load_kv = [&](int t, uint4 (&ku)[NCH], uint4 (&vu)[NCH]) {
-    const uint64_t bits = keep_lds[t];
+    const uint64_t bits = t < ntiles ? keep_lds[t < ntiles ? t : 0] : 0;
     const uint32_t ks = (uint32_t)(t * 64 * k_si * 2), vs = (uint32_t)(t * 64 * v_si * 2);
     const bool full = bits == ~uint64_t(0);
 #pragma unroll
@@ -183,7 +186,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fast_kernel(FwdArgsT<T, T> a)
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
-      for (int c = 0; c < 2; ++c) bf[t2][c] = buffer_load16_s(b_rsrc, b_off[t2][c] + s, 0);
+      for (int c = 0; c < 2; ++c) bf[t2][c] = buffer_load16_s(b_rsrc, t < ntiles ? b_off[t2][c] + s : kOut, 0);
   };
   // S^T of a tile (bias by identity MFMA, then Q K^T) from LDS buffer buf
   auto scores = [&](int buf, const uint4 (&bf)[2][2], f32x16 (&sacc)[2]) {
@@ -293,7 +296,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fast_kernel(FwdArgsT<T, T> a)
     if constexpr (HAS_BIAS) load_bias(t1, bias_b);
     store_kv(1, ku, vu);
   }
-  if (t2 < ntiles) load_kv(t2, ku, vu);
+  load_kv(t2, ku, vu);
   // drain every prologue load (Q included) so the wait counters are clean
   // at loop entry and only the loads issued in a step are ever in flight
   vmem_wait_all();
@@ -301,7 +304,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fast_kernel(FwdArgsT<T, T> a)
 #if OOPS_FWD_PIPE
   if (t0 < ntiles) scores(0, bias_a, sacc_a);
   if constexpr (HAS_BIAS)
-    if (t2 < ntiles) load_bias(t2, bias_a);
+    load_bias(t2, bias_a);
 #endif
 
   int buf = 0;
@@ -312,16 +315,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fast_kernel(FwdArgsT<T, T> a)
     const int b1 = buf == 2 ? 0 : buf + 1;
     const int b2 = b1 == 2 ? 0 : b1 + 1;
     if (t2 < ntiles) store_kv(b2, ku, vu);
-    if (t3 < ntiles) load_kv(t3, ku, vu);
+    load_kv(t3, ku, vu);
 #if OOPS_FWD_PIPE
     if (t1 < ntiles) scores(b1, bias_nxt, sacc_nxt);
     if constexpr (HAS_BIAS)
-      if (t3 < ntiles) load_bias(t3, bias_nxt);
+      load_bias(t3, bias_nxt);
     attend(buf, bits, sacc_cur);
 #else
     scores(buf, bias_cur, sacc_cur);
     if constexpr (HAS_BIAS)
-      if (t2 < ntiles) load_bias(t2, bias_cur);
+      load_bias(t2, bias_cur);
     attend(buf, bits, sacc_cur);
 #endif
     lds_barrier();
