@@ -28,6 +28,8 @@ if ROOT not in sys.path:
 METRIC = "tri-attn fwd+bwd TFLOP/s & ms/call at N=768 bf16; MFMA util % vs peak"
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
+COPY_CAL_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "triangle_attention_c3_bf16_traffic.txt")
 N, H, C = 768, 4, 32
 
 
@@ -128,6 +130,29 @@ def kernel_times(q, k, v, bias, dout, iters=20):
     return res
 
 
+def measured_traffic(kernel):
+    """HBM bytes per dispatch of ``kernel`` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (raw KiB readings scaled by a plain copy's readings), or None if absent."""
+
+    try:
+        lines = open(TRAFFIC_FILE).read().splitlines()
+    except OSError:
+        return None
+    factors, rows = {}, {}
+    for ln in lines:
+        parts = ln.split()
+        if not parts or ln.startswith("#"):
+            continue
+        if len(parts) == 2:
+            factors[parts[0]] = float(parts[1])
+        elif len(parts) == 3:
+            rows[parts[0]] = (float(parts[1]), float(parts[2]))
+    if kernel not in rows:
+        return None
+    fetch, write = rows[kernel]
+    return int((fetch * factors.get("fetch_factor", 1.0) + write * factors.get("write_factor", 1.0)) * 1024)
+
+
 # per-kernel MFMA work in units of 2*H*c*N^3 (one N x N x c GEMM per row and head)
 KERNEL_GEMMS = {"fwd": 2, "dq": 3, "dkv": 4, "dbias": 2, "delta": 0}
 
@@ -174,6 +199,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument(
+        "--copy-calibration",
+        action="store_true",
+        help="only copy a 256 MiB device buffer 3 times (scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)",
+    )
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(
@@ -184,6 +214,14 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.copy_calibration:
+        x = torch.empty(COPY_CAL_BYTES // 4, device="cuda:0")
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        return
 
     from oops_amd import _lib
 
@@ -249,7 +287,7 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(ach / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(dominant),
         },
     }
     if not args.no_cpu:

@@ -250,14 +250,8 @@ __global__ __launch_bounds__(256, 2) void attn_dkv_fast_kernel(BwdArgsT<T, T> a)
     const float ks = kvalid ? a.scale : 0.0f, vs = kvalid ? 1.0f : 0.0f;
 #pragma unroll
     for (int t = 0; t < NDT; ++t) {
-#pragma unroll
-      for (int i = 0; i < 16; i += 4) {
-        const int d = t * 32 + kappa(g2, i);
-        if (d < D) {
-          if (krow) store4<T>(krow, d, dk[t][i] * ks, dk[t][i + 1] * ks, dk[t][i + 2] * ks, dk[t][i + 3] * ks);
-          if (vrow) store4<T>(vrow, d, dv[t][i] * vs, dv[t][i + 1] * vs, dv[t][i + 2] * vs, dv[t][i + 3] * vs);
-        }
-      }
+      if (krow) store_tile<T>(krow, t * 32, D, g2, dk[t], ks);
+      if (vrow) store_tile<T>(vrow, t * 32, D, g2, dv[t], vs);
     }
   }
 }
@@ -514,14 +508,7 @@ __global__ __launch_bounds__(256, 2) void attn_dq_fast_kernel(BwdArgsT<T, T> a) 
   if (qv && a.dq != nullptr) {
     T* row = a.dq + S.q_off + g * S.q_sg + h * S.q_sh + (int64_t)q_lane * S.q_si;
 #pragma unroll
-    for (int t = 0; t < NDT; ++t)
-#pragma unroll
-      for (int i = 0; i < 16; i += 4) {
-        const int d = t * 32 + kappa(g2, i);
-        if (d < D)
-          store4<T>(row, d, acc[t][i] * a.scale, acc[t][i + 1] * a.scale, acc[t][i + 2] * a.scale,
-                    acc[t][i + 3] * a.scale);
-      }
+    for (int t = 0; t < NDT; ++t) store_tile<T>(row, t * 32, D, g2, acc[t], a.scale);
   }
 }
 

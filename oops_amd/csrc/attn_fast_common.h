@@ -69,5 +69,38 @@ __device__ __forceinline__ void store4(T* row, int d0, float x0, float x1, float
   *reinterpret_cast<v4*>(row + d0) = v;
 }
 
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float x, float y) {
+  const uint32_t lo = __builtin_bit_cast(uint16_t, (T)x), hi = __builtin_bit_cast(uint16_t, (T)y);
+  return lo | (hi << 16);
+}
+
+// Write one 32x32 accumulator tile's 32 head-dim values (lane (col, g) holds
+// acc[j] = row kappa(g, j)) to row[d0 .. d0+31], times s, for d < D (D % 8 == 0).
+// The two 32-lane halves trade values through v_permlane32_swap so that the
+// lower half holds d0 .. d0+15 and the upper half d0+16 .. d0+31: each lane
+// then writes 32 contiguous bytes and every 64-byte row segment is written
+// whole by one instruction, instead of four instructions each leaving it
+// partially written (which doubles the write traffic reaching HBM).
+template <typename T, typename Acc>
+__device__ __forceinline__ void store_tile(T* row, int d0, int D, int g, const Acc& acc, float s) {
+  uint32_t p[8];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    p[2 * q] = pack2<T>(acc[4 * q] * s, acc[4 * q + 1] * s);
+    p[2 * q + 1] = pack2<T>(acc[4 * q + 2] * s, acc[4 * q + 3] * s);
+  }
+  // p[0..1]: d kappa(g,0..3) = 4g..4g+3; p[2..3]: 8+4g..; p[4..5]: 16+4g..; p[6..7]: 24+4g..
+  const auto a = __builtin_amdgcn_permlane32_swap(p[0], p[4], false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(p[1], p[5], false, false);
+  const auto c = __builtin_amdgcn_permlane32_swap(p[2], p[6], false, false);
+  const auto e = __builtin_amdgcn_permlane32_swap(p[3], p[7], false, false);
+  const uint4 lo = make_uint4(a[0], b[0], a[1], b[1]);  // d0 + 16g + 0 .. 7
+  const uint4 hi = make_uint4(c[0], e[0], c[1], e[1]);  // d0 + 16g + 8 .. 15
+  const int d = d0 + 16 * g;
+  if (d + 8 <= D) *reinterpret_cast<uint4*>(row + d) = lo;
+  if (d + 16 <= D) *reinterpret_cast<uint4*>(row + d + 8) = hi;
+}
+
 }  // namespace fast
 }  // namespace oops

@@ -348,20 +348,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fast_kernel(FwdArgsT<T, T> a)
     T* lrow = a.out_lo != nullptr ? a.out_lo + o_row : nullptr;
 #pragma unroll
     for (int t = 0; t < NDT; ++t) {
+      float o[16], r[16];
 #pragma unroll
-      for (int i = 0; i < 16; i += 4) {
-        const int d = t * 32 + kappa(g2, i);  // d .. d+3 contiguous; D % 8 == 0
-        if (d < D) {
-          float o[4], r[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            o[e] = oacc[t][i + e] * inv;
-            r[e] = o[e] - E::to_f(E::from_f(o[e]));  // rounding residual of the output
-          }
-          store4<T>(orow, d, o[0], o[1], o[2], o[3]);
-          if (lrow) store4<T>(lrow, d, r[0], r[1], r[2], r[3]);
-        }
+      for (int e = 0; e < 16; ++e) {
+        o[e] = oacc[t][e] * inv;
+        r[e] = o[e] - E::to_f(E::from_f(o[e]));  // rounding residual of the output
       }
+      store_tile<T>(orow, t * 32, D, g2, o, 1.0f);
+      if (lrow) store_tile<T>(lrow, t * 32, D, g2, r, 1.0f);
     }
     if (g2 == 0 && a.lse != nullptr) {
       const float m_use = m_run == kNegInf ? 0.0f : m_run;
