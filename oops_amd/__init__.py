@@ -5,6 +5,6 @@ is the drop-in for ``from oops import ...`` on the attention path.
 """
 
 from ._errors import OOpsUnsupportedError
-from .attention import triangle_attention
+from .attention import pair_bias_attention, triangle_attention
 
-__all__ = ["OOpsUnsupportedError", "triangle_attention"]
+__all__ = ["OOpsUnsupportedError", "pair_bias_attention", "triangle_attention"]

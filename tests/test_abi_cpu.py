@@ -1,0 +1,149 @@
+"""The C-ABI library without a GPU: it loads, exports every symbol the header
+declares, and validates geometry on the host before any HIP call.
+
+No kernel is launched here; every call below fails validation (or only sizes
+the workspace) before the library touches the device.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from oops_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "oops_amd.h"
+
+
+def header_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(oops_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_exports_every_declared_symbol(lib):
+    declared = header_functions()
+    assert declared == sorted(_lib.EXPORTED_SYMBOLS)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.oops_abi_version() == _lib.ABI_VERSION
+
+
+def test_header_constants_match_python():
+    text = HEADER.read_text()
+    consts = dict(re.findall(r"#define\s+(OOPS_\w+)\s+(\d+)", text))
+    assert int(consts["OOPS_F32"]) == _lib.F32
+    assert int(consts["OOPS_BF16"]) == _lib.BF16
+    assert int(consts["OOPS_F16"]) == _lib.F16
+    assert int(consts["OOPS_BIAS_NONE"]) == _lib.BIAS_NONE
+    assert int(consts["OOPS_BIAS_FULL"]) == _lib.BIAS_FULL
+    assert int(consts["OOPS_BIAS_SHARED"]) == _lib.BIAS_SHARED
+    assert int(re.search(r"OOPS_TABLE_WIDTH\s*=\s*(\d+)", text).group(1)) == _lib.TABLE_WIDTH
+    # table column order: the enum lists the columns in _lib's order
+    enum = re.search(r"enum oops_table_column\s*\{(.*?)\}", text, re.S).group(1)
+    names = re.findall(r"OOPS_T_(\w+)", re.sub(r"/\*.*?\*/", "", enum, flags=re.S))
+    assert names.index("BIAS_MODE") == _lib.T_BIAS_MODE
+    assert names.index("L_OFF") == _lib.T_L_OFF
+    assert names.index("DB_OFF") == _lib.T_DB_OFF
+
+
+def _geometry(table, *, heads=4, head_size=32, dtype=_lib.BF16, has_bias=True):
+    arr = (ctypes.c_int64 * len(table))(*table)
+    geo = _lib.Geometry()
+    geo.dtype = dtype
+    geo.bias_dtype = dtype
+    geo.num_heads = heads
+    geo.head_size = head_size
+    geo.num_samples = len(table) // _lib.TABLE_WIDTH
+    geo.has_bias = int(has_bias)
+    geo.has_mask = 0
+    geo.vec_ok = 1
+    geo.scale = head_size**-0.5
+    geo.table_host = ctypes.addressof(arr)
+    geo.table_device = 0x1000  # never dereferenced on the host
+    return geo, arr
+
+
+def c3_table(n=768, h=4, c=32):
+    """Ending-node row of BASELINE config 3: q[g, i, h, d] at i*(n*h*c) + g*(h*c) + h*c + d."""
+
+    from oops_amd.attention import _core
+
+    qs = (0, h * c, c, n * h * c)
+    return _core.table_row(
+        groups=n, len_q=n, len_k=n, q=qs, k=qs, v=qs, bias=(0, 0, n * n, n), dbias=(0, 0, n * n, n),
+        bias_mode=_lib.BIAS_SHARED, lse_off=0,
+    )  # fmt: skip
+
+
+def test_workspace_sizing(lib):
+    geo, keep = _geometry(c3_table())
+    ws = lib.oops_attn_backward_workspace_bytes(ctypes.byref(geo))
+    # delta: one float per (group, head, query); then partial dBias slabs of H*N*N floats
+    delta = 768 * 4 * 768 * 4
+    slab = 4 * 768 * 768 * 4  # float32 partial dBias per part
+    parts, rest = divmod(ws - delta, slab)
+    assert rest == 0 and 2 <= parts <= 64, (ws, parts, rest)
+
+
+@pytest.mark.parametrize(
+    "field,value,message",
+    [
+        ("num_heads", 0, "num_heads"),
+        ("head_size", 0, "head_size"),
+        ("head_size", 257, "head_size"),
+        ("dtype", 7, "dtype"),
+        ("num_samples", 0, "num_samples"),
+    ],
+)
+def test_geometry_validation(lib, field, value, message):
+    geo, keep = _geometry(c3_table())
+    setattr(geo, field, value)
+    rc = lib.oops_attn_forward(ctypes.byref(geo), 1, 1, 1, None, 1, 1, None, 1, None)
+    assert rc == 1
+    assert message in lib.oops_last_error().decode()
+    assert lib.oops_attn_backward_workspace_bytes(ctypes.byref(geo)) == 0
+
+
+def test_table_validation(lib):
+    from oops_amd.attention import _core
+
+    row = c3_table()
+    bad = list(row)
+    bad[_lib.T_LEN_K] = 0
+    geo, keep = _geometry(bad)
+    assert lib.oops_attn_forward(ctypes.byref(geo), 1, 1, 1, None, 1, 1, None, 1, None) == 1
+    assert "empty axis" in lib.oops_last_error().decode()
+    bad = list(row)
+    bad[_lib.T_B_SG] = 5  # a shared bias with a group stride
+    geo, keep = _geometry(bad)
+    assert lib.oops_attn_forward(ctypes.byref(geo), 1, 1, 1, None, 1, 1, None, 1, None) == 1
+    assert "group stride 0" in lib.oops_last_error().decode()
+    geo, keep = _geometry(row)
+    geo.table_host = None
+    assert lib.oops_attn_forward(ctypes.byref(geo), 1, 1, 1, None, 1, 1, None, 1, None) == 1
+    assert lib.oops_attn_forward(None, 1, 1, 1, None, 1, 1, None, 1, None) == 1
+    assert "NULL" in lib.oops_last_error().decode()
+    del _core
+
+
+def test_pointer_and_workspace_validation(lib):
+    geo, keep = _geometry(c3_table())
+    # NULL operands
+    assert lib.oops_attn_forward(ctypes.byref(geo), None, 1, 1, None, 1, 1, None, 1, None) == 1
+    # has_bias without a bias pointer
+    assert lib.oops_attn_forward(ctypes.byref(geo), 1, 1, 1, None, None, 1, None, 1, None) == 1
+    assert "bias" in lib.oops_last_error().decode()
+    # too small a workspace
+    rc = lib.oops_attn_backward(ctypes.byref(geo), 1, 1, 1, None, 1, 1, None, 1, 1, 1, 1, 1, 1, 256, 16, None)
+    assert rc == 3
+    assert "workspace" in lib.oops_last_error().decode()
+    # misaligned workspace
+    need = lib.oops_attn_backward_workspace_bytes(ctypes.byref(geo))
+    rc = lib.oops_attn_backward(ctypes.byref(geo), 1, 1, 1, None, 1, 1, None, 1, 1, 1, 1, 1, 1, 8, need, None)
+    assert rc == 3 and "aligned" in lib.oops_last_error().decode()

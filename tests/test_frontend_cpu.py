@@ -1,0 +1,121 @@
+"""Front-end contract on the CPU: argument errors, admission, and shape
+propagation under FakeTensorMode (no kernel runs).
+
+Follows the reference's contract tests (tests/attention/triangle/
+test_triangle_attention.py:455-560, tests/attention/pair_bias/
+test_pair_bias_attention.py:488-640): ``ValueError`` for malformed shapes and
+mixed dense/nested operands, ``OOpsUnsupportedError`` for CPU tensors,
+unsupported dtypes, non-bool masks and forward-mode AD; fake tensors with
+(unbacked) symbolic sizes trace through the custom ops.
+"""
+
+import pytest
+import torch
+from torch._subclasses.fake_tensor import FakeTensorMode, is_fake
+from torch.autograd import forward_ad
+from torch.fx.experimental.symbolic_shapes import ShapeEnv
+
+from oops_amd import OOpsUnsupportedError, pair_bias_attention, triangle_attention
+
+
+class _NestedStandIn:
+    """Duck-typed NestedTensor marker (the front-ends detect ``.concat`` + ``.packed_like``)."""
+
+    concat = torch.zeros(1)
+
+    def packed_like(self, values):
+        return values
+
+
+def test_triangle_cpu_tensors_unsupported():
+    q = torch.randn(1, 3, 5, 2, 8)
+    with pytest.raises(OOpsUnsupportedError):
+        triangle_attention(q, q, q)
+
+
+def test_triangle_shape_errors():
+    q = torch.randn(1, 3, 5, 2, 8)
+    with pytest.raises(ValueError):
+        triangle_attention(q, q, q[..., :-1])
+    with pytest.raises(ValueError):
+        triangle_attention(q[0, 0], q[0, 0], q[0, 0])  # rank 3
+    with pytest.raises(ValueError):
+        triangle_attention(q, q, q, torch.ones(1, 4, 5, dtype=torch.bool))
+    with pytest.raises(ValueError):
+        triangle_attention(q, q, q, None, torch.randn(1, 2, 2, 5, 5))  # bias rows neither 1 nor R
+
+
+def test_triangle_mixed_nested_is_value_error():
+    q = torch.randn(1, 3, 3, 2, 8)
+    with pytest.raises(ValueError):
+        triangle_attention(q, _NestedStandIn(), q)
+    with pytest.raises(ValueError):
+        triangle_attention(q, q, q, _NestedStandIn())
+
+
+def test_triangle_forward_ad_unsupported():
+    q = torch.randn(1, 3, 3, 2, 8)
+    with forward_ad.dual_level():
+        dual = forward_ad.make_dual(q, torch.ones_like(q))
+        with pytest.raises(OOpsUnsupportedError):
+            triangle_attention(dual, q, q)
+
+
+def test_pair_bias_contract_on_cpu():
+    q = torch.randn(2, 2, 5, 8)
+    with pytest.raises(OOpsUnsupportedError):
+        pair_bias_attention(q, q, q)
+    with pytest.raises(ValueError):
+        pair_bias_attention(q, q, q[..., :-1])
+    with pytest.raises(ValueError):
+        pair_bias_attention(q[0, 0], q[0, 0], q[0, 0])  # rank 2
+    with pytest.raises(ValueError):
+        pair_bias_attention(q, _NestedStandIn(), q)
+    with pytest.raises(OOpsUnsupportedError):  # mask head axis of size 2
+        pair_bias_attention(q, q, q, torch.ones(2, 2, 5, 5, dtype=torch.bool))
+    with forward_ad.dual_level():
+        dual = forward_ad.make_dual(q, torch.ones_like(q))
+        with pytest.raises(OOpsUnsupportedError):
+            pair_bias_attention(dual, q, q)
+    # prefixed (rank 6) shape errors are ValueError, as in the reference
+    q6 = torch.randn(2, 2, 3, 2, 5, 8)
+    with pytest.raises(ValueError):
+        pair_bias_attention(q6, q6, q6, torch.ones(2, 2, 4, 5, dtype=torch.bool))
+    with pytest.raises(ValueError):
+        pair_bias_attention(q6, q6, q6, None, torch.randn(2, 2, 3, 2, 5, 4))
+
+
+@pytest.mark.parametrize("layout", ["starting", "ending", "batchless", "prefixed"])
+def test_triangle_fake_shapes(layout):
+    with FakeTensorMode():
+        if layout == "ending":
+            q = torch.empty(1, 12, 10, 2, 16, device="cuda", dtype=torch.bfloat16).transpose(1, 2)
+        elif layout == "batchless":
+            q = torch.empty(10, 12, 2, 16, device="cuda", dtype=torch.bfloat16)
+        elif layout == "prefixed":
+            q = torch.empty(2, 3, 10, 12, 2, 16, device="cuda", dtype=torch.bfloat16)
+        else:
+            q = torch.empty(1, 10, 12, 2, 16, device="cuda", dtype=torch.bfloat16)
+        rows, cols = q.shape[-4], q.shape[-3]
+        bias = torch.empty(*q.shape[:-4], 1, 2, cols, cols, device="cuda", dtype=torch.bfloat16)
+        mask = torch.empty(*q.shape[:-4], rows, cols, device="cuda", dtype=torch.bool)
+        out = triangle_attention(q, q, q, mask, bias)
+        assert is_fake(out)
+        assert out.shape == q.shape and out.dtype == q.dtype
+
+
+def test_pair_bias_fake_unbacked_lengths():
+    """The reference's "fake" scenario (test_pair_bias_attention.py:490-506)."""
+
+    shape_env = ShapeEnv()
+    query_length = shape_env.create_unbacked_symint()
+    key_length = shape_env.create_unbacked_symint()
+    torch._check(query_length >= 2)
+    torch._check(key_length >= 2)
+    with FakeTensorMode(shape_env=shape_env):
+        q = torch.empty(2, 2, query_length, 24, device="cuda")
+        k = torch.empty(2, 2, key_length, 24, device="cuda")
+        mask = torch.empty(2, query_length, key_length, device="cuda", dtype=torch.bool)
+        bias = torch.empty(2, 2, query_length, key_length, device="cuda")
+        out = pair_bias_attention(q, k, k, mask, bias)
+    assert is_fake(out) and out.shape == q.shape and out.dtype == q.dtype

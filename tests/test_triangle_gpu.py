@@ -19,6 +19,8 @@ from oracle import attention as ora
 from oops_amd import OOpsUnsupportedError, triangle_attention
 from oops_amd.attention import _core
 
+from accuracy import assert_close
+
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
@@ -26,25 +28,6 @@ DEV = "cuda"
 
 def _np(t):
     return None if t is None else t.detach().double().cpu().numpy()
-
-
-def assert_close(actual, expected, dtype, what="", tol16=2e-2):
-    actual = actual.detach().double().cpu().numpy()
-    err = np.abs(actual - expected)
-    if dtype == torch.float32:
-        # 1e-5 absolute on unit-scale values, relative beyond |ref| > 1
-        scaled = err / np.maximum(1.0, np.abs(expected))
-        assert scaled.max() <= 1e-5, f"{what}: scaled max-abs {scaled.max():.3g} (max-abs {err.max():.3g})"
-    else:
-        # 2e-2 absolute on unit-scale values; relative beyond |ref| > 1, where the
-        # 16-bit result's own rounding (up to 2^-9 relative) would exceed 2e-2
-        scaled = err / np.maximum(1.0, np.abs(expected))
-        assert scaled.max() <= tol16, f"{what}: scaled max-abs {scaled.max():.3g}"
-        # mean-relative error; skipped when the reference is ~0 everywhere
-        # (e.g. dQ of a single key, which cancels exactly)
-        denom = np.abs(expected).mean()
-        if denom > 1e-3:
-            assert err.mean() / denom <= 1e-2, f"{what}: mean-rel {err.mean() / denom:.3g}"
 
 
 def make_case(dtype, *, prefix=(2,), rows=4, cols=33, heads=2, head=24, bias_kind="shared", masked=True,
