@@ -16,15 +16,18 @@
 //   * resolves masks per 64-key tile from a bitmap built once per
 //     workgroup: fully kept tiles do no mask work, fully masked tiles are
 //     skipped, only mixed tiles select per score;
-//   * software-pipelines inside each wave: the QK^T MFMAs of tile i+1 are
-//     issued before the softmax of tile i, so the matrix core works while
-//     the vector ALU computes exponents.
+//   * writes O and its rounding residual with whole 64-byte row segments.
 // Work split: 4 wavefronts x 32 queries per workgroup, 64 keys per step.
-// K (row-major) and V (transposed, key-permuted) go through a 3-buffer LDS
-// ring (one barrier per step, written two steps ahead); bias fragments are
-// loaded from global memory straight into registers two steps ahead.  All
-// loads use range-checked buffer resources whose per-thread offsets are
-// fixed; the per-step part rides in the scalar offset.
+// K and V (both row-major, as read from memory) go through a 3-buffer LDS
+// ring (one barrier per step, written two steps ahead); the PV MFMA reads
+// V^T fragments with the gfx950 LDS transpose read.  Bias fragments are
+// loaded from global memory straight into registers one step ahead.  All
+// loads use range-checked buffer resources; a tile past the end reads at an
+// out-of-range offset (zeros, no memory traffic) so every load is
+// unconditional and the wait counts stay exact.
+// OOPS_FWD_PIPE=1 builds a variant that issues the QK^T MFMAs of step i+1
+// before the softmax of step i; it needs more registers (one wave less per
+// SIMD) and measured slower at head size 32, so it is off by default.
 //
 // Semantics are those of the generic forward (attn_fwd.hip), i.e. of the
 // reference's _attend (oops/attention/triangle/triton/kernel.py:151-262):
