@@ -122,7 +122,8 @@ def triangle_attention_backward(q, k, v, dout, mask=None, bias=None, scale=None,
     dq = np.empty(qh.shape, dtype=dtype)
     dk = np.empty(kh.shape, dtype=dtype)
     dv = np.empty(vh.shape, dtype=dtype)
-    db = None if b is None else np.zeros(b.shape, dtype=dtype)
+    # dS accumulates at the full prefix; axes the bias broadcasts over are summed at the end
+    db = None if b is None else np.zeros((*prefix, *b.shape[-4:]), dtype=dtype)
     step = _row_chunk(R, C, H)
     for r0 in range(0, R, step):
         sl = slice(r0, min(R, r0 + step))
@@ -144,6 +145,12 @@ def triangle_attention_backward(q, k, v, dout, mask=None, bias=None, scale=None,
                 db += ds.sum(axis=-4, keepdims=True)
             else:
                 db[..., sl, :, :, :] = ds
+    if db is not None:
+        lead = db.ndim - b.ndim
+        db = db.sum(axis=tuple(range(lead))) if lead else db
+        for axis, size in enumerate(b.shape[:-4]):
+            if size == 1 and db.shape[axis] != 1:
+                db = db.sum(axis=axis, keepdims=True)
     if keep_full is not None:
         key_keep = keep_full[..., None, :, None]  # (..., R, 1, C, 1) against (..., R, H, C, D)
         dk = np.where(key_keep, dk, 0.0)

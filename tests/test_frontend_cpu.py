@@ -119,3 +119,34 @@ def test_pair_bias_fake_unbacked_lengths():
         bias = torch.empty(2, 2, query_length, key_length, device="cuda")
         out = pair_bias_attention(q, k, k, mask, bias)
     assert is_fake(out) and out.shape == q.shape and out.dtype == q.dtype
+
+
+def _nested_qkv(lengths=(3, 5), prefix=()):
+    from nested_standin import NestedTensor
+
+    pr = len(prefix)
+    tmpl = NestedTensor([torch.empty(*prefix, n, n, 2, 8) for n in lengths], ragged_dims=(pr, pr + 1))
+    return [tmpl.packed_like(torch.randn(tmpl.concat.shape)) for _ in range(3)]
+
+
+def test_nested_contract_on_cpu():
+    from nested_standin import NestedTensor
+
+    q, k, v = _nested_qkv()
+    with pytest.raises(OOpsUnsupportedError):  # CPU values
+        triangle_attention(q, k, v)
+    mtmpl = NestedTensor([torch.empty(n, n, dtype=torch.bool) for n in (3, 5)], ragged_dims=(0, 1))
+    mask = mtmpl.packed_like(torch.ones(mtmpl.concat.shape, dtype=torch.bool))
+    with pytest.raises(ValueError):  # mask orientation differs from q/k/v
+        triangle_attention(q, k, v, mask.transpose(-2, -1))
+    with pytest.raises(ValueError):  # q/k/v orientations differ
+        triangle_attention(q, k.transpose(-4, -3), v)
+    k2, _, _ = _nested_qkv(lengths=(4, 4))
+    with pytest.raises(ValueError):  # per-sample layouts differ
+        triangle_attention(q, k2, v)
+    with pytest.raises(ValueError):  # dense mask with nested q/k/v
+        triangle_attention(q, k, v, torch.ones(3, 3, dtype=torch.bool))
+    with pytest.raises(OOpsUnsupportedError):  # ragged dims that are not the pair axes
+        sizes = [(n, 1, 2, n, 8) for n in (3, 5)]
+        odd = NestedTensor(ragged_dims=(0, 3), _sizes=sizes, _concat=torch.randn(34, 1, 2, 8))
+        triangle_attention(odd, odd, odd)

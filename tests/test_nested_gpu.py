@@ -1,0 +1,225 @@
+"""GPU parity of nested (ragged) triangle attention against the numpy oracle.
+
+Follows the reference's nested cases (tests/attention/triangle/
+test_triangle_attention.py:65-169, :226-419): canonical and transposed
+(ending-node) packing, static prefixes (broadcast mask/bias prefixes too),
+shared / per-row ("full") / mixed-group / absent bias, masks, and gradients of
+the packed q/k/v and bias values.  The expected values come from the oracle
+applied to each element separately and packed back with the same topology
+(the reference's per-sample unbind -> dense reference -> re-pack), using the
+test stand-in for DanLing's NestedTensor.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as ora
+from oops_amd import OOpsUnsupportedError, triangle_attention
+
+from accuracy import assert_close
+from nested_standin import NestedTensor
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _np(t):
+    return None if t is None else t.detach().double().cpu().numpy()
+
+
+def nested_case(dtype, *, lengths=(3, 5), heads=2, head_size=16, mask=True, bias_kind="shared", transposed=False,
+                prefix=(), broadcast_prefix=False, seed=0):
+    """Mirrors _nested_case (test_triangle_attention.py:65-140)."""
+
+    g = torch.Generator().manual_seed(seed)
+    pr = len(prefix)
+    tmpl = NestedTensor([torch.empty(*prefix, n, n, heads, head_size) for n in lengths], ragged_dims=(pr, pr + 1))
+    qkv_values = [torch.randn(tmpl.concat.shape, generator=g).to(dtype).to(DEV).requires_grad_(True) for _ in range(3)]
+    q, k, v = (tmpl.packed_like(x) for x in qkv_values)
+    nested_mask = None
+    if mask:
+        mtmpl = NestedTensor([torch.empty(*prefix, n, n, dtype=torch.bool) for n in lengths], ragged_dims=(pr, pr + 1))
+        shape = (mtmpl.concat.shape[0], *((1,) * pr)) if broadcast_prefix else mtmpl.concat.shape
+        mv = torch.rand(shape, generator=g) > 0.2
+        off = 0
+        for n in lengths:
+            mv[off] = True
+            off += n * n
+        nested_mask = mtmpl.packed_like(mv.to(DEV).expand(mtmpl.concat.shape))
+    bias_values = None
+    bias_prefix = (1,) * pr if broadcast_prefix else prefix
+    bias = None
+    if bias_kind == "shared":
+        btmpl = NestedTensor([torch.empty(*bias_prefix, 1, heads, n, n) for n in lengths],
+                             ragged_dims=(pr + 2, pr + 3))  # fmt: skip
+    elif bias_kind in ("full", "mixed"):
+        groups = lengths if bias_kind == "full" else (1, *lengths[1:])
+        btmpl = NestedTensor([torch.empty(*bias_prefix, c, heads, n, n) for c, n in zip(groups, lengths)],
+                             ragged_dims=(pr, pr + 2, pr + 3))  # fmt: skip
+    if bias_kind != "none":
+        bias_values = torch.randn(btmpl.concat.shape, generator=g).to(dtype).to(DEV).requires_grad_(True)
+        bias = btmpl.packed_like(bias_values)
+    if transposed:
+        q, k, v = (t.transpose(-4, -3) for t in (q, k, v))
+        if nested_mask is not None:
+            nested_mask = nested_mask.transpose(-2, -1)
+        if bias is not None:
+            bias = bias.transpose(-2, -1)
+    return q, k, v, nested_mask, bias, qkv_values, bias_values
+
+
+def pack_like(nested, elements):
+    """Pack per-element numpy arrays with ``nested``'s topology (its concat layout)."""
+
+    packed = NestedTensor([torch.from_numpy(np.ascontiguousarray(e)) for e in elements],
+                          ragged_dims=nested.ragged_dims, packed_dim_order=nested.packed_dim_order)  # fmt: skip
+    return packed.concat.numpy()
+
+
+def expected(q, k, v, mask, bias, dout_nested, scale=None):
+    parts = [torch.unbind(t) if t is not None else None for t in (q, k, v, mask, bias, dout_nested)]
+    outs, grads = [], {"q": [], "k": [], "v": [], "b": []}
+    for i in range(len(parts[0])):
+        qi, ki, vi = (_np(parts[j][i]) for j in range(3))
+        mi = None if mask is None else _np(parts[3][i]).astype(bool)
+        bi = None if bias is None else _np(parts[4][i])
+        o, _ = ora.triangle_attention_forward(qi, ki, vi, mi, bi, scale)
+        outs.append(o)
+        dq, dk, dv, db = ora.triangle_attention_backward(qi, ki, vi, _np(parts[5][i]), mi, bi, scale)
+        grads["q"].append(dq)
+        grads["k"].append(dk)
+        grads["v"].append(dv)
+        grads["b"].append(db)
+    return outs, grads
+
+
+@pytest.mark.parametrize(
+    "dtype,bias_kind,transposed,prefix,broadcast",
+    [
+        (torch.float32, "shared", False, (), False),
+        (torch.float32, "full", True, (), False),
+        (torch.float32, "mixed", False, (2,), False),
+        (torch.float32, "none", True, (2,), False),
+        (torch.float32, "shared", True, (2,), True),
+        (torch.bfloat16, "shared", False, (), False),
+        (torch.bfloat16, "shared", True, (), False),
+        (torch.bfloat16, "full", False, (2,), True),
+        (torch.float16, "mixed", True, (), False),
+    ],
+)
+def test_nested_forward_backward(dtype, bias_kind, transposed, prefix, broadcast):
+    lengths = (3, 5) if dtype == torch.float32 else (33, 70)
+    head = 16 if dtype == torch.float32 else 32
+    q, k, v, mask, bias, qkv_values, bias_values = nested_case(
+        dtype, lengths=lengths, head_size=head, bias_kind=bias_kind, transposed=transposed, prefix=prefix,
+        broadcast_prefix=broadcast, seed=len(prefix) + 3 * transposed,
+    )  # fmt: skip
+    out = triangle_attention(q, k, v, mask, bias)
+    assert isinstance(out, NestedTensor)
+    assert out.ragged_dims == q.ragged_dims and out.packed_dim_order == q.packed_dim_order
+    assert out.concat.shape == q.concat.shape and out.concat.dtype == dtype
+    dout_values = torch.randn(out.concat.shape, generator=torch.Generator().manual_seed(5)).to(dtype).to(DEV)
+    dout = q.packed_like(dout_values)
+    outs, grads = expected(q, k, v, mask, bias, dout)
+    assert_close(out.concat, pack_like(q, outs), dtype, "out")
+    leaves = [*qkv_values] + ([bias_values] if bias_values is not None else [])
+    got = torch.autograd.grad(out.concat, leaves, dout_values)
+    for name, g_ in zip(("q", "k", "v"), got[:3]):
+        assert_close(g_, pack_like(q, grads[name]), dtype, "d" + name)
+    if bias_values is not None:
+        assert got[3].dtype == bias_values.dtype and got[3].shape == bias_values.shape
+        assert_close(got[3], pack_like(bias, grads["b"]), dtype, "dbias")
+
+
+def test_nested_matches_dense():
+    """One-element nested call == the dense call on the same element."""
+
+    q, k, v, mask, bias, _, _ = nested_case(torch.bfloat16, lengths=(48,), head_size=32, seed=8)
+    out = triangle_attention(q, k, v, mask, bias)
+    qd, kd, vd, md, bd = (torch.unbind(t)[0].unsqueeze(0) for t in (q, k, v, mask, bias))
+    dense = triangle_attention(qd, kd, vd, md, bd)
+    torch.testing.assert_close(out.concat.reshape(dense.shape), dense, atol=0, rtol=0)
+
+
+def test_nested_errors():
+    q, k, v, mask, bias, _, _ = nested_case(torch.float32)
+    with pytest.raises(ValueError):  # mixed dense / nested
+        triangle_attention(q, k.concat, v)
+    with pytest.raises(ValueError):  # mask orientation differs from q/k/v
+        triangle_attention(q, k, v, mask.transpose(-2, -1), bias)
+    q2, k2, v2, _, _, _, _ = nested_case(torch.float32, lengths=(4, 5))
+    with pytest.raises(ValueError):  # key layout differs per sample
+        triangle_attention(q, k2, v)
+    with pytest.raises(OOpsUnsupportedError):
+        triangle_attention(q.packed_like(q.concat.double()), k.packed_like(k.concat.double()),
+                           v.packed_like(v.concat.double()))  # fmt: skip
+    del q2, v2
+
+
+@pytest.mark.parametrize("transposed", [False, True])
+def test_config_c5_ragged(transposed):
+    """BASELINE config 5 at full size: N_i in {256, 512, 768, 1024}, H=4, c=32, bf16, per-complex key
+    masks hiding the last 0-20% residues, shared bias; starting (canonical) and ending (transposed) node.
+
+    Rows are independent, so the oracle checks 4 rows of every complex; the shared dBias (a sum over
+    all rows) is checked against a float32 torch restatement over every row.
+    """
+
+    g = torch.Generator().manual_seed(4)
+    lengths = (256, 512, 768, 1024)
+    h, c = 4, 32
+    tmpl = NestedTensor([torch.empty(n, n, h, c) for n in lengths], ragged_dims=(0, 1))
+    vals = [torch.randn(tmpl.concat.shape, generator=g).to(torch.bfloat16).to(DEV).requires_grad_(True)
+            for _ in range(3)]  # fmt: skip
+    btmpl = NestedTensor([torch.empty(1, h, n, n) for n in lengths], ragged_dims=(2, 3))
+    bvals = torch.randn(btmpl.concat.shape, generator=g).to(torch.bfloat16).to(DEV).requires_grad_(True)
+    masks = []
+    for n in lengths:
+        hide = int(n * float(torch.rand(1, generator=g)) * 0.2)
+        m = torch.ones(n, n, dtype=torch.bool)
+        if hide:
+            m[:, n - hide :] = False
+        masks.append(m)
+    mtmpl = NestedTensor(masks, ragged_dims=(0, 1))
+    q, k, v = (tmpl.packed_like(x) for x in vals)
+    mask = mtmpl.packed_like(mtmpl.concat.to(DEV))
+    bias = btmpl.packed_like(bvals)
+    if transposed:
+        q, k, v = (t.transpose(-4, -3) for t in (q, k, v))
+        mask = mask.transpose(-2, -1)
+        bias = bias.transpose(-2, -1)
+    out = triangle_attention(q, k, v, mask, bias)
+    dvals = torch.randn(out.concat.shape, generator=g).to(torch.bfloat16).to(DEV)
+    gq, gk, gv, gb = torch.autograd.grad(out.concat, (*vals, bvals), dvals)
+    dout = q.packed_like(dvals)
+    outs, gqs, gks, gvs = (torch.unbind(q.packed_like(x)) for x in (out.concat, gq, gk, gv))
+    gbs = torch.unbind(bias.packed_like(gb))
+    parts = [torch.unbind(t) for t in (q, k, v, mask, bias, dout)]
+    for i, n in enumerate(lengths):
+        rows = torch.tensor([0, n // 3, n // 2 + 1, n - 1])
+        qi, ki, vi, mi, bi, di = (parts[j][i] for j in range(6))
+        sel = lambda t: _np(t[rows])  # noqa: E731
+        want_o, _ = ora.triangle_attention_forward(sel(qi), sel(ki), sel(vi), _np(mi[rows]).astype(bool), _np(bi))
+        assert_close(outs[i][rows], want_o, torch.bfloat16, f"out[{i}]")
+        dq, dk, dv, _ = ora.triangle_attention_backward(sel(qi), sel(ki), sel(vi), sel(di),
+                                                        _np(mi[rows]).astype(bool), _np(bi))  # fmt: skip
+        assert_close(gqs[i][rows], dq, torch.bfloat16, f"dq[{i}]")
+        assert_close(gks[i][rows], dk, torch.bfloat16, f"dk[{i}]")
+        assert_close(gvs[i][rows], dv, torch.bfloat16, f"dv[{i}]")
+        # shared dBias over every row: float32 torch restatement, chunked over rows
+        qf, kf, vf, df = (t.detach().float() for t in (qi, ki, vi, di))
+        bf = bi.detach().float()[0]  # (H, N, N)
+        keep = mi.bool()
+        acc = torch.zeros(h, n, n, dtype=torch.float64, device=DEV)
+        for r0 in range(0, n, 64):
+            sl = slice(r0, r0 + 64)
+            qq, kk, vv, dd = (t[sl].permute(0, 2, 1, 3) for t in (qf, kf, vf, df))  # (r, H, N, c)
+            s = qq @ kk.transpose(-1, -2) * c**-0.5 + bf
+            s = s.masked_fill(~keep[sl, None, None, :], float("-inf"))
+            p = torch.softmax(s, -1).nan_to_num(0.0)  # fully masked rows: P = 0
+            o = p @ vv
+            ds = p * (dd @ vv.transpose(-1, -2) - (dd * o).sum(-1, keepdim=True))
+            acc += ds.sum(0).double()
+        assert_close(gbs[i][0], acc.cpu().numpy(), torch.bfloat16, f"dbias[{i}]")

@@ -113,6 +113,13 @@ def test_invariants():
     db_shared = ora.triangle_attention_backward(q, k, v, do, None, shared)[3]
     db_full = ora.triangle_attention_backward(q, k, v, do, None, full)[3]
     np.testing.assert_allclose(db_shared, db_full.sum(axis=1, keepdims=True), atol=1e-12)
+    # a bias broadcast over the prefix: its gradient is the prefix sum of the expanded bias's
+    q2, k2, v2, do2 = (_rand(rng, 2, R, C, H, D) for _ in range(4))
+    bb = _rand(rng, 1, 1, H, C, C)
+    db_b = ora.triangle_attention_backward(q2, k2, v2, do2, None, bb)[3]
+    db_e = ora.triangle_attention_backward(q2, k2, v2, do2, None, np.broadcast_to(bb, (2, 1, H, C, C)).copy())[3]
+    assert db_b.shape == bb.shape
+    np.testing.assert_allclose(db_b, db_e.sum(axis=0, keepdims=True), atol=1e-12)
     # dV == P^T dO with P rows summing to 1
     s = np.einsum("brihd,brjhd->brhij", q, k) * D**-0.5
     p = np.exp(s - s.max(-1, keepdims=True))
