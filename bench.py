@@ -157,6 +157,96 @@ def measured_traffic(kernel):
 KERNEL_GEMMS = {"fwd": 2, "dq": 3, "dkv": 4, "dbias": 2, "delta": 0}
 
 
+def _median_ms(fn, iters=10, warmup=3):
+    import torch
+
+    return time_events(fn, iters, warmup, torch.cuda.current_stream())
+
+
+def other_configs(device):
+    """fwd+bwd ms and TFLOP/s of BASELINE configs 2, 4 and 5 (parity cases, reported beside the headline)."""
+
+    import torch
+
+    from oops_amd import pair_bias_attention, triangle_attention
+
+    res = {}
+
+    def grad_step(fn, leaves, dout):
+        def run():
+            out = fn()
+            o = out.concat if hasattr(out, "concat") else out
+            torch.autograd.grad(o, leaves, dout)
+
+        return run
+
+    # C2: starting node, N=384, key padding of the last 10-30% (seed 1)
+    g = torch.Generator().manual_seed(1)
+    n = 384
+    q, k, v, do = (torch.randn(1, n, n, H, C, generator=g).to(torch.bfloat16).to(device) for _ in range(4))
+    bias = torch.randn(1, 1, H, n, n, generator=g).to(torch.bfloat16).to(device)
+    keep = n - round(n * float(torch.empty(1).uniform_(0.10, 0.30, generator=g)))
+    mask = torch.ones(1, n, n, dtype=torch.bool, device=device)
+    mask[..., keep:] = False
+    mask[:, keep:, :] = False
+    leaves = [t.requires_grad_(True) for t in (q, k, v, bias)]
+    ms = _median_ms(grad_step(lambda: triangle_attention(q, k, v, mask, bias), leaves, do))
+    res["c2_starting_n384_keypad"] = {"ms": round(ms, 4), "tflops": round(14 * H * C * n**3 / ms / 1e9, 2)}
+
+    # C4: MSA rows S=512, N=384, H=8 head-major, key mask ~15%, shared bias (seed 3)
+    g = torch.Generator().manual_seed(3)
+    s_, n, h = 512, 384, 8
+    q, k, v = (torch.randn(s_, n, h, C, generator=g).to(torch.bfloat16).permute(0, 2, 1, 3).to(device)
+               for _ in range(3))  # fmt: skip
+    bias = torch.randn(1, h, n, n, generator=g).to(torch.bfloat16).to(device)
+    mask = torch.rand(s_, n, generator=g) > 0.15
+    mask[:, 0] = True
+    mask = mask.to(device)
+    do = torch.randn(s_, h, n, C, generator=g).to(torch.bfloat16).to(device)
+    leaves = [t.requires_grad_(True) for t in (q, k, v, bias)]
+    ms = _median_ms(grad_step(lambda: pair_bias_attention(q, k, v, mask, bias), leaves, do))
+    res["c4_msa_rows_s512_n384_h8"] = {"ms": round(ms, 4), "tflops": round(14 * s_ * h * C * n**2 / ms / 1e9, 2)}
+
+    # C5: ragged complexes N_i in {256, 512, 768, 1024}, both orientations, key masks hiding 0-20% (seed 4)
+    tests_dir = os.path.join(ROOT, "tests")
+    if tests_dir not in sys.path:
+        sys.path.insert(0, tests_dir)
+    from nested_standin import NestedTensor  # DanLing's NestedTensor is not installed here
+
+    g = torch.Generator().manual_seed(4)
+    lengths = (256, 512, 768, 1024)
+    tmpl = NestedTensor([torch.empty(n_, n_, H, C) for n_ in lengths], ragged_dims=(0, 1))
+    vals = [torch.randn(tmpl.concat.shape, generator=g).to(torch.bfloat16).to(device).requires_grad_(True)
+            for _ in range(3)]  # fmt: skip
+    btmpl = NestedTensor([torch.empty(1, H, n_, n_) for n_ in lengths], ragged_dims=(2, 3))
+    bvals = torch.randn(btmpl.concat.shape, generator=g).to(torch.bfloat16).to(device).requires_grad_(True)
+    masks = []
+    for n_ in lengths:
+        hide = int(n_ * 0.2 * float(torch.rand(1, generator=g)))
+        m = torch.ones(n_, n_, dtype=torch.bool)
+        if hide:
+            m[:, n_ - hide :] = False
+        masks.append(m)
+    mtmpl = NestedTensor(masks, ragged_dims=(0, 1))
+    nmask = mtmpl.packed_like(mtmpl.concat.to(device))
+    nq, nk, nv = (tmpl.packed_like(x) for x in vals)
+    nb = btmpl.packed_like(bvals)
+    tq, tk, tv = (t.transpose(-4, -3) for t in (nq, nk, nv))
+    tm, tb = nmask.transpose(-2, -1), nb.transpose(-2, -1)
+    dvals = torch.randn(tmpl.concat.shape, generator=g).to(torch.bfloat16).to(device)
+    leaves = [*vals, bvals]
+
+    def both():
+        o1 = triangle_attention(nq, nk, nv, nmask, nb).concat
+        o2 = triangle_attention(tq, tk, tv, tm, tb).concat
+        torch.autograd.grad((o1, o2), leaves, (dvals, dvals))
+
+    ms = _median_ms(both, iters=5, warmup=2)
+    flops = 2 * 14 * H * C * sum(n_**3 for n_ in lengths)
+    res["c5_ragged_both_directions"] = {"ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 2)}
+    return res
+
+
 def cpu_baseline(budget_s=15.0):
     """The numpy oracle (float32) on a bounded sample of rows of the same workload."""
 
@@ -199,6 +289,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--no-extra", action="store_true", help="skip the configs 2/4/5 timings")
     ap.add_argument(
         "--copy-calibration",
         action="store_true",
@@ -290,6 +381,10 @@ def main():
             "traffic": measured_traffic(dominant),
         },
     }
+    if not args.no_extra:
+        _log("bench: configs 2, 4, 5")
+        line["other_configs"] = other_configs(dev)
+        _log("bench: " + json.dumps(line["other_configs"]))
     if not args.no_cpu:
         _log("bench: cpu baseline")
         line["cpu_baseline"] = cpu_baseline(args.cpu_budget)
