@@ -30,6 +30,7 @@
  *                           oops/attention/triangle/triton/kernel.py:375-873) and
  *                          run_attention_backward
  *                          (oops/attention/flash/triton/generic.py:324-658)
+ *   oops_attn_forward_workspace_bytes: no counterpart (see its declaration)
  *   oops_attn_backward_workspace_bytes <- the partial-slab sizing of
  *                          SharedBiasSplit (oops/attention/triangle/triton/schedule.py:124-141)
  *   the geometry table  <- the int64 sample table of
@@ -114,7 +115,14 @@ typedef struct oops_attn_geometry {
  * as the reference does with its saved fp32 output (triton/ops.py:369-377). */
 int oops_attn_forward(const oops_attn_geometry* geo, const void* q, const void* k, const void* v,
                       const uint8_t* mask, const void* bias, void* out, void* out_lo, float* lse,
-                      void* stream);
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of device workspace oops_attn_forward needs for this geometry (0 when
+ * none: workspace may then be NULL).  The forward uses it for a fragment-major
+ * copy of a row-shared bias (H x Lq x Lk elements, padded to 32), which the
+ * fast kernels read with contiguous loads; there is no counterpart in the
+ * reference, whose kernels read the bias rows directly. */
+size_t oops_attn_forward_workspace_bytes(const oops_attn_geometry* geo);
 
 /* Bytes of device workspace oops_attn_backward needs for this geometry. */
 size_t oops_attn_backward_workspace_bytes(const oops_attn_geometry* geo);
@@ -122,7 +130,9 @@ size_t oops_attn_backward_workspace_bytes(const oops_attn_geometry* geo);
 /* Backward: dq/dk/dv in dtype with the Q/K/V strides of the table; dbias f32
  * at the table's dBias offsets (may be NULL when no bias gradient is wanted;
  * any of dq/dk/dv may be NULL likewise).  workspace must be device memory of
- * at least oops_attn_backward_workspace_bytes(geo) bytes, 256-byte aligned. */
+ * at least oops_attn_backward_workspace_bytes(geo) bytes, 256-byte aligned
+ * (delta, the partial dBias slabs of a row-shared bias and, as in the forward,
+ * the fragment-major bias copy). */
 int oops_attn_backward(const oops_attn_geometry* geo, const void* q, const void* k, const void* v,
                        const uint8_t* mask, const void* bias, const void* out, const void* out_lo,
                        const float* lse, const void* dout, void* dq, void* dk, void* dv, float* dbias, void* workspace,

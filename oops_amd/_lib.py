@@ -18,7 +18,7 @@ F32, BF16, F16 = 0, 1, 2
 BIAS_NONE, BIAS_FULL, BIAS_SHARED = 0, 1, 2
 PHASE_DELTA, PHASE_DQ, PHASE_DKV, PHASE_DBIAS = 1, 2, 4, 8
 TABLE_WIDTH = 40
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # geometry table columns (enum oops_table_column)
 (
@@ -37,6 +37,7 @@ ABI_VERSION = 1
 
 EXPORTED_SYMBOLS = (
     "oops_attn_forward",
+    "oops_attn_forward_workspace_bytes",
     "oops_attn_backward_workspace_bytes",
     "oops_attn_backward",
     "oops_last_error",
@@ -86,8 +87,10 @@ def load() -> ctypes.CDLL:
         lib = ctypes.CDLL(os.fspath(LIB_PATH))
         vp, sz, i32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
         geo = ctypes.POINTER(Geometry)
-        lib.oops_attn_forward.argtypes = [geo, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        lib.oops_attn_forward.argtypes = [geo, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
         lib.oops_attn_forward.restype = i32
+        lib.oops_attn_forward_workspace_bytes.argtypes = [geo]
+        lib.oops_attn_forward_workspace_bytes.restype = sz
         lib.oops_attn_backward_workspace_bytes.argtypes = [geo]
         lib.oops_attn_backward_workspace_bytes.restype = sz
         lib.oops_attn_backward.argtypes = [geo, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]

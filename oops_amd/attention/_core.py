@@ -175,10 +175,12 @@ def attention_forward(
     lse = torch.empty(lse_numel, dtype=torch.float32, device=q.device)
     vec = _vec_ok(table, (q, k, v, out), bias)
     geo, keep = _geometry(q, bias, mask, table, num_heads, scale, vec)
+    ws_bytes = lib.oops_attn_forward_workspace_bytes(ctypes.byref(geo))
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
     with torch.cuda.device(q.device):
         rc = lib.oops_attn_forward(
             ctypes.byref(geo), _ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(bias), _ptr(out), _ptr(out_lo),
-            _ptr(lse), _stream(q.device),
+            _ptr(lse), _ptr(workspace), ws_bytes, _stream(q.device),
         )
     _lib.check(rc, "attention forward")
     del keep

@@ -726,10 +726,18 @@ int head_group_of(const oops_attn_geometry& geo) { return head_group(geo); }
 hipError_t launch_backward(const oops_attn_geometry& geo, const Plan& plan, const void* q, const void* k,
                            const void* v, const uint8_t* mask, const void* bias, const void* out,
                            const void* out_lo, const float* lse, const void* dout, void* dq, void* dk, void* dv,
-                           float* dbias, float* delta, float* dbias_part, hipStream_t stream) {
-  const BwdLaunch L{q, k, v, out, out_lo, dout, bias, mask, lse, delta, dq, dk, dv, dbias, dbias_part};
+                           float* dbias, float* delta, float* dbias_part, void* bias_frag, hipStream_t stream) {
   const bool fast = backward_fast_ok(geo, plan);
+  const int phases = geo.phases == 0 ? 0xF : geo.phases;
   hipError_t err = hipSuccess;
+  // the fragment-major bias copy feeds the fast dQ and dK/dV kernels
+  const bool use_bf = fast && plan.bias_frag && (phases & (OOPS_PHASE_DQ | OOPS_PHASE_DKV));
+  if (use_bf) {
+    err = launch_bias_frag(geo, plan, bias, bias_frag, stream);
+    if (err != hipSuccess) return err;
+  }
+  const BwdLaunch L{q, k, v, out, out_lo, dout, bias, mask, lse, delta, dq, dk, dv, dbias, dbias_part,
+                    use_bf ? bias_frag : nullptr};
   const bool ok = dispatch_config(geo.dtype, geo.bias_dtype, plan.dp, [&](auto t, auto bt, auto dpc) {
     using T = typename decltype(t)::type;
     using BT = typename decltype(bt)::type;
@@ -740,7 +748,6 @@ hipError_t launch_backward(const oops_attn_geometry& geo, const Plan& plan, cons
     auto check = [&]() {
       if (err == hipSuccess) err = hipGetLastError();
     };
-    const int phases = geo.phases == 0 ? 0xF : geo.phases;
     if (phases & OOPS_PHASE_DELTA) {
       a.uniform_tiles = plan.delta_uniform;
       hipLaunchKernelGGL((attn_delta_kernel<T, BT, DP>), dim3((unsigned)plan.delta_tiles), block, 0, stream, a);

@@ -112,11 +112,22 @@ __global__ __launch_bounds__(256, 2) void attn_dkv_fast_kernel(BwdArgsT<T, T> a)
   const __amdgpu_buffer_rsrc_t l_rsrc = make_rsrc(a.lse + S.l_off + ((int64_t)g * H + h) * Lq, (uint32_t)(Lq * 4));
   const __amdgpu_buffer_rsrc_t d_rsrc =
       make_rsrc(a.delta + S.l_off + ((int64_t)g * H + h) * Lq, (uint32_t)(Lq * 4));
-  // bias rows of this wave's keys: A fragments (lane = query, 8 consecutive keys)
-  const T* bbase = HAS_BIAS ? a.bias + S.b_off + g * S.b_sg + h * S.b_sh : a.q;
-  const __amdgpu_buffer_rsrc_t b_rsrc =
-      make_rsrc(bbase, HAS_BIAS ? (uint32_t)(((int64_t)(Lq - 1) * b_si + Lk) * 2) : 0u);
+  // bias rows of this wave's keys: A fragments (lane = query, 8 consecutive
+  // keys), from the fragment-major copy of a shared bias (one contiguous
+  // 1 KB load per fragment) or from the bias rows themselves
   const int kw = kb * 128 + wave * 32;  // first key of this wave
+  const bool use_bf = HAS_BIAS && a.bias_frag != nullptr && S.bias_mode == OOPS_BIAS_SHARED;
+  __amdgpu_buffer_rsrc_t b_rsrc;
+  if (use_bf) {
+    const int kt = kw >> 5;
+    const bool in = kt < a.bf_nkt;  // a wave wholly past Lk: empty range
+    b_rsrc = make_rsrc(a.bias_frag + s_idx * a.bf_sample_stride + (int64_t)h * a.bf_nqt * a.bf_nkt * 1024 +
+                           (in ? kt : 0) * 1024,
+                       in ? (uint32_t)(((int64_t)a.bf_nqt * a.bf_nkt - (in ? kt : 0)) * 2048) : 0u);
+  } else {
+    const T* bbase = HAS_BIAS ? a.bias + S.b_off + g * S.b_sg + h * S.b_sh : a.q;
+    b_rsrc = make_rsrc(bbase, HAS_BIAS ? (uint32_t)(((int64_t)(Lq - 1) * b_si + Lk) * 2) : 0u);
+  }
 
   struct Stage {
     uint4 q[NCH], d[NCH];
@@ -202,9 +213,12 @@ __global__ __launch_bounds__(256, 2) void attn_dkv_fast_kernel(BwdArgsT<T, T> a)
     for (int r = 0; r < 2; ++r) {
       const int q = step * 64 + 32 * r + lq;
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
-        bias[r][c] = buffer_load16_s(
-            b_rsrc, q < Lq ? (uint32_t)((q * b_si + kw + 16 * c + g2 * 8) * 2) : kOut, 0);
+      for (int c = 0; c < 2; ++c) {
+        // fragment copy: tile row qt = 2 step + r, entry (c, lane); rows past the copy read 0
+        const uint32_t off = use_bf ? (uint32_t)((((2 * step + r) * a.bf_nkt * 2 + c) * 64 + lane) * 16)
+                                    : (q < Lq ? (uint32_t)((q * b_si + kw + 16 * c + g2 * 8) * 2) : kOut);
+        bias[r][c] = buffer_load16_s(b_rsrc, off, 0);
+      }
     }
   };
 
@@ -355,15 +369,32 @@ __global__ __launch_bounds__(256, 2) void attn_dq_fast_kernel(BwdArgsT<T, T> a) 
     k_off[i] = col < D ? (uint32_t)((r * k_si + col) * 2) : kOut;
     v_off[i] = col < D ? (uint32_t)((r * v_si + col) * 2) : kOut;
   }
-  const T* bbase = HAS_BIAS ? a.bias + S.b_off + g * S.b_sg + h * S.b_sh : a.q;
-  const __amdgpu_buffer_rsrc_t b_rsrc =
-      make_rsrc(bbase, HAS_BIAS ? (uint32_t)(((int64_t)(Lq - 1) * b_si + Lk) * 2) : 0u);
-  uint32_t b_off[2][2];
+  // bias fragments: from the fragment-major copy of a shared bias (one
+  // contiguous 1 KB load per fragment), else from the bias rows themselves
+  const bool use_bf = HAS_BIAS && a.bias_frag != nullptr && S.bias_mode == OOPS_BIAS_SHARED;
+  __amdgpu_buffer_rsrc_t b_rsrc;
+  uint32_t b_off[2][2], b_step;
+  if (use_bf) {
+    const int qt = qb * 4 + wave;
+    const bool in = qt < a.bf_nqt;  // a wave wholly past Lq: empty range
+    b_rsrc = make_rsrc(a.bias_frag + s_idx * a.bf_sample_stride +
+                           (((int64_t)h * a.bf_nqt + (in ? qt : 0)) * a.bf_nkt) * 1024,
+                       in ? (uint32_t)(a.bf_nkt * 2048) : 0u);
 #pragma unroll
-  for (int t2 = 0; t2 < 2; ++t2)
+    for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
-      b_off[t2][c] = qv ? (uint32_t)((q_lane * b_si + 32 * t2 + 16 * c + g2 * 8) * 2) : kOut;
+      for (int c = 0; c < 2; ++c) b_off[t2][c] = (uint32_t)(((t2 * 2 + c) * 64 + lane) * 16);
+    b_step = 4096;
+  } else {
+    const T* bbase = HAS_BIAS ? a.bias + S.b_off + g * S.b_sg + h * S.b_sh : a.q;
+    b_rsrc = make_rsrc(bbase, HAS_BIAS ? (uint32_t)(((int64_t)(Lq - 1) * b_si + Lk) * 2) : 0u);
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        b_off[t2][c] = qv ? (uint32_t)((q_lane * b_si + 32 * t2 + 16 * c + g2 * 8) * 2) : kOut;
+    b_step = 128;
+  }
   float* dbrow = write_dbias && qv ? a.dbias + S.db_off + g * S.db_sg + h * S.db_sh + (int64_t)q_lane * S.db_si
                                    : nullptr;
 
@@ -392,7 +423,7 @@ __global__ __launch_bounds__(256, 2) void attn_dq_fast_kernel(BwdArgsT<T, T> a) 
     }
   };
   auto load_bias = [&](int t, uint4 (&bf)[2][2]) {
-    const uint32_t s = (uint32_t)(t * 64 * 2);
+    const uint32_t s = (uint32_t)t * b_step;
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
@@ -412,7 +443,10 @@ __global__ __launch_bounds__(256, 2) void attn_dq_fast_kernel(BwdArgsT<T, T> a) 
 #pragma unroll
   for (int t = 0; t < NDT; ++t) acc[t] = f32x16{};
 
-  auto compute = [&](int buf, int t, uint64_t bits, const uint4 (&bf)[2][2]) {
+  // MASKED: a tile with masked or out-of-range keys (P selected per score);
+  // fully kept tiles run the variant without any per-score mask work
+  auto compute = [&](auto masked, int buf, int t, uint64_t bits, const uint4 (&bf)[2][2]) {
+    constexpr bool MASKED = decltype(masked)::value;
     const T* kt = &k_lds[buf * TBUF];
     const T* vt = &v_lds[buf * TBUF];
     const uint64_t lb = bits >> (g2 * 4);
@@ -435,7 +469,7 @@ __global__ __launch_bounds__(256, 2) void attn_dq_fast_kernel(BwdArgsT<T, T> a) 
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j], c1, neg_lse));
-        if (bits != ~uint64_t(0)) {
+        if constexpr (MASKED) {
           const int kk = 32 * t2 + ((j >> 2) << 3) + (j & 3);
           p = ((lb >> kk) & 1) ? p : 0.0f;
         }
@@ -485,12 +519,15 @@ __global__ __launch_bounds__(256, 2) void attn_dq_fast_kernel(BwdArgsT<T, T> a) 
   int buf = 0;
   auto step = [&](uint4 (&bias_cur)[2][2]) {
     const int t3 = next_tile(t2);
-    const uint64_t bits = keep_lds[t0];
+    const uint64_t bits = uniform64(keep_lds[t0]);
     const int b1 = buf == 2 ? 0 : buf + 1;
     const int b2 = b1 == 2 ? 0 : b1 + 1;
     if (t2 < ntiles) store_kv(b2, ku, vu);
     load_kv(t3, ku, vu);
-    compute(buf, t0, bits, bias_cur);
+    if (bits == ~uint64_t(0))
+      compute(std::false_type{}, buf, t0, bits, bias_cur);
+    else
+      compute(std::true_type{}, buf, t0, bits, bias_cur);
     if constexpr (HAS_BIAS)
       load_bias(t2, bias_cur);
     lds_barrier();
@@ -702,31 +739,39 @@ __global__ __launch_bounds__(256, 2) void attn_dbias_fast_kernel(BwdArgsT<T, T> 
     load_stage(g_begin + i + 3, stg);
     const T* kt = &k_lds[buf * TBUF];
     const T* vt = &v_lds[buf * TBUF];
-    const uint64_t bits = keep_lds[buf];
+    const uint64_t bits = uniform64(keep_lds[buf]);
     const uint64_t lb = bits >> (g2 * 4);
     f32x16 nd;
     const float ndlt = -qc.dlt, nlse = -qc.lse;
 #pragma unroll
     for (int j = 0; j < 16; ++j) nd[j] = ndlt;
+    // fully kept tiles take the variant without per-score mask work
+    auto tile = [&](auto masked) {
+      constexpr bool MASKED = decltype(masked)::value;
 #pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2) {
-      f32x16 sacc = bacc[t2];
-      f32x16 pacc = nd;
+      for (int t2 = 0; t2 < 2; ++t2) {
+        f32x16 sacc = bacc[t2];
+        f32x16 pacc = nd;
 #pragma unroll
-      for (int s = 0; s < NQF; ++s) {
-        sacc = E::mma(lds_frag<T>(kt + (32 * t2 + lq) * LD + s * 16 + g2 * 8), qc.q[s], sacc);
-        pacc = E::mma(lds_frag<T>(vt + (32 * t2 + lq) * LD + s * 16 + g2 * 8), qc.d[s], pacc);
-      }
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j], c1, nlse));
-        if (bits != ~uint64_t(0)) {
-          const int kk = 32 * t2 + ((j >> 2) << 3) + (j & 3);
-          p = ((lb >> kk) & 1) ? p : 0.0f;
+        for (int s = 0; s < NQF; ++s) {
+          sacc = E::mma(lds_frag<T>(kt + (32 * t2 + lq) * LD + s * 16 + g2 * 8), qc.q[s], sacc);
+          pacc = E::mma(lds_frag<T>(vt + (32 * t2 + lq) * LD + s * 16 + g2 * 8), qc.d[s], pacc);
         }
-        acc[t2][j] = __builtin_fmaf(p, pacc[j], acc[t2][j]);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j], c1, nlse));
+          if constexpr (MASKED) {
+            const int kk = 32 * t2 + ((j >> 2) << 3) + (j & 3);
+            p = ((lb >> kk) & 1) ? p : 0.0f;
+          }
+          acc[t2][j] = __builtin_fmaf(p, pacc[j], acc[t2][j]);
+        }
       }
-    }
+    };
+    if (bits == ~uint64_t(0))
+      tile(std::false_type{});
+    else
+      tile(std::true_type{});
     load_q(g_begin + i + 2, qc);
     lds_barrier();
     buf = b1;
@@ -766,13 +811,7 @@ OOPS_BWD_FAST_INST(__bf16, 64)
 OOPS_BWD_FAST_INST(_Float16, 32)
 OOPS_BWD_FAST_INST(_Float16, 64)
 
-bool backward_fast_ok(const oops_attn_geometry& geo, const Plan& plan) {
-  if (geo.force_generic) return false;
-  if (geo.dtype == OOPS_F32 || plan.dp > 64 || plan.any_pair_mask || !geo.vec_ok || geo.head_size % 8 != 0 ||
-      !plan.offsets_32bit)
-    return false;
-  return !(geo.has_bias && geo.bias_dtype != geo.dtype);
-}
+bool backward_fast_ok(const oops_attn_geometry& geo, const Plan& plan) { return fast_path_ok(geo, plan); }
 
 template <typename F>
 hipError_t dispatch_fast(const oops_attn_geometry& geo, const Plan& plan, F&& f) {

@@ -275,11 +275,15 @@ OOPS_FOR_EACH_CONFIG(OOPS_FWD_INST)
 namespace oops {
 
 hipError_t launch_forward(const oops_attn_geometry& geo, const Plan& plan, const void* q, const void* k,
-                          const void* v, const uint8_t* mask, const void* bias, void* out, void* out_lo, float* lse,
-                          hipStream_t stream) {
+                          const void* v, const uint8_t* mask, const void* bias, void* bias_frag, void* out,
+                          void* out_lo, float* lse, hipStream_t stream) {
   hipError_t err = hipSuccess;
-  if (!geo.force_generic &&
-      launch_forward_fast(geo, plan, q, k, v, mask, bias, out, out_lo, lse, stream, &err))
+  if (plan.bias_frag) {
+    err = launch_bias_frag(geo, plan, bias, bias_frag, stream);
+    if (err != hipSuccess) return err;
+  }
+  if (launch_forward_fast(geo, plan, q, k, v, mask, bias, plan.bias_frag ? bias_frag : nullptr, out, out_lo, lse,
+                          stream, &err))
     return err;
   const bool ok = dispatch_config(geo.dtype, geo.bias_dtype, plan.dp, [&](auto t, auto bt, auto dpc) {
     using T = typename decltype(t)::type;
@@ -296,6 +300,9 @@ hipError_t launch_forward(const oops_attn_geometry& geo, const Plan& plan, const
     a.lse = lse;
     a.table = geo.table_device;
     a.uniform_tiles = plan.fwd_uniform;
+    a.bias_frag = nullptr;
+    a.bf_sample_stride = 0;
+    a.bf_nqt = a.bf_nkt = 0;
     a.num_samples = geo.num_samples;
     a.num_heads = geo.num_heads;
     a.head_size = geo.head_size;

@@ -145,15 +145,33 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fast_kernel(FwdArgsT<T, T> a)
     k_off[i] = col < D ? (uint32_t)((r * k_si + col) * 2) : kOut;
     v_off[i] = col < D ? (uint32_t)((r * v_si + col) * 2) : kOut;
   }
-  const T* bbase = HAS_BIAS ? a.bias + S.b_off + g * S.b_sg + h * S.b_sh : a.q;
-  const __amdgpu_buffer_rsrc_t b_rsrc =
-      make_rsrc(bbase, HAS_BIAS ? (uint32_t)(((int64_t)(Lq - 1) * b_si + Lk) * 2) : 0u);
-  uint32_t b_off[2][2];
+  // bias fragments: from the fragment-major copy of a shared bias (one
+  // contiguous 1 KB load per fragment), else from the bias rows themselves
+  const bool use_bf = HAS_BIAS && a.bias_frag != nullptr && S.bias_mode == OOPS_BIAS_SHARED;
+  __amdgpu_buffer_rsrc_t b_rsrc;
+  uint32_t b_off[2][2], b_step;
+  if (use_bf) {
+    const int qt = qb * 4 + wave;
+    // a wave wholly past Lq may index a tile row beyond the copy: empty range
+    const bool in = qt < a.bf_nqt;
+    b_rsrc = make_rsrc(a.bias_frag + s_idx * a.bf_sample_stride +
+                           (((int64_t)h * a.bf_nqt + (in ? qt : 0)) * a.bf_nkt) * 1024,
+                       in ? (uint32_t)(a.bf_nkt * 2048) : 0u);
 #pragma unroll
-  for (int t2 = 0; t2 < 2; ++t2)
+    for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
-      b_off[t2][c] = qv ? (uint32_t)((q_lane * b_si + 32 * t2 + 16 * c + g2 * 8) * 2) : kOut;
+      for (int c = 0; c < 2; ++c) b_off[t2][c] = (uint32_t)(((t2 * 2 + c) * 64 + lane) * 16);
+    b_step = 4096;
+  } else {
+    const T* bbase = HAS_BIAS ? a.bias + S.b_off + g * S.b_sg + h * S.b_sh : a.q;
+    b_rsrc = make_rsrc(bbase, HAS_BIAS ? (uint32_t)(((int64_t)(Lq - 1) * b_si + Lk) * 2) : 0u);
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        b_off[t2][c] = qv ? (uint32_t)((q_lane * b_si + 32 * t2 + 16 * c + g2 * 8) * 2) : kOut;
+    b_step = 128;
+  }
 
   // tile -> registers (K, V chunks of this thread; masked keys read zeros)
   // An absent tile (t >= ntiles) issues its loads with out-of-range offsets:
@@ -185,7 +203,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fast_kernel(FwdArgsT<T, T> a)
   // (the tile offset goes into the vector offset: the hardware range check
   // covers the vector offset, which keeps the last row's tail in bounds)
   auto load_bias = [&](int t, uint4 (&bf)[2][2]) {
-    const uint32_t s = (uint32_t)(t * 64 * 2);
+    const uint32_t s = (uint32_t)t * b_step;
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
@@ -375,13 +393,75 @@ OOPS_FWD_FAST_INST(__bf16, 64)
 OOPS_FWD_FAST_INST(_Float16, 32)
 OOPS_FWD_FAST_INST(_Float16, 64)
 
-bool launch_forward_fast(const oops_attn_geometry& geo, const Plan& plan, const void* q, const void* k,
-                         const void* v, const uint8_t* mask, const void* bias, void* out, void* out_lo,
-                         float* lse, hipStream_t stream, hipError_t* err) {
+bool fast_path_ok(const oops_attn_geometry& geo, const Plan& plan) {
+  if (geo.force_generic) return false;
   if (geo.dtype == OOPS_F32 || plan.dp > 64 || plan.max_len_k > 64 * kMaxKeyTiles || plan.any_pair_mask ||
       !geo.vec_ok || geo.head_size % 8 != 0 || !plan.offsets_32bit)
     return false;
-  if (geo.has_bias && geo.bias_dtype != geo.dtype) return false;
+  return !(geo.has_bias && geo.bias_dtype != geo.dtype);
+}
+
+// attn_bias_frag_kernel: the fragment-major copy of every shared bias.  For
+// sample s, head h, 32-query tile qt and 32-key tile kt the copy holds
+// 2 x 64 entries of 8 elements: entry (c, lane) = bias[qt*32 + lane%32]
+// [kt*32 + 16c + 8*(lane/32) .. +8], zero outside the sample.  These are
+// exactly the bias fragments of the fast kernels' identity MFMAs, so a wave
+// reads a fragment with one contiguous 1 KB load instead of 32 rows of
+// 32 bytes (which the L1 serves one row at a time).  One thread per entry.
+template <typename T>
+__global__ __launch_bounds__(256) void attn_bias_frag_kernel(const T* __restrict__ bias, T* __restrict__ bf,
+                                                             const int64_t* table, int num_samples, int H,
+                                                             int nqt, int nkt, int64_t sample_stride) {
+  const int64_t per_sample = (int64_t)H * nqt * nkt * 128;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= per_sample * num_samples) return;
+  const int s = (int)(i / per_sample);
+  int64_t r = i - (int64_t)s * per_sample;
+  const int lane = (int)(r & 63);
+  r >>= 6;
+  const int c = (int)(r & 1);
+  r >>= 1;
+  const int kt = (int)(r % nkt);
+  r /= nkt;
+  const int qt = (int)(r % nqt);
+  const int h = (int)(r / nqt);
+  const Sample& S = reinterpret_cast<const Sample*>(table)[s];
+  uint4 v = make_uint4(0, 0, 0, 0);
+  const int q = qt * 32 + (lane & 31);
+  const int k = kt * 32 + 16 * c + 8 * (lane >> 5);
+  if (S.bias_mode == OOPS_BIAS_SHARED && S.b_off >= 0 && q < S.Lq && k < S.Lk) {
+    const T* row = bias + S.b_off + h * S.b_sh + (int64_t)q * S.b_si;
+    if (k + 8 <= S.Lk) {
+      v = *reinterpret_cast<const uint4*>(row + k);
+    } else {
+      T e[8];
+      for (int j = 0; j < 8; ++j) e[j] = k + j < S.Lk ? row[k + j] : (T)0.0f;
+      v = __builtin_bit_cast(uint4, e);
+    }
+  }
+  const int64_t dst = (int64_t)s * sample_stride + ((((int64_t)h * nqt + qt) * nkt + kt) * 2 + c) * 512 + lane * 8;
+  *reinterpret_cast<uint4*>(bf + dst) = v;
+}
+
+hipError_t launch_bias_frag(const oops_attn_geometry& geo, const Plan& plan, const void* bias, void* bf,
+                            hipStream_t stream) {
+  const int64_t n = (int64_t)geo.num_samples * geo.num_heads * plan.bf_nqt * plan.bf_nkt * 128;
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (geo.dtype == OOPS_BF16)
+    hipLaunchKernelGGL(attn_bias_frag_kernel<__bf16>, grid, dim3(256), 0, stream, static_cast<const __bf16*>(bias),
+                       static_cast<__bf16*>(bf), geo.table_device, geo.num_samples, geo.num_heads, plan.bf_nqt,
+                       plan.bf_nkt, plan.bf_sample_stride);
+  else
+    hipLaunchKernelGGL(attn_bias_frag_kernel<_Float16>, grid, dim3(256), 0, stream,
+                       static_cast<const _Float16*>(bias), static_cast<_Float16*>(bf), geo.table_device,
+                       geo.num_samples, geo.num_heads, plan.bf_nqt, plan.bf_nkt, plan.bf_sample_stride);
+  return hipGetLastError();
+}
+
+bool launch_forward_fast(const oops_attn_geometry& geo, const Plan& plan, const void* q, const void* k,
+                         const void* v, const uint8_t* mask, const void* bias, const void* bias_frag, void* out,
+                         void* out_lo, float* lse, hipStream_t stream, hipError_t* err) {
+  if (!fast_path_ok(geo, plan)) return false;
   auto go = [&](auto tag, auto dpc) {
     using T = typename decltype(tag)::type;
     constexpr int DP = decltype(dpc)::value;
@@ -403,6 +483,10 @@ bool launch_forward_fast(const oops_attn_geometry& geo, const Plan& plan, const 
     a.scale = geo.scale;
     a.total_tiles = plan.fwd_tiles;
     a.head_group = head_group(geo);
+    a.bias_frag = static_cast<const T*>(bias_frag);
+    a.bf_sample_stride = plan.bf_sample_stride;
+    a.bf_nqt = plan.bf_nqt;
+    a.bf_nkt = plan.bf_nkt;
     const dim3 grid((unsigned)xcd_grid(plan.fwd_tiles));
     if (a.bias != nullptr)
       hipLaunchKernelGGL((attn_fwd_fast_kernel<T, DP, true>), grid, dim3(256), 0, stream, a);

@@ -25,6 +25,9 @@ struct FwdArgsT {
   int head_size;
   int vec_ok;
   float scale;
+  const T* bias_frag;        // fragment-major copy of the shared biases, or nullptr
+  int64_t bf_sample_stride;  // elements per sample in bias_frag
+  int bf_nqt, bf_nkt;        // 32-query / 32-key tiles per head in bias_frag
 };
 
 template <typename T, typename BT>
@@ -55,6 +58,9 @@ struct BwdArgsT {
   int parts;
   int head_group;
   float scale;
+  const T* bias_frag;        // as in FwdArgsT
+  int64_t bf_sample_stride;
+  int bf_nqt, bf_nkt;
 };
 
 }  // namespace oops
@@ -125,16 +131,30 @@ struct Plan {
   bool any_pair_mask = false;                    // a mask that depends on the query
   bool offsets_32bit = true;                     // every per-(group, head) K/V/bias block < 2 GiB
   int64_t max_len_q = 0, max_len_k = 0;
+  // fragment-major copy of the shared biases for the fast kernels (see attn_bias_frag_kernel)
+  bool bias_frag = false;
+  int bf_nqt = 0, bf_nkt = 0;   // 32-query / 32-key tiles per head (max over samples)
+  int64_t bf_sample_stride = 0; // elements per sample
+  size_t bf_bytes = 0;
 };
+
+// True when the 16-bit fast kernels serve this geometry (forward and backward).
+bool fast_path_ok(const oops_attn_geometry& geo, const Plan& plan);
+
+// Writes the fragment-major copy of every shared bias of the table into bf
+// (plan.bf_bytes bytes); see attn_bias_frag_kernel.
+hipError_t launch_bias_frag(const oops_attn_geometry& geo, const Plan& plan, const void* bias, void* bf,
+                            hipStream_t stream);
 
 // Fast paths (16-bit, head size <= 64); return false when the geometry is not covered.
 bool launch_forward_fast(const oops_attn_geometry& geo, const Plan& plan, const void* q, const void* k,
-                         const void* v, const uint8_t* mask, const void* bias, void* out, void* out_lo,
-                         float* lse, hipStream_t stream, hipError_t* err);
+                         const void* v, const uint8_t* mask, const void* bias, const void* bias_frag, void* out,
+                         void* out_lo, float* lse, hipStream_t stream, hipError_t* err);
 
+// bias_frag: plan.bf_bytes of device memory when plan.bias_frag (the copy is written here), else unused
 hipError_t launch_forward(const oops_attn_geometry& geo, const Plan& plan, const void* q, const void* k,
-                          const void* v, const uint8_t* mask, const void* bias, void* out, void* out_lo,
-                          float* lse, hipStream_t stream);
+                          const void* v, const uint8_t* mask, const void* bias, void* bias_frag, void* out,
+                          void* out_lo, float* lse, hipStream_t stream);
 
 // Device pointers of one backward call.
 struct BwdLaunch {
@@ -144,6 +164,7 @@ struct BwdLaunch {
   float* delta;
   void *dq, *dk, *dv;
   float *dbias, *dbias_part;
+  const void* bias_frag;  // fragment-major shared biases (fast kernels), or nullptr
 };
 
 int head_group_of(const oops_attn_geometry& geo);
@@ -176,6 +197,10 @@ inline void fill_bwd_args(BwdArgsT<T, BT>& a, const oops_attn_geometry& geo, con
   a.parts = plan.parts;
   a.head_group = head_group_of(geo);
   a.scale = geo.scale;
+  a.bias_frag = static_cast<const T*>(L.bias_frag);
+  a.bf_sample_stride = plan.bf_sample_stride;
+  a.bf_nqt = plan.bf_nqt;
+  a.bf_nkt = plan.bf_nkt;
 }
 
 bool backward_fast_ok(const oops_attn_geometry& geo, const Plan& plan);
@@ -187,6 +212,6 @@ hipError_t launch_dbias_fast(const oops_attn_geometry& geo, const Plan& plan, co
 hipError_t launch_backward(const oops_attn_geometry& geo, const Plan& plan, const void* q, const void* k,
                            const void* v, const uint8_t* mask, const void* bias, const void* out,
                            const void* out_lo, const float* lse, const void* dout, void* dq, void* dk, void* dv, float* dbias,
-                           float* delta, float* dbias_part, hipStream_t stream);
+                           float* delta, float* dbias_part, void* bias_frag, hipStream_t stream);
 
 }  // namespace oops

@@ -24,6 +24,7 @@ int fail(int code, const char* fmt, long long a = 0, long long b = 0) {
 constexpr int64_t kMaxGrid = (int64_t(1) << 31) - 1;
 constexpr int64_t kTargetSharedBiasBlocks = 2048;  // 8 workgroups per CU on 256 CUs
 constexpr int kMaxParts = 64;
+constexpr size_t kMaxBiasFragBytes = size_t(1) << 30;
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -146,36 +147,74 @@ int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
     if (plan.sbias_tiles > kMaxGrid || plan.sred_tiles > kMaxGrid)
       return fail(OOPS_EINVAL, "dBias launch grid exceeds 2^31-1 workgroups");
   }
+  // fragment-major copy of the shared biases for the fast kernels: one slab
+  // of H x ceil(Lq/32) x ceil(Lk/32) x 1024 elements per sample (the largest
+  // sample's extent, so a kernel finds its slab from the sample index alone)
+  if (geo->has_bias && plan.any_shared && oops::fast_path_ok(*geo, plan)) {
+    const int64_t nqt = cdiv(plan.max_len_q, 32), nkt = cdiv(plan.max_len_k, 32);
+    const int64_t stride = H * nqt * nkt * 1024;
+    const size_t bytes = (size_t)stride * (size_t)geo->num_samples * 2;
+    // a ragged batch whose slabs would far exceed its biases keeps the direct loads
+    if (bytes <= kMaxBiasFragBytes && (int64_t)geo->num_samples * H * nqt * nkt * 128 <= kMaxGrid * 256) {
+      plan.bias_frag = true;
+      plan.bf_nqt = (int)nqt;
+      plan.bf_nkt = (int)nkt;
+      plan.bf_sample_stride = stride;
+      plan.bf_bytes = bytes;
+    }
+  }
   return OOPS_OK;
 }
 
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
-size_t workspace_bytes(const oops::Plan& plan) {
-  size_t bytes = align256(sizeof(float) * (size_t)plan.lse_extent);
+// Backward workspace: delta [lse_extent f32] | dBias partial slabs | bias fragment copy.
+size_t parts_bytes(const oops::Plan& plan) {
   const int parts = std::max(plan.parts, plan.fast_parts);
-  if (plan.any_shared && parts > 1) bytes += align256(sizeof(float) * (size_t)parts * plan.dbias_extent);
-  return bytes;
+  return plan.any_shared && parts > 1 ? align256(sizeof(float) * (size_t)parts * plan.dbias_extent) : 0;
+}
+
+size_t workspace_bytes(const oops::Plan& plan) {
+  return align256(sizeof(float) * (size_t)plan.lse_extent) + parts_bytes(plan) + align256(plan.bf_bytes);
+}
+
+size_t forward_workspace_bytes(const oops::Plan& plan) { return align256(plan.bf_bytes); }
+
+int check_workspace(void* workspace, size_t ws_bytes, size_t need) {
+  if (need == 0) return OOPS_OK;
+  if (workspace == nullptr || ws_bytes < need)
+    return fail(OOPS_EWORKSPACE, "workspace of %lld bytes required, %lld given", (long long)need,
+                (long long)(workspace ? ws_bytes : 0));
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+    return fail(OOPS_EWORKSPACE, "workspace must be 256-byte aligned");
+  return OOPS_OK;
 }
 
 }  // namespace
 
 extern "C" {
 
-int oops_abi_version(void) { return 1; }
+int oops_abi_version(void) { return 2; }
 
 const char* oops_last_error(void) { return g_last_error.c_str(); }
 
+size_t oops_attn_forward_workspace_bytes(const oops_attn_geometry* geo) {
+  oops::Plan plan;
+  if (make_plan(geo, plan)) return 0;
+  return forward_workspace_bytes(plan);
+}
+
 int oops_attn_forward(const oops_attn_geometry* geo, const void* q, const void* k, const void* v,
-                      const uint8_t* mask, const void* bias, void* out, void* out_lo, float* lse,
-                      void* stream) {
+                      const uint8_t* mask, const void* bias, void* out, void* out_lo, float* lse, void* workspace,
+                      size_t ws_bytes, void* stream) {
   g_last_error.clear();
   oops::Plan plan;
   if (int rc = make_plan(geo, plan)) return rc;
   if (!q || !k || !v || !out) return fail(OOPS_EINVAL, "q, k, v and out must be non-NULL");
   if (geo->has_bias && !bias) return fail(OOPS_EINVAL, "has_bias is set but bias is NULL");
   if (geo->has_mask && !mask) return fail(OOPS_EINVAL, "has_mask is set but mask is NULL");
-  const hipError_t err = oops::launch_forward(*geo, plan, q, k, v, mask, bias, out, out_lo, lse,
+  if (int rc = check_workspace(workspace, ws_bytes, forward_workspace_bytes(plan))) return rc;
+  const hipError_t err = oops::launch_forward(*geo, plan, q, k, v, mask, bias, workspace, out, out_lo, lse,
                                               static_cast<hipStream_t>(stream));
   if (err != hipSuccess) {
     g_last_error = std::string("forward launch failed: ") + hipGetErrorString(err);
@@ -200,18 +239,14 @@ int oops_attn_backward(const oops_attn_geometry* geo, const void* q, const void*
   if (!q || !k || !v || !out || !lse || !dout) return fail(OOPS_EINVAL, "q, k, v, out, lse and dout must be non-NULL");
   if (geo->has_bias && !bias) return fail(OOPS_EINVAL, "has_bias is set but bias is NULL");
   if (geo->has_mask && !mask) return fail(OOPS_EINVAL, "has_mask is set but mask is NULL");
-  const size_t need = workspace_bytes(plan);
-  if (workspace == nullptr || ws_bytes < need)
-    return fail(OOPS_EWORKSPACE, "workspace of %lld bytes required, %lld given", (long long)need,
-                (long long)(workspace ? ws_bytes : 0));
-  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return fail(OOPS_EWORKSPACE, "workspace must be 256-byte aligned");
-  float* delta = static_cast<float*>(workspace);
-  float* parts = plan.any_shared && std::max(plan.parts, plan.fast_parts) > 1
-                     ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                                align256(sizeof(float) * (size_t)plan.lse_extent))
-                     : nullptr;
+  if (int rc = check_workspace(workspace, ws_bytes, workspace_bytes(plan))) return rc;
+  char* ws = static_cast<char*>(workspace);
+  float* delta = reinterpret_cast<float*>(ws);
+  const size_t delta_bytes = align256(sizeof(float) * (size_t)plan.lse_extent);
+  float* parts = parts_bytes(plan) ? reinterpret_cast<float*>(ws + delta_bytes) : nullptr;
+  void* bias_frag = plan.bias_frag ? ws + delta_bytes + parts_bytes(plan) : nullptr;
   const hipError_t err = oops::launch_backward(*geo, plan, q, k, v, mask, bias, out, out_lo, lse, dout, dq, dk, dv,
-                                               geo->has_bias ? dbias : nullptr, delta, parts,
+                                               geo->has_bias ? dbias : nullptr, delta, parts, bias_frag,
                                                static_cast<hipStream_t>(stream));
   if (err != hipSuccess) {
     g_last_error = std::string("backward launch failed: ") + hipGetErrorString(err);

@@ -87,8 +87,30 @@ def test_workspace_sizing(lib):
     # delta: one float per (group, head, query); then partial dBias slabs of H*N*N floats
     delta = 768 * 4 * 768 * 4
     slab = 4 * 768 * 768 * 4  # float32 partial dBias per part
-    parts, rest = divmod(ws - delta, slab)
+    frag = 4 * 768 * 768 * 2  # fragment-major bias copy (bf16)
+    parts, rest = divmod(ws - delta - frag, slab)
     assert rest == 0 and 2 <= parts <= 64, (ws, parts, rest)
+
+
+def test_forward_workspace_sizing(lib):
+    """A row-shared 16-bit bias gets a fragment-major copy: H x ceil(Lq/32)32 x ceil(Lk/32)32 elements."""
+
+    geo, keep = _geometry(c3_table())
+    ws = lib.oops_attn_forward_workspace_bytes(ctypes.byref(geo))
+    assert ws == 4 * 768 * 768 * 2
+    # the backward holds the same copy after delta and the partial slabs
+    bwd = lib.oops_attn_backward_workspace_bytes(ctypes.byref(geo))
+    assert (bwd - 768 * 4 * 768 * 4 - ws) % (4 * 768 * 768 * 4) == 0
+    # no copy for float32, without a bias, or on the generic kernels
+    for field, value in (("dtype", _lib.F32), ("has_bias", 0), ("force_generic", 1)):
+        geo2, keep2 = _geometry(c3_table())
+        setattr(geo2, field, value)
+        if field == "dtype":
+            geo2.bias_dtype = _lib.F32
+        assert lib.oops_attn_forward_workspace_bytes(ctypes.byref(geo2)) == 0, field
+    # a forward call without it is refused before anything is enqueued
+    assert lib.oops_attn_forward(ctypes.byref(geo), 1, 1, 1, None, 1, 1, None, 1, None, 0, None) == 3
+    assert "workspace" in lib.oops_last_error().decode()
 
 
 @pytest.mark.parametrize(
@@ -104,7 +126,7 @@ def test_workspace_sizing(lib):
 def test_geometry_validation(lib, field, value, message):
     geo, keep = _geometry(c3_table())
     setattr(geo, field, value)
-    rc = lib.oops_attn_forward(ctypes.byref(geo), 1, 1, 1, None, 1, 1, None, 1, None)
+    rc = lib.oops_attn_forward(ctypes.byref(geo), 1, 1, 1, None, 1, 1, None, 1, None, 0, None)
     assert rc == 1
     assert message in lib.oops_last_error().decode()
     assert lib.oops_attn_backward_workspace_bytes(ctypes.byref(geo)) == 0
@@ -117,17 +139,17 @@ def test_table_validation(lib):
     bad = list(row)
     bad[_lib.T_LEN_K] = 0
     geo, keep = _geometry(bad)
-    assert lib.oops_attn_forward(ctypes.byref(geo), 1, 1, 1, None, 1, 1, None, 1, None) == 1
+    assert lib.oops_attn_forward(ctypes.byref(geo), 1, 1, 1, None, 1, 1, None, 1, None, 0, None) == 1
     assert "empty axis" in lib.oops_last_error().decode()
     bad = list(row)
     bad[_lib.T_B_SG] = 5  # a shared bias with a group stride
     geo, keep = _geometry(bad)
-    assert lib.oops_attn_forward(ctypes.byref(geo), 1, 1, 1, None, 1, 1, None, 1, None) == 1
+    assert lib.oops_attn_forward(ctypes.byref(geo), 1, 1, 1, None, 1, 1, None, 1, None, 0, None) == 1
     assert "group stride 0" in lib.oops_last_error().decode()
     geo, keep = _geometry(row)
     geo.table_host = None
-    assert lib.oops_attn_forward(ctypes.byref(geo), 1, 1, 1, None, 1, 1, None, 1, None) == 1
-    assert lib.oops_attn_forward(None, 1, 1, 1, None, 1, 1, None, 1, None) == 1
+    assert lib.oops_attn_forward(ctypes.byref(geo), 1, 1, 1, None, 1, 1, None, 1, None, 0, None) == 1
+    assert lib.oops_attn_forward(None, 1, 1, 1, None, 1, 1, None, 1, None, 0, None) == 1
     assert "NULL" in lib.oops_last_error().decode()
     del _core
 
@@ -135,9 +157,9 @@ def test_table_validation(lib):
 def test_pointer_and_workspace_validation(lib):
     geo, keep = _geometry(c3_table())
     # NULL operands
-    assert lib.oops_attn_forward(ctypes.byref(geo), None, 1, 1, None, 1, 1, None, 1, None) == 1
+    assert lib.oops_attn_forward(ctypes.byref(geo), None, 1, 1, None, 1, 1, None, 1, None, 0, None) == 1
     # has_bias without a bias pointer
-    assert lib.oops_attn_forward(ctypes.byref(geo), 1, 1, 1, None, None, 1, None, 1, None) == 1
+    assert lib.oops_attn_forward(ctypes.byref(geo), 1, 1, 1, None, None, 1, None, 1, None, 0, None) == 1
     assert "bias" in lib.oops_last_error().decode()
     # too small a workspace
     rc = lib.oops_attn_backward(ctypes.byref(geo), 1, 1, 1, None, 1, 1, None, 1, 1, 1, 1, 1, 1, 256, 16, None)
