@@ -109,8 +109,8 @@ def kernel_times(q, k, v, bias, dout, iters=20):
     fwd = lambda: _core.attention_forward(qd, kd, vd, None, bd, table, H, scale, lse_numel, True)
     o, o_lo, lse = fwd()
     res = {"fwd": time_events(fwd, iters, 3, stream)}
-    for name, ph in (("delta", _lib.PHASE_DELTA), ("dq", _lib.PHASE_DQ), ("dkv", _lib.PHASE_DKV),
-                     ("dbias", _lib.PHASE_DBIAS)):  # fmt: skip
+    # dq includes delta = rowsum(O * dO), which the dQ kernel computes itself
+    for name, ph in (("dq", _lib.PHASE_DQ), ("dkv", _lib.PHASE_DKV), ("dbias", _lib.PHASE_DBIAS)):
 
         def bwd(ph=ph):
             with _core.profile_phases(ph):
@@ -125,7 +125,7 @@ def kernel_times(q, k, v, bias, dout, iters=20):
                                      [True, True, True, True])  # fmt: skip
 
     overhead = time_events(empty_bwd, iters, 3, stream)
-    for name in ("delta", "dq", "dkv", "dbias"):
+    for name in ("dq", "dkv", "dbias"):
         res[name] = max(res[name] - overhead, 1e-6)
     return res
 
@@ -154,7 +154,7 @@ def measured_traffic(kernel):
 
 
 # per-kernel MFMA work in units of 2*H*c*N^3 (one N x N x c GEMM per row and head)
-KERNEL_GEMMS = {"fwd": 2, "dq": 3, "dkv": 4, "dbias": 2, "delta": 0}
+KERNEL_GEMMS = {"fwd": 2, "dq": 3, "dkv": 4, "dbias": 2}
 
 
 def _median_ms(fn, iters=10, warmup=3):

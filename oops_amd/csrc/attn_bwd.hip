@@ -748,15 +748,18 @@ hipError_t launch_backward(const oops_attn_geometry& geo, const Plan& plan, cons
     auto check = [&]() {
       if (err == hipSuccess) err = hipGetLastError();
     };
-    if (phases & OOPS_PHASE_DELTA) {
+    const bool need_dq = dq != nullptr || (a.dbias != nullptr && plan.any_full);
+    const bool run_dq = (phases & OOPS_PHASE_DQ) && need_dq && plan.fwd_tiles > 0;
+    // the fast dQ kernel computes delta itself when it runs first
+    const bool fused_delta = fast && run_dq;
+    if ((phases & OOPS_PHASE_DELTA) && !fused_delta) {
       a.uniform_tiles = plan.delta_uniform;
       hipLaunchKernelGGL((attn_delta_kernel<T, BT, DP>), dim3((unsigned)plan.delta_tiles), block, 0, stream, a);
       check();
     }
-    const bool need_dq = dq != nullptr || (a.dbias != nullptr && plan.any_full);
-    if ((phases & OOPS_PHASE_DQ) && need_dq && plan.fwd_tiles > 0) {
+    if (run_dq) {
       if (fast) {
-        if (err == hipSuccess) err = launch_dq_fast(geo, plan, L, stream);
+        if (err == hipSuccess) err = launch_dq_fast(geo, plan, L, fused_delta, stream);
       } else {
         a.uniform_tiles = plan.fwd_uniform;
         hipLaunchKernelGGL((attn_dq_kernel<T, BT, DP>), dim3((unsigned)plan.fwd_tiles), block, 0, stream, a);

@@ -26,7 +26,7 @@ namespace oops {
 using namespace fast;
 
 template <typename T, int DP, bool HAS_BIAS>
-__global__ __launch_bounds__(256, 2) void attn_dkv_fast_kernel(BwdArgsT<T, T> a) {
+__global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArgsT<T, T> a) {
   using E = Elem<T>;
   using Frag = typename E::Frag;
   constexpr int LD = DP + 8;        // Q / dO tile row (elements)
@@ -278,7 +278,7 @@ __global__ __launch_bounds__(256, 2) void attn_dkv_fast_kernel(BwdArgsT<T, T> a)
 // per-group ("full") bias gets dBias = dS written from registers.
 // Reference: _backward_query (oops/attention/triangle/triton/kernel.py:428-565).
 template <typename T, int DP, bool HAS_BIAS>
-__global__ __launch_bounds__(256, 2) void attn_dq_fast_kernel(BwdArgsT<T, T> a) {
+__global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT<T, T> a) {
   using E = Elem<T>;
   using Frag = typename E::Frag;
   constexpr int LD = DP + 8;
@@ -348,9 +348,32 @@ __global__ __launch_bounds__(256, 2) void attn_dq_fast_kernel(BwdArgsT<T, T> a) 
   const float neg_lse = qv ? -a.lse[lidx] : 0.0f;
   f32x16 ndelta;
   {
-    const float nd = qv ? -a.delta[lidx] : 0.0f;
+    float dl;
+    if (a.delta_in_dq) {
+      // delta = rowsum((O + O_lo) * dO) over this lane's columns of dO, then
+      // the partner lane's (the other 32-lane half holds the other columns)
+      const int64_t o_row = S.o_off + g * S.o_sg + h * S.o_sh + (int64_t)q_lane * S.o_si;
+      const T* orow = a.out + o_row;
+      const T* lrow = a.out_lo != nullptr ? a.out_lo + o_row : nullptr;
+      float part = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) ndelta[j] = nd;
+      for (int s = 0; s < NQF; ++s) {
+        const int col = s * 16 + g2 * 8;
+        const bool ok = qv && col < D;
+        const uint4 ou = ok ? *reinterpret_cast<const uint4*>(orow + col) : make_uint4(0, 0, 0, 0);
+        const uint4 lu = ok && lrow ? *reinterpret_cast<const uint4*>(lrow + col) : make_uint4(0, 0, 0, 0);
+        const T* oe = reinterpret_cast<const T*>(&ou);
+        const T* le = reinterpret_cast<const T*>(&lu);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) part += (E::to_f(oe[i]) + E::to_f(le[i])) * E::to_f(df[s][i]);
+      }
+      dl = sum_halves(part);
+      if (g2 == 0 && qv) a.delta[lidx] = dl;
+    } else {
+      dl = qv ? a.delta[lidx] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) ndelta[j] = -dl;
   }
   Frag ident[2];
   identity_frags<T>(ident, 1.0f / a.scale, lane);
@@ -558,7 +581,7 @@ __global__ __launch_bounds__(256, 2) void attn_dq_fast_kernel(BwdArgsT<T, T> a) 
 // added by attn_dbias_reduce_kernel.
 // Reference: _backward_shared_bias (oops/attention/triangle/triton/kernel.py:721-873).
 template <typename T, int DP>
-__global__ __launch_bounds__(256, 2) void attn_dbias_fast_kernel(BwdArgsT<T, T> a) {
+__global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(BwdArgsT<T, T> a) {
   using E = Elem<T>;
   using Frag = typename E::Frag;
   constexpr int LD = DP + 8;
@@ -844,7 +867,8 @@ hipError_t launch_dkv_fast(const oops_attn_geometry& geo, const Plan& plan, cons
   });
 }
 
-hipError_t launch_dq_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L, hipStream_t stream) {
+hipError_t launch_dq_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L, bool delta_in_dq,
+                          hipStream_t stream) {
   return dispatch_fast(geo, plan, [&](auto tag, auto dpc) {
     using T = typename decltype(tag)::type;
     constexpr int DP = decltype(dpc)::value;
@@ -852,6 +876,7 @@ hipError_t launch_dq_fast(const oops_attn_geometry& geo, const Plan& plan, const
     fill_bwd_args(a, geo, plan, L);
     a.uniform_tiles = plan.fwd_uniform;
     a.total_tiles = plan.fwd_tiles;
+    a.delta_in_dq = delta_in_dq ? 1 : 0;
     const dim3 grid((unsigned)xcd_grid(plan.fwd_tiles));
     if (a.bias != nullptr)
       hipLaunchKernelGGL((attn_dq_fast_kernel<T, DP, true>), grid, dim3(256), 0, stream, a);

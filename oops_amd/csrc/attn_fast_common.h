@@ -3,6 +3,21 @@
 
 #include "attn_kernels.h"
 
+// Minimum workgroups per CU the fast kernels are compiled for (VGPR budget:
+// 512 / (4 x this) registers per lane).
+#ifndef OOPS_FWD_OCC
+#define OOPS_FWD_OCC 2
+#endif
+#ifndef OOPS_DQ_OCC
+#define OOPS_DQ_OCC 2
+#endif
+#ifndef OOPS_DKV_OCC
+#define OOPS_DKV_OCC 2
+#endif
+#ifndef OOPS_DBIAS_OCC
+#define OOPS_DBIAS_OCC 2
+#endif
+
 namespace oops {
 namespace fast {
 

@@ -46,7 +46,7 @@ using namespace fast;
 
 
 template <typename T, int DP, bool HAS_BIAS>
-__global__ __launch_bounds__(256, 2) void attn_fwd_fast_kernel(FwdArgsT<T, T> a) {
+__global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArgsT<T, T> a) {
   using E = Elem<T>;
   using Frag = typename E::Frag;
   using P2 = typename Pair<T>::v2;

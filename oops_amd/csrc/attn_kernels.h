@@ -61,6 +61,7 @@ struct BwdArgsT {
   const T* bias_frag;        // as in FwdArgsT
   int64_t bf_sample_stride;
   int bf_nqt, bf_nkt;
+  int delta_in_dq;           // fast dQ kernel computes delta (and stores it) instead of reading it
 };
 
 }  // namespace oops
@@ -201,11 +202,15 @@ inline void fill_bwd_args(BwdArgsT<T, BT>& a, const oops_attn_geometry& geo, con
   a.bf_sample_stride = plan.bf_sample_stride;
   a.bf_nqt = plan.bf_nqt;
   a.bf_nkt = plan.bf_nkt;
+  a.delta_in_dq = 0;
 }
 
 bool backward_fast_ok(const oops_attn_geometry& geo, const Plan& plan);
 hipError_t launch_dkv_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L, hipStream_t stream);
-hipError_t launch_dq_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L, hipStream_t stream);
+// delta_in_dq: the kernel computes delta = rowsum((O + O_lo) * dO) itself and stores it for the
+// later kernels (no separate delta pass)
+hipError_t launch_dq_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L, bool delta_in_dq,
+                          hipStream_t stream);
 hipError_t launch_dbias_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L,
                              hipStream_t stream);
 
