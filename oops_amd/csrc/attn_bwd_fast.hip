@@ -589,8 +589,14 @@ __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(Bw
   constexpr int NQF = DP / 16;
   constexpr int NCH = DP / 32;
 
+  // query side (Q, dO of the wave's 32 queries): loaded with whole-row
+  // coalesced loads, then turned into MFMA fragments through a per-wave LDS
+  // region (written and read by that wave only)
+  constexpr int QLD = DP + 8;
+  constexpr int NQR = DP / 16;  // 16-byte chunks per lane for 32 rows
   __shared__ __attribute__((aligned(16))) T k_lds[3 * TBUF];
   __shared__ __attribute__((aligned(16))) T v_lds[3 * TBUF];
+  __shared__ __attribute__((aligned(16))) T qw_lds[4 * 2 * 32 * QLD];
   __shared__ uint64_t keep_lds[3];
 
   const int tid = threadIdx.x;
@@ -599,6 +605,8 @@ __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(Bw
   const int lq = lane & 31;
   const int g2 = lane >> 5;
   const int P = a.parts;
+  T* const q_w = &qw_lds[wave * 2 * 32 * QLD];
+  T* const d_w = q_w + 32 * QLD;
 
   int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
   if (tile >= a.total_tiles) return;
@@ -674,8 +682,19 @@ __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(Bw
   const T* do_h = a.dout + S.do_off + h * S.do_sh;
   const uint32_t q_bytes_all = (uint32_t)(((int64_t)(Lq - 1) * S.q_si + D) * 2);
   const uint32_t do_bytes_all = (uint32_t)(((int64_t)(Lq - 1) * S.do_si + D) * 2);
-  const uint32_t q_lane_off = (uint32_t)(q_lane * (int)S.q_si * 2);
-  const uint32_t do_lane_off = (uint32_t)(q_lane * (int)S.do_si * 2);
+  // chunk i of this lane: row q_row[i] of the wave's 32 queries, columns q_col[i] .. +8
+  const int q0w = qb * 128 + wave * 32;
+  uint32_t q_ck_off[NQR], do_ck_off[NQR];
+  int q_row[NQR], q_col[NQR];
+#pragma unroll
+  for (int i = 0; i < NQR; ++i) {
+    const int c = i * 64 + lane;
+    q_row[i] = c / (DP / 8);
+    q_col[i] = (c % (DP / 8)) * 8;
+    const bool ok = q0w + q_row[i] < Lq && q_col[i] < D;
+    q_ck_off[i] = ok ? (uint32_t)(((q0w + q_row[i]) * (int)S.q_si + q_col[i]) * 2) : kOut;
+    do_ck_off[i] = ok ? (uint32_t)(((q0w + q_row[i]) * (int)S.do_si + q_col[i]) * 2) : kOut;
+  }
   const int64_t k_sg = S.k_sg, v_sg = S.v_sg, q_sg = S.q_sg, do_sg = S.do_sg;
   const float* l_h = a.lse + S.l_off + (int64_t)h * Lq;
   const float* d_h = a.delta + S.l_off + (int64_t)h * Lq;
@@ -714,29 +733,40 @@ __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(Bw
   // wave wait for the load at once.  Queries past Lq read zeros (their
   // scores then contribute P * (0 - 0) = 0 and are never written).
   struct QStage {
-    Frag q[NQF], d[NQF];
+    uint4 q[NQR], d[NQR];
     float lse, dlt;
   };
-  const uint32_t q_bytes = qv ? 16u * NQF : 0u;
   auto load_q = [&](int64_t g, QStage& qs) {
-    const bool live = qv && g < g_end;
-    const int64_t gg = g < g_end ? g : g_begin;
-    const __amdgpu_buffer_rsrc_t qr = make_rsrc(q_h + gg * q_sg, q_bytes_all);
-    const __amdgpu_buffer_rsrc_t dr = make_rsrc(do_h + gg * do_sg, do_bytes_all);
+    const bool live = g < g_end;
+    const int64_t gg = live ? g : g_begin;
+    const __amdgpu_buffer_rsrc_t qrs = make_rsrc(q_h + gg * q_sg, q_bytes_all);
+    const __amdgpu_buffer_rsrc_t drs = make_rsrc(do_h + gg * do_sg, do_bytes_all);
 #pragma unroll
-    for (int s = 0; s < NQF; ++s) {
-      const int col = s * 16 + g2 * 8;
-      const bool ok = live && col < D;
-      qs.q[s] = __builtin_bit_cast(Frag, buffer_load16(qr, ok ? q_lane_off + col * 2 : kOut));
-      qs.d[s] = __builtin_bit_cast(Frag, buffer_load16(dr, ok ? do_lane_off + col * 2 : kOut));
+    for (int i = 0; i < NQR; ++i) {
+      qs.q[i] = buffer_load16(qrs, live ? q_ck_off[i] : kOut);
+      qs.d[i] = buffer_load16(drs, live ? do_ck_off[i] : kOut);
     }
     const __amdgpu_buffer_rsrc_t lr = make_rsrc(l_h + gg * l_sg, (uint32_t)(Lq * 4));
     const __amdgpu_buffer_rsrc_t drr = make_rsrc(d_h + gg * l_sg, (uint32_t)(Lq * 4));
-    const uint32_t loff = live ? (uint32_t)(q_lane * 4) : kOut;
+    const uint32_t loff = live && qv ? (uint32_t)(q_lane * 4) : kOut;
     qs.lse = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(lr, loff, 0, 0));
     qs.dlt = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(drr, loff, 0, 0));
   };
-  (void)q_bytes;
+  // the wave's rows into its LDS region, then this lane's fragments back
+  // (LDS operations of one wave complete in order, so the region is free
+  // again once the fragments have been read)
+  auto q_frags = [&](const QStage& qs, Frag (&qf)[NQF], Frag (&df)[NQF]) {
+#pragma unroll
+    for (int i = 0; i < NQR; ++i) {
+      *reinterpret_cast<uint4*>(&q_w[q_row[i] * QLD + q_col[i]]) = qs.q[i];
+      *reinterpret_cast<uint4*>(&d_w[q_row[i] * QLD + q_col[i]]) = qs.d[i];
+    }
+#pragma unroll
+    for (int s = 0; s < NQF; ++s) {
+      qf[s] = lds_frag<T>(&q_w[lq * QLD + s * 16 + g2 * 8]);
+      df[s] = lds_frag<T>(&d_w[lq * QLD + s * 16 + g2 * 8]);
+    }
+  };
 
   const int64_t ng = g_end - g_begin;
   Stage stg;
@@ -764,6 +794,8 @@ __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(Bw
     const T* vt = &v_lds[buf * TBUF];
     const uint64_t bits = uniform64(keep_lds[buf]);
     const uint64_t lb = bits >> (g2 * 4);
+    Frag qf[NQF], df[NQF];
+    q_frags(qc, qf, df);
     f32x16 nd;
     const float ndlt = -qc.dlt, nlse = -qc.lse;
 #pragma unroll
@@ -777,8 +809,8 @@ __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(Bw
         f32x16 pacc = nd;
 #pragma unroll
         for (int s = 0; s < NQF; ++s) {
-          sacc = E::mma(lds_frag<T>(kt + (32 * t2 + lq) * LD + s * 16 + g2 * 8), qc.q[s], sacc);
-          pacc = E::mma(lds_frag<T>(vt + (32 * t2 + lq) * LD + s * 16 + g2 * 8), qc.d[s], pacc);
+          sacc = E::mma(lds_frag<T>(kt + (32 * t2 + lq) * LD + s * 16 + g2 * 8), qf[s], sacc);
+          pacc = E::mma(lds_frag<T>(vt + (32 * t2 + lq) * LD + s * 16 + g2 * 8), df[s], pacc);
         }
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
