@@ -259,11 +259,13 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
           sacc[t2][j] = ((lb >> kk) & 1) ? sacc[t2][j] : kNegInf;
         }
     }
-    float mx = sacc[0][0];
+    // tile max as a tree (short dependency chain), then across the halves
+    float m8[8];
 #pragma unroll
-    for (int j = 1; j < 16; ++j) mx = fmaxf(mx, sacc[0][j]);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) mx = fmaxf(mx, sacc[1][j]);
+    for (int i = 0; i < 8; ++i)
+      m8[i] = fmaxf(fmaxf(sacc[i >> 2][4 * (i & 3)], sacc[i >> 2][4 * (i & 3) + 1]),
+                    fmaxf(sacc[i >> 2][4 * (i & 3) + 2], sacc[i >> 2][4 * (i & 3) + 3]));
+    float mx = fmaxf(fmaxf(fmaxf(m8[0], m8[1]), fmaxf(m8[2], m8[3])), fmaxf(fmaxf(m8[4], m8[5]), fmaxf(m8[6], m8[7])));
     mx = max_halves(mx) * c1;
     const bool grow = mx > m_run + kLazyRescale;
     if (__any(grow)) {
@@ -275,6 +277,8 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
       for (int t = 0; t < NDT; ++t) oacc[t] *= alpha;
     }
     const float neg_m = m_run == kNegInf ? 0.0f : -m_run;
+    // row sum in four independent chains, added to l_run at the end
+    float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
@@ -285,7 +289,7 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
           P2 pr;
           pr[0] = (T)__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t2][8 * m + e], c1, neg_m));
           pr[1] = (T)__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t2][8 * m + e + 1], c1, neg_m));
-          l_run = Pair<T>::dot(pr, ones, l_run);
+          ls[e >> 1] = Pair<T>::dot(pr, ones, ls[e >> 1]);
           pf[e] = pr[0];
           pf[e + 1] = pr[1];
         }
@@ -295,6 +299,7 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
           oacc[t] = E::mma(vf, pf, oacc[t]);
         }
       }
+    l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
   };
 
   // ---- pipeline.  Step i (tile t0, LDS buffer i % 3):
@@ -314,7 +319,6 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
   }
   if (t1 < ntiles) {
     load_kv(t1, ku, vu);
-    if constexpr (HAS_BIAS) load_bias(t1, bias_b);
     store_kv(1, ku, vu);
   }
   load_kv(t2, ku, vu);
@@ -343,9 +347,12 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
       load_bias(t3, bias_nxt);
     attend(buf, bits, sacc_cur);
 #else
-    scores(buf, bias_cur, sacc_cur);
+    // one set of bias registers: the next tile's fragments are loaded as
+    // soon as this tile's bias MFMAs have read them
+    scores(buf, bias_a, sacc_cur);
     if constexpr (HAS_BIAS)
-      load_bias(t2, bias_cur);
+      load_bias(t1, bias_a);
+    (void)bias_cur;
     attend(buf, bits, sacc_cur);
 #endif
     lds_barrier();
