@@ -37,7 +37,7 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
 
   __shared__ __attribute__((aligned(16))) T q_lds[3 * TBUF];
   __shared__ __attribute__((aligned(16))) T do_lds[3 * TBUF];
-  __shared__ __attribute__((aligned(16))) float nlse_lds[3 * 64];  // -LSE, rows permuted
+  __shared__ __attribute__((aligned(16))) float nlse_lds[3 * 64];  // -LSE / c1, rows permuted
   __shared__ __attribute__((aligned(16))) float ndlt_lds[3 * 64];  // -delta, rows permuted
 
   const int tid = threadIdx.x;
@@ -148,6 +148,8 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
       st.dlt = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(d_rsrc, off, 0, 0));
     }
   };
+  // -LSE is the S accumulator's input, in units of the unscaled scores
+  const float inv_c1 = 1.0f / (a.scale * kLog2e);
   auto store_stage = [&](int buf, const Stage& st) {
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
@@ -159,7 +161,7 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
     }
     if (tid < 64) {
       const int pos = (tid & 32) + perm32(tid & 31);
-      nlse_lds[buf * 64 + pos] = -st.lse;
+      nlse_lds[buf * 64 + pos] = -st.lse * inv_c1;
       ndlt_lds[buf * 64 + pos] = -st.dlt;
     }
   };
@@ -175,12 +177,11 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
     const T* dt = &do_lds[buf * TBUF];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      f32x16 sacc;
+      // S - LSE / c1: the accumulator starts from -LSE / c1
+      f32x16 sacc = *reinterpret_cast<const f32x16*>(&nlse_lds[buf * 64 + 32 * r + g2 * 16]);
       if constexpr (HAS_BIAS) {
-        sacc = E::mma(__builtin_bit_cast(Frag, bias[r][0]), ident[0], f32x16{});
+        sacc = E::mma(__builtin_bit_cast(Frag, bias[r][0]), ident[0], sacc);
         sacc = E::mma(__builtin_bit_cast(Frag, bias[r][1]), ident[1], sacc);
-      } else {
-        sacc = f32x16{};
       }
       f32x16 pacc = *reinterpret_cast<const f32x16*>(&ndlt_lds[buf * 64 + 32 * r + g2 * 16]);
 #pragma unroll
@@ -188,11 +189,10 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
         sacc = E::mma(lds_frag<T>(qt + (32 * r + lq) * LD + s * 16 + g2 * 8), kf[s], sacc);
         pacc = E::mma(lds_frag<T>(dt + (32 * r + lq) * LD + s * 16 + g2 * 8), vf[s], pacc);
       }
-      const f32x16 nlse = *reinterpret_cast<const f32x16*>(&nlse_lds[buf * 64 + 32 * r + g2 * 16]);
       float p[16], ds[16];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j], c1, nlse[j]));
+        p[j] = __builtin_amdgcn_exp2f(sacc[j] * c1);
         if (wave_masked) p[j] = kvalid ? p[j] : 0.0f;
         ds[j] = p[j] * pacc[j];
       }
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
   // ---- pipeline: step i computes buffer i % 3; the stage of step i+2
   // (loaded during step i-1) is written at the top of step i.
   Stage stg;
-  uint4 bias_a[2][2], bias_b[2][2];
+  uint4 bias_a[2][2];
   if (nsteps > 0) {
     load_stage(0, stg);
     if constexpr (HAS_BIAS) load_bias(0, bias_a);
@@ -233,7 +233,7 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
   }
   if (nsteps > 1) {
     load_stage(1, stg);
-    if constexpr (HAS_BIAS) load_bias(1, bias_b);
+
     store_stage(1, stg);
   }
   load_stage(2, stg);
@@ -247,14 +247,14 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
     load_stage(i + 3, stg);
     compute(buf, i * 64, bias_cur);
     if constexpr (HAS_BIAS)
-      load_bias(i + 2, bias_cur);
+      load_bias(i + 1, bias_cur);  // one register set: the next step's bias
     lds_barrier();
     buf = b1;
   };
   for (int i = 0; i < nsteps; i += 2) {
     step(i, bias_a);
     if (i + 1 >= nsteps) break;
-    step(i + 1, bias_b);
+    step(i + 1, bias_a);
   }
 
   // ---- write dK = scale * dK^T^T, dV (zero for masked keys)
