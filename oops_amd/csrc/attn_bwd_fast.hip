@@ -25,7 +25,7 @@ namespace oops {
 
 using namespace fast;
 
-template <typename T, int DP, bool HAS_BIAS>
+template <typename T, int DP, bool HAS_BIAS, int R>
 __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArgsT<T, T> a) {
   using E = Elem<T>;
   using Frag = typename E::Frag;
@@ -35,10 +35,10 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
   constexpr int NQF = DP / 16;
   constexpr int NCH = DP / 32;      // 16-byte chunks of Q (and dO) per thread per step
 
-  __shared__ __attribute__((aligned(16))) T q_lds[3 * TBUF];
-  __shared__ __attribute__((aligned(16))) T do_lds[3 * TBUF];
-  __shared__ __attribute__((aligned(16))) float nlse_lds[3 * 64];  // -LSE / c1, rows permuted
-  __shared__ __attribute__((aligned(16))) float ndlt_lds[3 * 64];  // -delta, rows permuted
+  __shared__ __attribute__((aligned(16))) T q_lds[3 * R * TBUF];
+  __shared__ __attribute__((aligned(16))) T do_lds[3 * R * TBUF];
+  __shared__ __attribute__((aligned(16))) float nlse_lds[3 * R * 64];  // -LSE / c1, rows permuted
+  __shared__ __attribute__((aligned(16))) float ndlt_lds[3 * R * 64];  // -delta, rows permuted
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -46,16 +46,19 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
   const int lq = lane & 31;
   const int g2 = lane >> 5;
 
-  // XCD-aware order (see attn_fwd_fast.hip): logical (head group, g, head, key block)
+  // XCD-aware order (see attn_fwd_fast.hip): logical (head group, row block,
+  // head, key block); a row block is R consecutive groups g that share the
+  // bias, so each bias fragment loaded serves R rows
   int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
   if (tile >= a.total_tiles) return;
   const Sample* tab = reinterpret_cast<const Sample*>(a.table);
   const int H = a.num_heads;
   const int s_idx = find_sample(tile, tab, a.num_samples, a.uniform_tiles,
-                                [&](const Sample& s) { return s.G * H * cdiv(s.Lk, 128); });
+                                [&](const Sample& s) { return cdiv(s.G, R) * H * cdiv(s.Lk, 128); });
   if (s_idx < 0) return;
   const Sample& S = tab[__builtin_amdgcn_readfirstlane(s_idx)];
   const int64_t G = S.G;
+  const int64_t GB = cdiv(G, R);
   const int Lq = (int)S.Lq, Lk = (int)S.Lk;
   const int nkb = (int)cdiv(Lk, 128);
   const int HG = a.head_group;
@@ -63,40 +66,57 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
   int64_t rest = tile / nkb;
   const int hh = (int)(rest % HG);
   rest /= HG;
-  const int g = (int)(rest % G);
-  const int h = (int)(rest / G) * HG + hh;
+  const int g0 = (int)(rest % GB) * R;
+  const int h = (int)(rest / GB) * HG + hh;
   const int D = a.head_size;
   const int q_si = (int)S.q_si, do_si = (int)S.do_si, b_si = (int)S.b_si;
   const int nsteps = (Lq + 63) >> 6;
+  bool row_ok[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) row_ok[r] = g0 + r < G;
 
-  // ---- this lane's key: K, V fragments (B operands: lane = key, k = head dim)
+  // ---- this lane's key: K, V fragments of each row (B operands: lane = key, k = head dim)
   const int key = kb * 128 + wave * 32 + lq;
-  bool kvalid = key < Lk;
   const bool has_mask = a.mask != nullptr && S.m_off >= 0;
-  if (kvalid && has_mask) kvalid = a.mask[S.m_off + g * S.m_sg + key] != 0;
-  const bool wave_masked = __any(!kvalid);
-  Frag kf[NQF], vf[NQF];
-  {
-    const T* kbase = a.k + S.k_off + g * S.k_sg + h * S.k_sh;
-    const T* vbase = a.v + S.v_off + g * S.v_sg + h * S.v_sh;
+  bool kvalid[R], wave_masked[R];
+  Frag kf[R][NQF], vf[R][NQF];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int g = g0 + r;
+    bool kv = row_ok[r] && key < Lk;
+    if (kv && has_mask) kv = a.mask[S.m_off + g * S.m_sg + key] != 0;
+    kvalid[r] = kv;
+    wave_masked[r] = __any(!kv);
+    const T* kbase = a.k + S.k_off + (row_ok[r] ? g : g0) * S.k_sg + h * S.k_sh;
+    const T* vbase = a.v + S.v_off + (row_ok[r] ? g : g0) * S.v_sg + h * S.v_sh;
     const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kbase, (uint32_t)(((int64_t)(Lk - 1) * S.k_si + D) * 2));
     const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vbase, (uint32_t)(((int64_t)(Lk - 1) * S.v_si + D) * 2));
 #pragma unroll
     for (int s = 0; s < NQF; ++s) {
       const int col = s * 16 + g2 * 8;
-      const bool ok = kvalid && col < D;
-      kf[s] = __builtin_bit_cast(Frag, buffer_load16(k_rsrc, ok ? (uint32_t)((key * (int)S.k_si + col) * 2) : kOut));
-      vf[s] = __builtin_bit_cast(Frag, buffer_load16(v_rsrc, ok ? (uint32_t)((key * (int)S.v_si + col) * 2) : kOut));
+      const bool ok = kv && col < D;
+      kf[r][s] = __builtin_bit_cast(Frag, buffer_load16(k_rsrc, ok ? (uint32_t)((key * (int)S.k_si + col) * 2) : kOut));
+      vf[r][s] = __builtin_bit_cast(Frag, buffer_load16(v_rsrc, ok ? (uint32_t)((key * (int)S.v_si + col) * 2) : kOut));
     }
   }
   Frag ident[2];
   identity_frags<T>(ident, 1.0f / a.scale, lane);
 
   // ---- per-thread staging offsets (bytes); the step adds q0 * stride via soffset
-  const T* qbase = a.q + S.q_off + g * S.q_sg + h * S.q_sh;
-  const T* dobase = a.dout + S.do_off + g * S.do_sg + h * S.do_sh;
-  const __amdgpu_buffer_rsrc_t q_rsrc = make_rsrc(qbase, (uint32_t)(((int64_t)(Lq - 1) * q_si + D) * 2));
-  const __amdgpu_buffer_rsrc_t do_rsrc = make_rsrc(dobase, (uint32_t)(((int64_t)(Lq - 1) * do_si + D) * 2));
+  __amdgpu_buffer_rsrc_t q_rsrc[R], do_rsrc[R], l_rsrc[R], d_rsrc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    // a row past G (odd G) reads nothing: empty ranges
+    const int g = row_ok[r] ? g0 + r : g0;
+    const uint32_t live = row_ok[r] ? 1u : 0u;
+    q_rsrc[r] = make_rsrc(a.q + S.q_off + g * S.q_sg + h * S.q_sh, live * (uint32_t)(((int64_t)(Lq - 1) * q_si + D) * 2));
+    do_rsrc[r] =
+        make_rsrc(a.dout + S.do_off + g * S.do_sg + h * S.do_sh, live * (uint32_t)(((int64_t)(Lq - 1) * do_si + D) * 2));
+    // LSE / delta rows: rows past Lq read 0; they contribute nothing because
+    // their dO (and Q) rows read as zero, so dS = P * (0 - 0) = 0
+    l_rsrc[r] = make_rsrc(a.lse + S.l_off + ((int64_t)g * H + h) * Lq, live * (uint32_t)(Lq * 4));
+    d_rsrc[r] = make_rsrc(a.delta + S.l_off + ((int64_t)g * H + h) * Lq, live * (uint32_t)(Lq * 4));
+  }
   uint32_t st_row[NCH], q_off[NCH], do_off[NCH];
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
@@ -107,14 +127,10 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
     q_off[i] = col < D ? (uint32_t)((r * q_si + col) * 2) : kOut;
     do_off[i] = col < D ? (uint32_t)((r * do_si + col) * 2) : kOut;
   }
-  // LSE / delta rows: rows past Lq read 0; they contribute nothing because
-  // their dO (and Q) rows read as zero, so dS = P * (0 - 0) = 0
-  const __amdgpu_buffer_rsrc_t l_rsrc = make_rsrc(a.lse + S.l_off + ((int64_t)g * H + h) * Lq, (uint32_t)(Lq * 4));
-  const __amdgpu_buffer_rsrc_t d_rsrc =
-      make_rsrc(a.delta + S.l_off + ((int64_t)g * H + h) * Lq, (uint32_t)(Lq * 4));
   // bias rows of this wave's keys: A fragments (lane = query, 8 consecutive
   // keys), from the fragment-major copy of a shared bias (one contiguous
-  // 1 KB load per fragment) or from the bias rows themselves
+  // 1 KB load per fragment) or from the bias rows themselves; with R > 1 the
+  // bias is shared by the rows (the host picks R > 1 only then)
   const int kw = kb * 128 + wave * 32;  // first key of this wave
   const bool use_bf = HAS_BIAS && a.bias_frag != nullptr && S.bias_mode == OOPS_BIAS_SHARED;
   __amdgpu_buffer_rsrc_t b_rsrc;
@@ -125,99 +141,111 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
                            (in ? kt : 0) * 1024,
                        in ? (uint32_t)(((int64_t)a.bf_nqt * a.bf_nkt - (in ? kt : 0)) * 2048) : 0u);
   } else {
-    const T* bbase = HAS_BIAS ? a.bias + S.b_off + g * S.b_sg + h * S.b_sh : a.q;
+    const T* bbase = HAS_BIAS ? a.bias + S.b_off + g0 * S.b_sg + h * S.b_sh : a.q;
     b_rsrc = make_rsrc(bbase, HAS_BIAS ? (uint32_t)(((int64_t)(Lq - 1) * b_si + Lk) * 2) : 0u);
   }
 
   struct Stage {
-    uint4 q[NCH], d[NCH];
-    float lse, dlt;
+    uint4 q[R][NCH], d[R][NCH];
+    float lse[R], dlt[R];
   };
   auto load_stage = [&](int step, Stage& st) {
     const int q0 = step * 64;
     const uint32_t qs = (uint32_t)(q0 * q_si * 2), ds = (uint32_t)(q0 * do_si * 2);
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      const bool ok = q0 + (int)st_row[i] < Lq;
-      st.q[i] = buffer_load16_s(q_rsrc, ok ? q_off[i] : kOut, qs);
-      st.d[i] = buffer_load16_s(do_rsrc, ok ? do_off[i] : kOut, ds);
-    }
-    if (tid < 64) {
-      const uint32_t off = (uint32_t)((q0 + tid) * 4);  // range-checked: rows past Lq read 0
-      st.lse = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(l_rsrc, off, 0, 0));
-      st.dlt = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(d_rsrc, off, 0, 0));
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        const bool ok = q0 + (int)st_row[i] < Lq;
+        st.q[r][i] = buffer_load16_s(q_rsrc[r], ok ? q_off[i] : kOut, qs);
+        st.d[r][i] = buffer_load16_s(do_rsrc[r], ok ? do_off[i] : kOut, ds);
+      }
+      if (tid < 64) {
+        const uint32_t off = (uint32_t)((q0 + tid) * 4);  // range-checked: rows past Lq read 0
+        st.lse[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(l_rsrc[r], off, 0, 0));
+        st.dlt[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(d_rsrc[r], off, 0, 0));
+      }
     }
   };
   // -LSE is the S accumulator's input, in units of the unscaled scores
   const float inv_c1 = 1.0f / (a.scale * kLog2e);
   auto store_stage = [&](int buf, const Stage& st) {
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      const int c = tid + 256 * i;
-      const int r = c / (DP / 8);
-      const int col = (c % (DP / 8)) * 8;
-      *reinterpret_cast<uint4*>(&q_lds[buf * TBUF + r * LD + col]) = st.q[i];
-      *reinterpret_cast<uint4*>(&do_lds[buf * TBUF + r * LD + col]) = st.d[i];
-    }
-    if (tid < 64) {
-      const int pos = (tid & 32) + perm32(tid & 31);
-      nlse_lds[buf * 64 + pos] = -st.lse * inv_c1;
-      ndlt_lds[buf * 64 + pos] = -st.dlt;
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        const int c = tid + 256 * i;
+        const int row = c / (DP / 8);
+        const int col = (c % (DP / 8)) * 8;
+        *reinterpret_cast<uint4*>(&q_lds[(buf * R + r) * TBUF + row * LD + col]) = st.q[r][i];
+        *reinterpret_cast<uint4*>(&do_lds[(buf * R + r) * TBUF + row * LD + col]) = st.d[r][i];
+      }
+      if (tid < 64) {
+        const int pos = (tid & 32) + perm32(tid & 31);
+        nlse_lds[(buf * R + r) * 64 + pos] = -st.lse[r] * inv_c1;
+        ndlt_lds[(buf * R + r) * 64 + pos] = -st.dlt[r];
+      }
     }
   };
 
   const float c1 = a.scale * kLog2e;
-  f32x16 dk[NDT], dv[NDT];
+  f32x16 dk[R][NDT], dv[R][NDT];
 #pragma unroll
-  for (int t = 0; t < NDT; ++t) dk[t] = dv[t] = f32x16{};
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) dk[r][t] = dv[r][t] = f32x16{};
 
-  // one step: two 32-query row tiles of LDS buffer buf against this wave's keys
-  auto compute = [&](int buf, int q0, const uint4 (&bias)[2][2]) {
-    const T* qt = &q_lds[buf * TBUF];
-    const T* dt = &do_lds[buf * TBUF];
+  // one step: for each row, two 32-query tiles of LDS buffer buf against this wave's keys
+  auto compute = [&](int buf, const uint4 (&bias)[2][2]) {
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      // S - LSE / c1: the accumulator starts from -LSE / c1
-      f32x16 sacc = *reinterpret_cast<const f32x16*>(&nlse_lds[buf * 64 + 32 * r + g2 * 16]);
-      if constexpr (HAS_BIAS) {
-        sacc = E::mma(__builtin_bit_cast(Frag, bias[r][0]), ident[0], sacc);
-        sacc = E::mma(__builtin_bit_cast(Frag, bias[r][1]), ident[1], sacc);
-      }
-      f32x16 pacc = *reinterpret_cast<const f32x16*>(&ndlt_lds[buf * 64 + 32 * r + g2 * 16]);
+    for (int r = 0; r < R; ++r) {
+      if (!row_ok[r]) continue;
+      const T* qt = &q_lds[(buf * R + r) * TBUF];
+      const T* dt = &do_lds[(buf * R + r) * TBUF];
 #pragma unroll
-      for (int s = 0; s < NQF; ++s) {
-        sacc = E::mma(lds_frag<T>(qt + (32 * r + lq) * LD + s * 16 + g2 * 8), kf[s], sacc);
-        pacc = E::mma(lds_frag<T>(dt + (32 * r + lq) * LD + s * 16 + g2 * 8), vf[s], pacc);
-      }
-      float p[16], ds[16];
+      for (int qr = 0; qr < 2; ++qr) {
+        // S - LSE / c1: the accumulator starts from -LSE / c1
+        f32x16 sacc = *reinterpret_cast<const f32x16*>(&nlse_lds[(buf * R + r) * 64 + 32 * qr + g2 * 16]);
+        if constexpr (HAS_BIAS) {
+          sacc = E::mma(__builtin_bit_cast(Frag, bias[qr][0]), ident[0], sacc);
+          sacc = E::mma(__builtin_bit_cast(Frag, bias[qr][1]), ident[1], sacc);
+        }
+        f32x16 pacc = *reinterpret_cast<const f32x16*>(&ndlt_lds[(buf * R + r) * 64 + 32 * qr + g2 * 16]);
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        p[j] = __builtin_amdgcn_exp2f(sacc[j] * c1);
-        if (wave_masked) p[j] = kvalid ? p[j] : 0.0f;
-        ds[j] = p[j] * pacc[j];
-      }
+        for (int s = 0; s < NQF; ++s) {
+          sacc = E::mma(lds_frag<T>(qt + (32 * qr + lq) * LD + s * 16 + g2 * 8), kf[r][s], sacc);
+          pacc = E::mma(lds_frag<T>(dt + (32 * qr + lq) * LD + s * 16 + g2 * 8), vf[r][s], pacc);
+        }
+        float p[16], ds[16];
 #pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const Frag pf = pack8<T>(&p[8 * m]);
-        const Frag sf = pack8<T>(&ds[8 * m]);
+        for (int j = 0; j < 16; ++j) {
+          p[j] = __builtin_amdgcn_exp2f(sacc[j] * c1);
+          if (wave_masked[r]) p[j] = kvalid[r] ? p[j] : 0.0f;
+          ds[j] = p[j] * pacc[j];
+        }
 #pragma unroll
-        for (int t = 0; t < NDT; ++t) {
-          dv[t] = E::mma(lds_read_tr_frag<T>(dt, LD, 32 * r + 16 * m, 32 * t, lane), pf, dv[t]);
-          dk[t] = E::mma(lds_read_tr_frag<T>(qt, LD, 32 * r + 16 * m, 32 * t, lane), sf, dk[t]);
+        for (int m = 0; m < 2; ++m) {
+          const Frag pf = pack8<T>(&p[8 * m]);
+          const Frag sf = pack8<T>(&ds[8 * m]);
+#pragma unroll
+          for (int t = 0; t < NDT; ++t) {
+            dv[r][t] = E::mma(lds_read_tr_frag<T>(dt, LD, 32 * qr + 16 * m, 32 * t, lane), pf, dv[r][t]);
+            dk[r][t] = E::mma(lds_read_tr_frag<T>(qt, LD, 32 * qr + 16 * m, 32 * t, lane), sf, dk[r][t]);
+          }
         }
       }
     }
   };
   auto load_bias = [&](int step, uint4 (&bias)[2][2]) {
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int q = step * 64 + 32 * r + lq;
+    for (int qr = 0; qr < 2; ++qr) {
+      const int q = step * 64 + 32 * qr + lq;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        // fragment copy: tile row qt = 2 step + r, entry (c, lane); rows past the copy read 0
-        const uint32_t off = use_bf ? (uint32_t)((((2 * step + r) * a.bf_nkt * 2 + c) * 64 + lane) * 16)
+        // fragment copy: tile row qt = 2 step + qr, entry (c, lane); rows past the copy read 0
+        const uint32_t off = use_bf ? (uint32_t)((((2 * step + qr) * a.bf_nkt * 2 + c) * 64 + lane) * 16)
                                     : (q < Lq ? (uint32_t)((q * b_si + kw + 16 * c + g2 * 8) * 2) : kOut);
-        bias[r][c] = buffer_load16_s(b_rsrc, off, 0);
+        bias[qr][c] = buffer_load16_s(b_rsrc, off, 0);
       }
     }
   };
@@ -225,47 +253,44 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
   // ---- pipeline: step i computes buffer i % 3; the stage of step i+2
   // (loaded during step i-1) is written at the top of step i.
   Stage stg;
-  uint4 bias_a[2][2];
+  uint4 bias_r[2][2];
   if (nsteps > 0) {
     load_stage(0, stg);
-    if constexpr (HAS_BIAS) load_bias(0, bias_a);
+    if constexpr (HAS_BIAS) load_bias(0, bias_r);
     store_stage(0, stg);
   }
   if (nsteps > 1) {
     load_stage(1, stg);
-
     store_stage(1, stg);
   }
   load_stage(2, stg);
   vmem_wait_all();
   __syncthreads();
   int buf = 0;
-  auto step = [&](int i, uint4 (&bias_cur)[2][2]) {
+  for (int i = 0; i < nsteps; ++i) {
     const int b1 = buf == 2 ? 0 : buf + 1;
     const int b2 = b1 == 2 ? 0 : b1 + 1;
     if (i + 2 < nsteps) store_stage(b2, stg);
     load_stage(i + 3, stg);
-    compute(buf, i * 64, bias_cur);
+    compute(buf, bias_r);
     if constexpr (HAS_BIAS)
-      load_bias(i + 1, bias_cur);  // one register set: the next step's bias
+      load_bias(i + 1, bias_r);  // one register set: the next step's bias
     lds_barrier();
     buf = b1;
-  };
-  for (int i = 0; i < nsteps; i += 2) {
-    step(i, bias_a);
-    if (i + 1 >= nsteps) break;
-    step(i + 1, bias_a);
   }
 
   // ---- write dK = scale * dK^T^T, dV (zero for masked keys)
-  if (key < Lk) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (!row_ok[r] || key >= Lk) continue;
+    const int g = g0 + r;
     T* krow = a.dk ? a.dk + S.k_off + g * S.k_sg + h * S.k_sh + (int64_t)key * S.k_si : nullptr;
     T* vrow = a.dv ? a.dv + S.v_off + g * S.v_sg + h * S.v_sh + (int64_t)key * S.v_si : nullptr;
-    const float ks = kvalid ? a.scale : 0.0f, vs = kvalid ? 1.0f : 0.0f;
+    const float ks = kvalid[r] ? a.scale : 0.0f, vs = kvalid[r] ? 1.0f : 0.0f;
 #pragma unroll
     for (int t = 0; t < NDT; ++t) {
-      if (krow) store_tile<T>(krow, t * 32, D, g2, dk[t], ks);
-      if (vrow) store_tile<T>(vrow, t * 32, D, g2, dv[t], vs);
+      if (krow) store_tile<T>(krow, t * 32, D, g2, dk[r][t], ks);
+      if (vrow) store_tile<T>(vrow, t * 32, D, g2, dv[r][t], vs);
     }
   }
 }
@@ -856,8 +881,9 @@ __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(Bw
 }
 
 #define OOPS_BWD_FAST_INST(T, DP)                                                \
-  template __global__ void attn_dkv_fast_kernel<T, DP, true>(BwdArgsT<T, T>);  \
-  template __global__ void attn_dkv_fast_kernel<T, DP, false>(BwdArgsT<T, T>); \
+  template __global__ void attn_dkv_fast_kernel<T, DP, true, 1>(BwdArgsT<T, T>);  \
+  template __global__ void attn_dkv_fast_kernel<T, DP, true, 2>(BwdArgsT<T, T>);  \
+  template __global__ void attn_dkv_fast_kernel<T, DP, false, 1>(BwdArgsT<T, T>); \
   template __global__ void attn_dq_fast_kernel<T, DP, true>(BwdArgsT<T, T>);   \
   template __global__ void attn_dq_fast_kernel<T, DP, false>(BwdArgsT<T, T>);  \
   template __global__ void attn_dbias_fast_kernel<T, DP>(BwdArgsT<T, T>);
@@ -888,13 +914,18 @@ hipError_t launch_dkv_fast(const oops_attn_geometry& geo, const Plan& plan, cons
     constexpr int DP = decltype(dpc)::value;
     BwdArgsT<T, T> a;
     fill_bwd_args(a, geo, plan, L);
-    a.uniform_tiles = plan.dkv_uniform;
-    a.total_tiles = plan.dkv_tiles;
-    const dim3 grid((unsigned)xcd_grid(plan.dkv_tiles));
-    if (a.bias != nullptr)
-      hipLaunchKernelGGL((attn_dkv_fast_kernel<T, DP, true>), grid, dim3(256), 0, stream, a);
+    // OOPS_DKV_ROWS=2: two rows per workgroup share each bias fragment (row-shared
+    // biases only); it costs a wave of occupancy and measured slower at the headline shape
+    const bool pair = OOPS_DKV_ROWS == 2 && a.bias != nullptr && !plan.any_full && plan.dkv_tiles_r2 > 0;
+    a.uniform_tiles = pair ? plan.dkv_uniform_r2 : plan.dkv_uniform;
+    a.total_tiles = pair ? plan.dkv_tiles_r2 : plan.dkv_tiles;
+    const dim3 grid((unsigned)xcd_grid(a.total_tiles));
+    if (pair)
+      hipLaunchKernelGGL((attn_dkv_fast_kernel<T, DP, true, 2>), grid, dim3(256), 0, stream, a);
+    else if (a.bias != nullptr)
+      hipLaunchKernelGGL((attn_dkv_fast_kernel<T, DP, true, 1>), grid, dim3(256), 0, stream, a);
     else
-      hipLaunchKernelGGL((attn_dkv_fast_kernel<T, DP, false>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((attn_dkv_fast_kernel<T, DP, false, 1>), grid, dim3(256), 0, stream, a);
     return hipGetLastError();
   });
 }

@@ -17,6 +17,10 @@
 #ifndef OOPS_DBIAS_OCC
 #define OOPS_DBIAS_OCC 2
 #endif
+// Groups (rows) per workgroup of the dK/dV kernel with a row-shared bias: 1 or 2.
+#ifndef OOPS_DKV_ROWS
+#define OOPS_DKV_ROWS 1
+#endif
 
 namespace oops {
 namespace fast {

@@ -121,6 +121,7 @@ struct Plan {
   int64_t fwd_tiles = 0, fwd_uniform = 0;        // 128-query blocks
   int64_t delta_tiles = 0, delta_uniform = 0;    // 64-query blocks
   int64_t dkv_tiles = 0, dkv_uniform = 0;        // 128-key blocks
+  int64_t dkv_tiles_r2 = 0, dkv_uniform_r2 = 0;  // same, two groups per block
   int64_t sbias_tiles = 0, sbias_uniform = 0;    // shared dBias blocks (incl. parts)
   int64_t sred_tiles = 0, sred_uniform = 0;      // shared dBias reduction blocks
   int64_t lse_extent = 0;                        // floats

@@ -57,8 +57,8 @@ int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
   plan.dp = padded_head(geo->head_size);
   const int64_t H = geo->num_heads;
   const Sample* tab = reinterpret_cast<const Sample*>(geo->table_host);
-  int64_t c_fwd = -1, c_delta = -1, c_dkv = -1, c_sb = -1;
-  bool u_fwd = true, u_delta = true, u_dkv = true, u_sb = true;
+  int64_t c_fwd = -1, c_delta = -1, c_dkv = -1, c_sb = -1, c_dkv2 = -1;
+  bool u_fwd = true, u_delta = true, u_dkv = true, u_sb = true, u_dkv2 = true;
   int64_t min_shared_groups = INT64_MAX, sbias_base = 0, sbias_base64 = 0, c_sb64 = -1;
   bool u_sb64 = true;
   auto track = [](int64_t c, int64_t& first, bool& uniform) {
@@ -87,6 +87,9 @@ int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
     plan.fwd_tiles += c1;
     plan.delta_tiles += c2;
     plan.dkv_tiles += c3;
+    const int64_t c3r2 = cdiv(S.G, 2) * H * cdiv(S.Lk, 128);
+    plan.dkv_tiles_r2 += c3r2;
+    track(c3r2, c_dkv2, u_dkv2);
     sbias_base += cs;
     const int64_t cs64 = S.bias_mode == OOPS_BIAS_SHARED ? H * cdiv(S.Lq, 128) * cdiv(S.Lk, 64) : 0;
     sbias_base64 += cs64;
@@ -124,6 +127,7 @@ int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
   plan.fwd_uniform = u_fwd ? c_fwd : 0;
   plan.delta_uniform = u_delta ? c_delta : 0;
   plan.dkv_uniform = u_dkv ? c_dkv : 0;
+  plan.dkv_uniform_r2 = u_dkv2 ? c_dkv2 : 0;
   if (plan.any_shared) {
     int64_t parts = cdiv(kTargetSharedBiasBlocks, std::max<int64_t>(sbias_base, 1));
     parts = std::min<int64_t>({parts, kMaxParts, min_shared_groups});
