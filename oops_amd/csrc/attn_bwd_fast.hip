@@ -302,7 +302,11 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
 // LSE), dS = P dP, dQ^T += K^T dS^T (K^T by LDS transpose reads).  A
 // per-group ("full") bias gets dBias = dS written from registers.
 // Reference: _backward_query (oops/attention/triangle/triton/kernel.py:428-565).
-template <typename T, int DP, bool HAS_BIAS>
+// MASKED_TILES: the geometry may have 64-key tiles with masked or
+// out-of-range keys (else only the unmasked tile code is compiled);
+// FULL_DBIAS: some sample has a per-group bias whose dBias = dS is written
+// here.  Both only add code that costs registers when compiled in.
+template <typename T, int DP, bool HAS_BIAS, bool MASKED_TILES, bool FULL_DBIAS>
 __global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT<T, T> a) {
   using E = Elem<T>;
   using Frag = typename E::Frag;
@@ -345,7 +349,7 @@ __global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT
   const int k_si = (int)S.k_si, v_si = (int)S.v_si, b_si = (int)S.b_si;
   const bool has_mask = a.mask != nullptr && S.m_off >= 0;
   const uint8_t* mbase = has_mask ? a.mask + S.m_off + g * S.m_sg : nullptr;
-  const bool write_dbias = a.dbias != nullptr && S.bias_mode == OOPS_BIAS_FULL;
+  const bool write_dbias = FULL_DBIAS && a.dbias != nullptr && S.bias_mode == OOPS_BIAS_FULL;
 
   for (int t = wave; t < ntiles; t += 4) {
     const int key = t * 64 + lane;
@@ -523,7 +527,7 @@ __global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT
         }
         ds[j] = p * pacc[j];
       }
-      if (dbrow) {
+      if (FULL_DBIAS && dbrow) {
         const int k0 = t * 64 + 32 * t2;
 #pragma unroll
         for (int j = 0; j < 16; j += 4) {
@@ -547,7 +551,7 @@ __global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT
   };
 
   uint4 ku[NCH], vu[NCH];
-  uint4 bias_a[2][2], bias_b[2][2];
+  uint4 bias_a[2][2];
   int t0 = next_tile(-1);
   int t1 = next_tile(t0);
   int t2 = next_tile(t1);
@@ -558,36 +562,30 @@ __global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT
   }
   if (t1 < ntiles) {
     load_kv(t1, ku, vu);
-    if constexpr (HAS_BIAS) load_bias(t1, bias_b);
     store_kv(1, ku, vu);
   }
   load_kv(t2, ku, vu);
   vmem_wait_all();
   __syncthreads();
   int buf = 0;
-  auto step = [&](uint4 (&bias_cur)[2][2]) {
+  while (t0 < ntiles) {
     const int t3 = next_tile(t2);
     const uint64_t bits = uniform64(keep_lds[t0]);
     const int b1 = buf == 2 ? 0 : buf + 1;
     const int b2 = b1 == 2 ? 0 : b1 + 1;
     if (t2 < ntiles) store_kv(b2, ku, vu);
     load_kv(t3, ku, vu);
-    if (bits == ~uint64_t(0))
-      compute(std::false_type{}, buf, t0, bits, bias_cur);
-    else
-      compute(std::true_type{}, buf, t0, bits, bias_cur);
+    if (!MASKED_TILES || bits == ~uint64_t(0))
+      compute(std::false_type{}, buf, t0, bits, bias_a);
+    else if constexpr (MASKED_TILES)
+      compute(std::true_type{}, buf, t0, bits, bias_a);
     if constexpr (HAS_BIAS)
-      load_bias(t2, bias_cur);
+      load_bias(t1, bias_a);  // one register set: the next tile's bias
     lds_barrier();
     buf = b1;
     t0 = t1;
     t1 = t2;
     t2 = t3;
-  };
-  while (t0 < ntiles) {
-    step(bias_a);
-    if (t0 >= ntiles) break;
-    step(bias_b);
   }
 
   if (qv && a.dq != nullptr) {
@@ -605,7 +603,8 @@ __global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT
 // dS block accumulates in registers (no atomics).  Partial sums per part are
 // added by attn_dbias_reduce_kernel.
 // Reference: _backward_shared_bias (oops/attention/triangle/triton/kernel.py:721-873).
-template <typename T, int DP>
+// MASKED_TILES: as in attn_dq_fast_kernel.
+template <typename T, int DP, bool MASKED_TILES>
 __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(BwdArgsT<T, T> a) {
   using E = Elem<T>;
   using Frag = typename E::Frag;
@@ -848,9 +847,9 @@ __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(Bw
         }
       }
     };
-    if (bits == ~uint64_t(0))
+    if (!MASKED_TILES || bits == ~uint64_t(0))
       tile(std::false_type{});
-    else
+    else if constexpr (MASKED_TILES)
       tile(std::true_type{});
     load_q(g_begin + i + 2, qc);
     lds_barrier();
@@ -880,13 +879,19 @@ __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(Bw
   }
 }
 
+#define OOPS_DQ_FAST_INST(T, DP, B)                                                         \
+  template __global__ void attn_dq_fast_kernel<T, DP, B, false, false>(BwdArgsT<T, T>); \
+  template __global__ void attn_dq_fast_kernel<T, DP, B, true, false>(BwdArgsT<T, T>);  \
+  template __global__ void attn_dq_fast_kernel<T, DP, B, false, true>(BwdArgsT<T, T>);  \
+  template __global__ void attn_dq_fast_kernel<T, DP, B, true, true>(BwdArgsT<T, T>);
 #define OOPS_BWD_FAST_INST(T, DP)                                                \
   template __global__ void attn_dkv_fast_kernel<T, DP, true, 1>(BwdArgsT<T, T>);  \
   template __global__ void attn_dkv_fast_kernel<T, DP, true, 2>(BwdArgsT<T, T>);  \
   template __global__ void attn_dkv_fast_kernel<T, DP, false, 1>(BwdArgsT<T, T>); \
-  template __global__ void attn_dq_fast_kernel<T, DP, true>(BwdArgsT<T, T>);   \
-  template __global__ void attn_dq_fast_kernel<T, DP, false>(BwdArgsT<T, T>);  \
-  template __global__ void attn_dbias_fast_kernel<T, DP>(BwdArgsT<T, T>);
+  OOPS_DQ_FAST_INST(T, DP, true)                                                 \
+  OOPS_DQ_FAST_INST(T, DP, false)                                                \
+  template __global__ void attn_dbias_fast_kernel<T, DP, false>(BwdArgsT<T, T>);     \
+  template __global__ void attn_dbias_fast_kernel<T, DP, true>(BwdArgsT<T, T>);
 OOPS_BWD_FAST_INST(__bf16, 32)
 OOPS_BWD_FAST_INST(__bf16, 64)
 OOPS_BWD_FAST_INST(_Float16, 32)
@@ -941,10 +946,22 @@ hipError_t launch_dq_fast(const oops_attn_geometry& geo, const Plan& plan, const
     a.total_tiles = plan.fwd_tiles;
     a.delta_in_dq = delta_in_dq ? 1 : 0;
     const dim3 grid((unsigned)xcd_grid(plan.fwd_tiles));
-    if (a.bias != nullptr)
-      hipLaunchKernelGGL((attn_dq_fast_kernel<T, DP, true>), grid, dim3(256), 0, stream, a);
-    else
-      hipLaunchKernelGGL((attn_dq_fast_kernel<T, DP, false>), grid, dim3(256), 0, stream, a);
+    const bool full = a.dbias != nullptr && plan.any_full;
+    auto go = [&](auto has_bias, auto masked, auto full_db) {
+      hipLaunchKernelGGL((attn_dq_fast_kernel<T, DP, decltype(has_bias)::value, decltype(masked)::value,
+                                              decltype(full_db)::value>),
+                         grid, dim3(256), 0, stream, a);
+    };
+    auto by_full = [&](auto has_bias, auto masked) {
+      if (full) go(has_bias, masked, std::true_type{});
+      else go(has_bias, masked, std::false_type{});
+    };
+    auto by_mask = [&](auto has_bias) {
+      if (plan.masked_tiles) by_full(has_bias, std::true_type{});
+      else by_full(has_bias, std::false_type{});
+    };
+    if (a.bias != nullptr) by_mask(std::true_type{});
+    else by_mask(std::false_type{});
     return hipGetLastError();
   });
 }
@@ -959,8 +976,11 @@ hipError_t launch_dbias_fast(const oops_attn_geometry& geo, const Plan& plan, co
     a.parts = plan.fast_parts;
     a.uniform_tiles = plan.fast_sbias_uniform;
     a.total_tiles = plan.fast_sbias_tiles;
-    hipLaunchKernelGGL((attn_dbias_fast_kernel<T, DP>), dim3((unsigned)xcd_grid(plan.fast_sbias_tiles)), dim3(256),
-                       0, stream, a);
+    const dim3 grid((unsigned)xcd_grid(plan.fast_sbias_tiles));
+    if (plan.masked_tiles)
+      hipLaunchKernelGGL((attn_dbias_fast_kernel<T, DP, true>), grid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((attn_dbias_fast_kernel<T, DP, false>), grid, dim3(256), 0, stream, a);
     return hipGetLastError();
   });
 }

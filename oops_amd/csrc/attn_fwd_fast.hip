@@ -45,7 +45,10 @@ namespace oops {
 using namespace fast;
 
 
-template <typename T, int DP, bool HAS_BIAS>
+// MASKED_TILES: the geometry may have 64-key tiles with masked or
+// out-of-range keys; without it the per-score mask code is not compiled
+// (it costs registers even when never executed).
+template <typename T, int DP, bool HAS_BIAS, bool MASKED_TILES>
 __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArgsT<T, T> a) {
   using E = Elem<T>;
   using Frag = typename E::Frag;
@@ -248,7 +251,7 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
 
   // softmax of one tile's scores + O^T += V^T P^T from LDS buffer buf
   auto attend = [&](int buf, uint64_t bits, f32x16 (&sacc)[2]) {
-    if (bits != ~uint64_t(0)) {
+    if (MASKED_TILES && bits != ~uint64_t(0)) {
       // mixed tile: masked / out-of-range keys get -inf
       const uint64_t lb = bits >> (g2 * 4);
 #pragma unroll
@@ -392,9 +395,11 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
   }
 }
 
-#define OOPS_FWD_FAST_INST(T, DP)                                                \
-  template __global__ void attn_fwd_fast_kernel<T, DP, true>(FwdArgsT<T, T>);  \
-  template __global__ void attn_fwd_fast_kernel<T, DP, false>(FwdArgsT<T, T>);
+#define OOPS_FWD_FAST_INST(T, DP)                                                       \
+  template __global__ void attn_fwd_fast_kernel<T, DP, true, false>(FwdArgsT<T, T>);  \
+  template __global__ void attn_fwd_fast_kernel<T, DP, true, true>(FwdArgsT<T, T>);   \
+  template __global__ void attn_fwd_fast_kernel<T, DP, false, false>(FwdArgsT<T, T>); \
+  template __global__ void attn_fwd_fast_kernel<T, DP, false, true>(FwdArgsT<T, T>);
 OOPS_FWD_FAST_INST(__bf16, 32)
 OOPS_FWD_FAST_INST(__bf16, 64)
 OOPS_FWD_FAST_INST(_Float16, 32)
@@ -495,10 +500,16 @@ bool launch_forward_fast(const oops_attn_geometry& geo, const Plan& plan, const 
     a.bf_nqt = plan.bf_nqt;
     a.bf_nkt = plan.bf_nkt;
     const dim3 grid((unsigned)xcd_grid(plan.fwd_tiles));
-    if (a.bias != nullptr)
-      hipLaunchKernelGGL((attn_fwd_fast_kernel<T, DP, true>), grid, dim3(256), 0, stream, a);
-    else
-      hipLaunchKernelGGL((attn_fwd_fast_kernel<T, DP, false>), grid, dim3(256), 0, stream, a);
+    auto go = [&](auto has_bias, auto masked) {
+      hipLaunchKernelGGL((attn_fwd_fast_kernel<T, DP, decltype(has_bias)::value, decltype(masked)::value>), grid,
+                         dim3(256), 0, stream, a);
+    };
+    auto by_mask = [&](auto has_bias) {
+      if (plan.masked_tiles) go(has_bias, std::true_type{});
+      else go(has_bias, std::false_type{});
+    };
+    if (a.bias != nullptr) by_mask(std::true_type{});
+    else by_mask(std::false_type{});
     *err = hipGetLastError();
   };
   if (plan.fwd_tiles == 0) {

@@ -131,6 +131,7 @@ struct Plan {
   int fast_parts = 1;
   bool any_full = false, any_shared = false;
   bool any_pair_mask = false;                    // a mask that depends on the query
+  bool masked_tiles = false;                     // some 64-key tile has masked or out-of-range keys
   bool offsets_32bit = true;                     // every per-(group, head) K/V/bias block < 2 GiB
   int64_t max_len_q = 0, max_len_k = 0;
   // fragment-major copy of the shared biases for the fast kernels (see attn_bias_frag_kernel)

@@ -102,6 +102,7 @@ int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
     plan.max_len_q = std::max(plan.max_len_q, S.Lq);
     plan.max_len_k = std::max(plan.max_len_k, S.Lk);
     if (geo->has_mask && S.m_off >= 0 && S.m_si != 0) plan.any_pair_mask = true;
+    if ((geo->has_mask && S.m_off >= 0) || S.Lk % 64 != 0) plan.masked_tiles = true;
     {
       const int64_t elt = geo->dtype == OOPS_F32 ? 4 : 2;
       const int64_t lim = int64_t(1) << 31;
