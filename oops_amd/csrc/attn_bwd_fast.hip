@@ -794,22 +794,21 @@ __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(Bw
 
   const int64_t ng = g_end - g_begin;
   Stage stg;
-  QStage qa, qb2;
+  QStage qc;
   if (ng > 0) {
     load_stage(g_begin, stg);
     store_stage(0, stg);
-    load_q(g_begin, qa);
   }
   if (ng > 1) {
     load_stage(g_begin + 1, stg);
     store_stage(1, stg);
-    load_q(g_begin + 1, qb2);
   }
+  load_q(g_begin, qc);
   load_stage(g_begin + 2, stg);
   vmem_wait_all();
   __syncthreads();
   int buf = 0;
-  auto step = [&](int64_t i, QStage& qc) {
+  for (int64_t i = 0; i < ng; ++i) {
     const int b1 = buf == 2 ? 0 : buf + 1;
     const int b2 = b1 == 2 ? 0 : b1 + 1;
     if (i + 2 < ng) store_stage(b2, stg);
@@ -820,8 +819,11 @@ __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(Bw
     const uint64_t lb = bits >> (g2 * 4);
     Frag qf[NQF], df[NQF];
     q_frags(qc, qf, df);
-    f32x16 nd;
     const float ndlt = -qc.dlt, nlse = -qc.lse;
+    // one set of query-side registers: the next group's rows are loaded as
+    // soon as this group's have gone through LDS
+    load_q(g_begin + i + 1, qc);
+    f32x16 nd;
 #pragma unroll
     for (int j = 0; j < 16; ++j) nd[j] = ndlt;
     // fully kept tiles take the variant without per-score mask work
@@ -851,14 +853,8 @@ __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(Bw
       tile(std::false_type{});
     else if constexpr (MASKED_TILES)
       tile(std::true_type{});
-    load_q(g_begin + i + 2, qc);
     lds_barrier();
     buf = b1;
-  };
-  for (int64_t i = 0; i < ng; i += 2) {
-    step(i, qa);
-    if (i + 1 >= ng) break;
-    step(i + 1, qb2);
   }
 
   if (qv) {
