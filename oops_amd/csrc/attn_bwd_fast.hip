@@ -319,6 +319,7 @@ __global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT
   __shared__ __attribute__((aligned(16))) T k_lds[3 * TBUF];
   __shared__ __attribute__((aligned(16))) T v_lds[3 * TBUF];
   __shared__ uint64_t keep_lds[kMaxKeyTiles];
+  __shared__ float dl_lds[4 * 32];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -361,43 +362,86 @@ __global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT
 
   const int q_lane = qb * 128 + wave * 32 + lq;
   const bool qv = q_lane < Lq;
-  Frag qf[NQF], df[NQF];
-  {
-    const T* qrow = a.q + S.q_off + g * S.q_sg + h * S.q_sh + (int64_t)q_lane * S.q_si;
-    const T* drow = a.dout + S.do_off + g * S.do_sg + h * S.do_sh + (int64_t)q_lane * S.do_si;
-#pragma unroll
-    for (int s = 0; s < NQF; ++s) {
-      const int col = s * 16 + g2 * 8;
-      const bool ok = qv && col < D;
-      qf[s] = __builtin_bit_cast(Frag, ok ? *reinterpret_cast<const uint4*>(qrow + col) : make_uint4(0, 0, 0, 0));
-      df[s] = __builtin_bit_cast(Frag, ok ? *reinterpret_cast<const uint4*>(drow + col) : make_uint4(0, 0, 0, 0));
-    }
-  }
   const int64_t lidx = S.l_off + ((int64_t)g * H + h) * Lq + q_lane;
   const float neg_lse = qv ? -a.lse[lidx] : 0.0f;
+  Frag qf[NQF], df[NQF];
   f32x16 ndelta;
   {
+    // The wave's 32 query rows of Q and dO are read whole (DP/8 lanes per
+    // row, 16-byte chunks), staged through a wave-private region of the K/V
+    // ring (free until the ring's first store, after the barrier below) and
+    // read back as MFMA fragments.
+    constexpr int NQR = DP / 16;
+    constexpr int LPR = DP / 8;
+    const int q0w = qb * 128 + wave * 32;
+    const int64_t gh_q = S.q_off + g * S.q_sg + h * S.q_sh;
+    const int64_t gh_d = S.do_off + g * S.do_sg + h * S.do_sh;
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q + gh_q, (uint32_t)(((int64_t)(Lq - 1) * S.q_si + D) * 2));
+    const __amdgpu_buffer_rsrc_t dr = make_rsrc(a.dout + gh_d, (uint32_t)(((int64_t)(Lq - 1) * S.do_si + D) * 2));
+    int q_row[NQR], q_col[NQR];
+    bool ok[NQR];
+    uint4 qu[NQR], du[NQR];
+#pragma unroll
+    for (int i = 0; i < NQR; ++i) {
+      const int c = i * 64 + lane;
+      q_row[i] = c / LPR;
+      q_col[i] = (c % LPR) * 8;
+      ok[i] = q0w + q_row[i] < Lq && q_col[i] < D;
+      qu[i] = buffer_load16(qr, ok[i] ? (uint32_t)(((q0w + q_row[i]) * (int)S.q_si + q_col[i]) * 2) : kOut);
+      du[i] = buffer_load16(dr, ok[i] ? (uint32_t)(((q0w + q_row[i]) * (int)S.do_si + q_col[i]) * 2) : kOut);
+    }
     float dl;
     if (a.delta_in_dq) {
-      // delta = rowsum((O + O_lo) * dO) over this lane's columns of dO, then
-      // the partner lane's (the other 32-lane half holds the other columns)
-      const int64_t o_row = S.o_off + g * S.o_sg + h * S.o_sh + (int64_t)q_lane * S.o_si;
-      const T* orow = a.out + o_row;
-      const T* lrow = a.out_lo != nullptr ? a.out_lo + o_row : nullptr;
-      float part = 0.0f;
+      // delta = rowsum((O + O_lo) * dO): partial sums over this lane's
+      // chunks, reduced over the row's lanes, gathered through LDS
+      const int64_t gh_o = S.o_off + g * S.o_sg + h * S.o_sh;
+      const uint32_t o_bytes = (uint32_t)(((int64_t)(Lq - 1) * S.o_si + D) * 2);
+      const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.out + gh_o, o_bytes);
+      const __amdgpu_buffer_rsrc_t lrr = make_rsrc(a.out_lo != nullptr ? a.out_lo + gh_o : a.out,
+                                                   a.out_lo != nullptr ? o_bytes : 0u);
+      float part[NQR];
 #pragma unroll
-      for (int s = 0; s < NQF; ++s) {
-        const int col = s * 16 + g2 * 8;
-        const bool ok = qv && col < D;
-        const uint4 ou = ok ? *reinterpret_cast<const uint4*>(orow + col) : make_uint4(0, 0, 0, 0);
-        const uint4 lu = ok && lrow ? *reinterpret_cast<const uint4*>(lrow + col) : make_uint4(0, 0, 0, 0);
+      for (int i = 0; i < NQR; ++i) {
+        const uint32_t off = ok[i] ? (uint32_t)(((q0w + q_row[i]) * (int)S.o_si + q_col[i]) * 2) : kOut;
+        const uint4 ou = buffer_load16(orr, off);
+        const uint4 lu = buffer_load16(lrr, off);
         const T* oe = reinterpret_cast<const T*>(&ou);
         const T* le = reinterpret_cast<const T*>(&lu);
+        const T* de = reinterpret_cast<const T*>(&du[i]);
+        float s = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) part += (E::to_f(oe[i]) + E::to_f(le[i])) * E::to_f(df[s][i]);
+        for (int e = 0; e < 8; ++e) s += (E::to_f(oe[e]) + E::to_f(le[e])) * E::to_f(de[e]);
+#pragma unroll
+        for (int m = 1; m < LPR; m <<= 1) s += __shfl_xor(s, m);
+        part[i] = s;
       }
-      dl = sum_halves(part);
-      if (g2 == 0 && qv) a.delta[lidx] = dl;
+#pragma unroll
+      for (int i = 0; i < NQR; ++i)
+        if (lane % LPR == 0) {
+          dl_lds[wave * 32 + q_row[i]] = part[i];
+          if (q0w + q_row[i] < Lq) a.delta[lidx - lq + q_row[i]] = part[i];
+        }
+    }
+    T* const q_w = &k_lds[wave * 32 * LD];
+    T* const d_w = &v_lds[wave * 32 * LD];
+#pragma unroll
+    for (int i = 0; i < NQR; ++i) {
+      *reinterpret_cast<uint4*>(&q_w[q_row[i] * LD + q_col[i]]) = qu[i];
+      *reinterpret_cast<uint4*>(&d_w[q_row[i] * LD + q_col[i]]) = du[i];
+    }
+    // other lanes of this wave read what was just written (LDS operations
+    // of one wave complete in order; the fences keep the compiler's order)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int s = 0; s < NQF; ++s) {
+      qf[s] = lds_frag<T>(&q_w[lq * LD + s * 16 + g2 * 8]);
+      df[s] = lds_frag<T>(&d_w[lq * LD + s * 16 + g2 * 8]);
+    }
+    if (a.delta_in_dq) {
+      dl = dl_lds[wave * 32 + lq];
+      dl = qv ? dl : 0.0f;
     } else {
       dl = qv ? a.delta[lidx] : 0.0f;
     }
