@@ -129,5 +129,32 @@ __device__ __forceinline__ void store_tile(T* row, int d0, int D, int g, const A
   if (d + 16 <= D) *reinterpret_cast<uint4*>(row + d + 8) = hi;
 }
 
+// ---- LDS tiles filled by direct global -> LDS loads (buffer_load ... lds).
+// One such load of a wave writes 64 consecutive 16-byte slots (lane i: slot
+// i).  A tile row of DP 16-bit elements spans DP/8 slots; logical 16-byte
+// chunk c of row r sits in slot c ^ swz(r) of that row, so the 16 rows read
+// by one 16-lane group of a fragment read (same logical chunk) land in 16
+// distinct 16-byte bank groups.
+template <int DP>
+__device__ __forceinline__ int swz(int row) {
+  static_assert(DP == 32 || DP == 64, "swizzle defined for 32- and 64-element rows");
+  return (row >> (DP == 32 ? 2 : 1)) & (DP / 8 - 1);
+}
+// element offset of (row, col) in a swizzled tile of DP-element rows
+template <int DP>
+__device__ __forceinline__ int swz_off(int row, int col) {
+  return row * DP + ((((col >> 3) ^ swz<DP>(row))) << 3) + (col & 7);
+}
+// 16 bytes per lane from a buffer resource into 64 consecutive LDS slots
+// starting at lds (wave-uniform); an out-of-range offset writes zeros
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, const void* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds), 16, voff, soff, 0, 0);
+}
+// wait until at most N vector-memory operations of this wave are outstanding
+template <int N>
+__device__ __forceinline__ void vmem_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
 }  // namespace fast
 }  // namespace oops

@@ -18,16 +18,15 @@
 //     skipped, only mixed tiles select per score;
 //   * writes O and its rounding residual with whole 64-byte row segments.
 // Work split: 4 wavefronts x 32 queries per workgroup, 64 keys per step.
-// K and V (both row-major, as read from memory) go through a 3-buffer LDS
-// ring (one barrier per step, written two steps ahead); the PV MFMA reads
-// V^T fragments with the gfx950 LDS transpose read.  Bias fragments are
-// loaded from global memory straight into registers one step ahead.  All
-// loads use range-checked buffer resources; a tile past the end reads at an
-// out-of-range offset (zeros, no memory traffic) so every load is
-// unconditional and the wait counts stay exact.
-// OOPS_FWD_PIPE=1 builds a variant that issues the QK^T MFMAs of step i+1
-// before the softmax of step i; it needs more registers (one wave less per
-// SIMD) and measured slower at head size 32, so it is off by default.
+// K and V tiles go from global memory straight into a 4-buffer LDS ring
+// (buffer_load ... lds, issued three steps ahead, one barrier per step); K
+// rows are XOR-swizzled in 16-byte chunks so the fragment reads are free of
+// bank conflicts, and the PV MFMA reads V^T fragments with the gfx950 LDS
+// transpose read.  Bias fragments are loaded from global memory straight
+// into registers one step ahead.  All loads use range-checked buffer
+// resources; a tile past the end reads at an out-of-range offset (zeros, no
+// memory traffic) so every load is unconditional and the wait counts stay
+// exact.
 //
 // Semantics are those of the generic forward (attn_fwd.hip), i.e. of the
 // reference's _attend (oops/attention/triangle/triton/kernel.py:151-262):
@@ -36,13 +35,12 @@
 // (relative error <= 2^-9 for bf16), below the rounding of P itself.
 #include "attn_fast_common.h"
 
-#ifndef OOPS_FWD_PIPE
-#define OOPS_FWD_PIPE 0
-#endif
 
 namespace oops {
 
 using namespace fast;
+
+constexpr int kRing = 4;  // K/V tile buffers in LDS
 
 
 // MASKED_TILES: the geometry may have 64-key tiles with masked or
@@ -53,20 +51,27 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
   using E = Elem<T>;
   using Frag = typename E::Frag;
   using P2 = typename Pair<T>::v2;
-  constexpr int KLD = DP + 8;        // K tile row (elements)
-  constexpr int VLD = DP + 8;        // V tile row (elements), natural layout
   constexpr int NDT = DP / 32;
   constexpr int NQF = DP / 16;
-  constexpr int NCH = DP / 32;       // 16-byte K (and V) chunks per thread per step
-  constexpr int KBUF = 64 * KLD;     // elements per K buffer
-  constexpr int VBUF = 64 * VLD;
+  constexpr int KT = 64 * DP;        // elements per K (or V) tile: 64 swizzled rows
+  constexpr int CPR = DP / 8;        // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;      // rows per direct-to-LDS load of a wave
+  constexpr int IPW = 16 / RPI;      // loads per wave per tile and tensor (16 rows per wave)
+  constexpr int NDMA = 2 * IPW;      // K and V loads per wave per tile
 
-  __shared__ __attribute__((aligned(16))) T k_lds[3 * KBUF];
-  __shared__ __attribute__((aligned(16))) T v_lds[3 * VBUF];
+  // The ring position is a compile-time constant wherever a buffer is
+  // addressed (the loop is unrolled over the ring): buffer offsets become
+  // instruction immediates, and the compiler can tell that the loads into
+  // one buffer do not overlap the reads of another.  The waits for the
+  // direct-to-LDS loads are explicit (before each step's barrier).
+  __shared__ __attribute__((aligned(16))) T k_lds[kRing * KT];
+  __shared__ __attribute__((aligned(16))) T v_lds[kRing * KT];
+  auto kbuf = [&](auto bc) -> T* { return k_lds + decltype(bc)::value * KT; };
+  auto vbuf = [&](auto bc) -> T* { return v_lds + decltype(bc)::value * KT; };
   __shared__ uint64_t keep_lds[kMaxKeyTiles];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = (tid >> 6) & 3;  // (& 3: lets the compiler bound LDS addresses)
   const int lane = tid & 63;
   const int lq = lane & 31;
   const int g2 = lane >> 5;
@@ -135,18 +140,22 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
       for (int j = 0; j < 8; ++j) ident[c][j] = (lq == 16 * c + g2 * 8 + j) ? w : (T)0.0f;
   }
 
-  // ---- fixed per-thread load offsets (bytes); the step adds k0 * stride via soffset
+  // ---- fixed per-lane offsets (bytes) of the direct-to-LDS tile loads:
+  // wave w fills rows 16w .. 16w+15 of the K and V tiles; lane l writes slot
+  // l of its load, i.e. row l / CPR, slot l % CPR, which holds the logical
+  // chunk (l % CPR) ^ swz(row).  The step adds k0 * stride via soffset.
   const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kbase, (uint32_t)(((int64_t)(Lk - 1) * k_si + D) * 2));
   const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vbase, (uint32_t)(((int64_t)(Lk - 1) * v_si + D) * 2));
-  uint32_t kv_row[NCH], k_off[NCH], v_off[NCH];
+  int d_row[IPW];
+  uint32_t k_off[IPW], v_off[IPW];
 #pragma unroll
-  for (int i = 0; i < NCH; ++i) {
-    const int c = tid + 256 * i;
-    const int r = c / (DP / 8);
-    const int col = (c % (DP / 8)) * 8;
-    kv_row[i] = r;
+  for (int i = 0; i < IPW; ++i) {
+    const int r = 16 * wave + i * RPI + lane / CPR;
+    const int col = ((lane % CPR) ^ swz<DP>(r)) * 8;  // K: swizzled rows
+    const int vcol = (lane % CPR) * 8;                // V: plain rows
+    d_row[i] = r;
     k_off[i] = col < D ? (uint32_t)((r * k_si + col) * 2) : kOut;
-    v_off[i] = col < D ? (uint32_t)((r * v_si + col) * 2) : kOut;
+    v_off[i] = vcol < D ? (uint32_t)((r * v_si + vcol) * 2) : kOut;
   }
   // bias fragments: from the fragment-major copy of a shared bias (one
   // contiguous 1 KB load per fragment), else from the bias rows themselves
@@ -180,25 +189,16 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
   // An absent tile (t >= ntiles) issues its loads with out-of-range offsets:
   // no memory traffic, and no branch, so the compiler can count outstanding
   // loads exactly and never has to wait for all of them.
-  auto load_kv = [&](int t, uint4 (&ku)[NCH], uint4 (&vu)[NCH]) {
+  auto load_kv = [&](int t, auto bc) {
     const uint64_t bits = t < ntiles ? keep_lds[t < ntiles ? t : 0] : 0;
     const uint32_t ks = (uint32_t)(t * 64 * k_si * 2), vs = (uint32_t)(t * 64 * v_si * 2);
     const bool full = bits == ~uint64_t(0);
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      const bool ok = full || ((bits >> kv_row[i]) & 1);
-      ku[i] = buffer_load16_s(k_rsrc, ok ? k_off[i] : kOut, ks);
-      vu[i] = buffer_load16_s(v_rsrc, ok ? v_off[i] : kOut, vs);
-    }
-  };
-  auto store_kv = [&](int buf, const uint4 (&ku)[NCH], const uint4 (&vu)[NCH]) {
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      const int c = tid + 256 * i;
-      const int r = c / (DP / 8);
-      const int col = (c % (DP / 8)) * 8;
-      *reinterpret_cast<uint4*>(&k_lds[buf * KBUF + r * KLD + col]) = ku[i];
-      *reinterpret_cast<uint4*>(&v_lds[buf * VBUF + r * VLD + col]) = vu[i];
+    for (int i = 0; i < IPW; ++i) {
+      const bool ok = full || ((bits >> d_row[i]) & 1);
+      const int r0 = 16 * wave + i * RPI;
+      dma16(k_rsrc, kbuf(bc) + r0 * DP, ok ? k_off[i] : kOut, ks);
+      dma16(v_rsrc, vbuf(bc) + r0 * DP, ok ? v_off[i] : kOut, vs);
     }
   };
   // bias B-fragments of a tile: keys past Lk fall in the next row or past the
@@ -213,7 +213,7 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
       for (int c = 0; c < 2; ++c) bf[t2][c] = buffer_load16_s(b_rsrc, t < ntiles ? b_off[t2][c] + s : kOut, 0);
   };
   // S^T of a tile (bias by identity MFMA, then Q K^T) from LDS buffer buf
-  auto scores = [&](int buf, const uint4 (&bf)[2][2], f32x16 (&sacc)[2]) {
+  auto scores = [&](auto bc, const uint4 (&bf)[2][2], f32x16 (&sacc)[2]) {
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
       if constexpr (HAS_BIAS) {
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
 #pragma unroll
       for (int s = 0; s < NQF; ++s) {
         const Frag kf = __builtin_bit_cast(
-            Frag, *reinterpret_cast<const uint4*>(&k_lds[buf * KBUF + (32 * t2 + lq) * KLD + s * 16 + g2 * 8]));
+            Frag, *reinterpret_cast<const uint4*>(kbuf(bc) + swz_off<DP>(32 * t2 + lq, s * 16 + g2 * 8)));
         sacc[t2] = E::mma(kf, qf[s], sacc[t2]);
       }
     }
@@ -250,7 +250,7 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
   ones[1] = (T)1.0f;
 
   // softmax of one tile's scores + O^T += V^T P^T from LDS buffer buf
-  auto attend = [&](int buf, uint64_t bits, f32x16 (&sacc)[2]) {
+  auto attend = [&](auto bc, uint64_t bits, f32x16 (&sacc)[2]) {
     if (MASKED_TILES && bits != ~uint64_t(0)) {
       // mixed tile: masked / out-of-range keys get -inf
       const uint64_t lb = bits >> (g2 * 4);
@@ -298,76 +298,60 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
         }
 #pragma unroll
         for (int t = 0; t < NDT; ++t) {
-          const Frag vf = lds_read_tr_frag<T>(&v_lds[buf * VBUF], VLD, 32 * t2 + 16 * m, t * 32, lane);
+          const Frag vf = lds_read_tr_frag<T>(vbuf(bc), DP, 32 * t2 + 16 * m, t * 32, lane);
           oacc[t] = E::mma(vf, pf, oacc[t]);
         }
       }
     l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
   };
 
-  // ---- pipeline.  Step i (tile t0, LDS buffer i % 3):
-  //   store K/V of t2 (loaded during step i-1) into buffer (i+2) % 3,
-  //   issue K/V loads of t3, issue QK^T of t1 (its buffer was filled in
-  //   step i-1), issue bias loads of t3 (into the stage t1 just freed), softmax + PV of t0, barrier.
-  uint4 ku[NCH], vu[NCH];
-  uint4 bias_a[2][2], bias_b[2][2];
-  f32x16 sacc_a[2], sacc_b[2];
+  // ---- pipeline.  Step i computes tile t0 from ring buffer i % kRing.  It
+  // first issues the direct-to-LDS loads of the tile kRing - 1 steps ahead
+  // (into the buffer the previous step released), then S of t0 (its bias
+  // fragments were loaded one step ahead), then the bias loads of t1, then
+  // the softmax and PV of t0.  Before the step's barrier, the loads of the
+  // next step's tile must have landed: issued two steps earlier, they are
+  // followed by 2 * NDMA tile loads and 3 x 4 bias loads.
+  static_assert(kRing == 4, "the wait count below assumes a 4-buffer ring");
+  uint4 bias_a[2][2];
+  f32x16 sacc[2];
   int t0 = next_tile(-1);
   int t1 = next_tile(t0);
   int t2 = next_tile(t1);
-  if (t0 < ntiles) {
-    load_kv(t0, ku, vu);
-    if constexpr (HAS_BIAS) load_bias(t0, bias_a);
-    store_kv(0, ku, vu);
-  }
-  if (t1 < ntiles) {
-    load_kv(t1, ku, vu);
-    store_kv(1, ku, vu);
-  }
-  load_kv(t2, ku, vu);
-  // drain every prologue load (Q included) so the wait counters are clean
-  // at loop entry and only the loads issued in a step are ever in flight
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  using B2 = std::integral_constant<int, 2>;
+  using B3 = std::integral_constant<int, 3>;
+  load_kv(t0, B0{});
+  load_kv(t1, B1{});
+  load_kv(t2, B2{});
+  if constexpr (HAS_BIAS) load_bias(t0, bias_a);
+  // drain every prologue load (Q included) so that only the loads issued
+  // in the loop are ever in flight there
   vmem_wait_all();
   __syncthreads();
-#if OOPS_FWD_PIPE
-  if (t0 < ntiles) scores(0, bias_a, sacc_a);
-  if constexpr (HAS_BIAS)
-    load_bias(t2, bias_a);
-#endif
-
-  int buf = 0;
-  // bias_nxt holds bias(t1); once scores(t1) has consumed it, it receives bias(t3)
-  auto step = [&](auto& sacc_cur, auto& sacc_nxt, auto& bias_nxt, auto& bias_cur) {
+  // the ring position is a compile-time constant in each of four unrolled steps
+  auto step = [&](auto bc, auto bc_load) {
     const int t3 = next_tile(t2);
     const uint64_t bits = keep_lds[t0];
-    const int b1 = buf == 2 ? 0 : buf + 1;
-    const int b2 = b1 == 2 ? 0 : b1 + 1;
-    if (t2 < ntiles) store_kv(b2, ku, vu);
-    load_kv(t3, ku, vu);
-#if OOPS_FWD_PIPE
-    if (t1 < ntiles) scores(b1, bias_nxt, sacc_nxt);
-    if constexpr (HAS_BIAS)
-      load_bias(t3, bias_nxt);
-    attend(buf, bits, sacc_cur);
-#else
-    // one set of bias registers: the next tile's fragments are loaded as
-    // soon as this tile's bias MFMAs have read them
-    scores(buf, bias_a, sacc_cur);
-    if constexpr (HAS_BIAS)
-      load_bias(t1, bias_a);
-    (void)bias_cur;
-    attend(buf, bits, sacc_cur);
-#endif
+    load_kv(t3, bc_load);
+    scores(bc, bias_a, sacc);
+    if constexpr (HAS_BIAS) load_bias(t1, bias_a);
+    attend(bc, bits, sacc);
+    vmem_wait<2 * NDMA + (HAS_BIAS ? 12 : 0)>();
     lds_barrier();
-    buf = b1;
     t0 = t1;
     t1 = t2;
     t2 = t3;
   };
   while (t0 < ntiles) {
-    step(sacc_a, sacc_b, bias_b, bias_a);
+    step(B0{}, B3{});
     if (t0 >= ntiles) break;
-    step(sacc_b, sacc_a, bias_a, bias_b);
+    step(B1{}, B0{});
+    if (t0 >= ntiles) break;
+    step(B2{}, B1{});
+    if (t0 >= ntiles) break;
+    step(B3{}, B2{});
   }
 
   // ---- epilogue
