@@ -704,8 +704,11 @@ __global__ __launch_bounds__(256) void attn_dbias_reduce_kernel(BwdArgs a) {
   const int64_t q = (e / Lk) % Lq;
   const int64_t h = e / (Lk * Lq);
   const int64_t off = S.db_off + h * S.db_sh + q * S.db_si + key;
+  // per-sample parts (fast path): a sample with one part wrote dBias directly
+  const int parts = a.part_groups > 0 ? parts_for(S.G, a.part_groups, a.parts) : a.parts;
+  if (parts < 2) return;
   float acc = 0.0f;
-  for (int p = 0; p < a.parts; ++p) acc += a.dbias_part[(int64_t)p * a.dbias_extent + off];
+  for (int p = 0; p < parts; ++p) acc += a.dbias_part[(int64_t)p * a.dbias_extent + off];
   a.dbias[off] = acc;
 }
 
@@ -779,6 +782,7 @@ hipError_t launch_backward(const oops_attn_geometry& geo, const Plan& plan, cons
       if (fast) {
         if (err == hipSuccess) err = launch_dbias_fast(geo, plan, L, stream);
         a.parts = plan.fast_parts;
+        a.part_groups = plan.fast_part_groups;
       } else {
         a.uniform_tiles = plan.sbias_uniform;
         hipLaunchKernelGGL((attn_dbias_shared_kernel<T, BT, DP>), dim3((unsigned)plan.sbias_tiles), block, 0,

@@ -29,8 +29,7 @@ template <typename T, int DP, bool HAS_BIAS, int R>
 __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArgsT<T, T> a) {
   using E = Elem<T>;
   using Frag = typename E::Frag;
-  constexpr int LD = DP + 8;        // Q / dO tile row (elements)
-  constexpr int TBUF = 64 * LD;     // elements per tile buffer
+  constexpr int TBUF = 64 * DP;     // elements per tile buffer (64 swizzled rows, see swz)
   constexpr int NDT = DP / 32;
   constexpr int NQF = DP / 16;
   constexpr int NCH = DP / 32;      // 16-byte chunks of Q (and dO) per thread per step
@@ -49,7 +48,7 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
   // XCD-aware order (see attn_fwd_fast.hip): logical (head group, row block,
   // head, key block); a row block is R consecutive groups g that share the
   // bias, so each bias fragment loaded serves R rows
-  int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
+  int64_t tile = xcd_tile(blockIdx.x, gridDim.x, xcd_chunk(a.uniform_tiles));
   if (tile >= a.total_tiles) return;
   const Sample* tab = reinterpret_cast<const Sample*>(a.table);
   const int H = a.num_heads;
@@ -177,8 +176,8 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
         const int c = tid + 256 * i;
         const int row = c / (DP / 8);
         const int col = (c % (DP / 8)) * 8;
-        *reinterpret_cast<uint4*>(&q_lds[(buf * R + r) * TBUF + row * LD + col]) = st.q[r][i];
-        *reinterpret_cast<uint4*>(&do_lds[(buf * R + r) * TBUF + row * LD + col]) = st.d[r][i];
+        *reinterpret_cast<uint4*>(&q_lds[(buf * R + r) * TBUF + swz_off<DP>(row, col)]) = st.q[r][i];
+        *reinterpret_cast<uint4*>(&do_lds[(buf * R + r) * TBUF + swz_off<DP>(row, col)]) = st.d[r][i];
       }
       if (tid < 64) {
         const int pos = (tid & 32) + perm32(tid & 31);
@@ -195,6 +194,9 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
 #pragma unroll
     for (int t = 0; t < NDT; ++t) dk[r][t] = dv[r][t] = f32x16{};
 
+  TrLane trl[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) trl[t] = tr_lane<DP>(lane, 32 * t);
   // one step: for each row, two 32-query tiles of LDS buffer buf against this wave's keys
   auto compute = [&](int buf, const uint4 (&bias)[2][2]) {
 #pragma unroll
@@ -213,8 +215,8 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
         f32x16 pacc = *reinterpret_cast<const f32x16*>(&ndlt_lds[(buf * R + r) * 64 + 32 * qr + g2 * 16]);
 #pragma unroll
         for (int s = 0; s < NQF; ++s) {
-          sacc = E::mma(lds_frag<T>(qt + (32 * qr + lq) * LD + s * 16 + g2 * 8), kf[r][s], sacc);
-          pacc = E::mma(lds_frag<T>(dt + (32 * qr + lq) * LD + s * 16 + g2 * 8), vf[r][s], pacc);
+          sacc = E::mma(lds_frag<T>(qt + swz_off<DP>(32 * qr + lq, s * 16 + g2 * 8)), kf[r][s], sacc);
+          pacc = E::mma(lds_frag<T>(dt + swz_off<DP>(32 * qr + lq, s * 16 + g2 * 8)), vf[r][s], pacc);
         }
         float p[16], ds[16];
 #pragma unroll
@@ -229,8 +231,9 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
           const Frag sf = pack8<T>(&ds[8 * m]);
 #pragma unroll
           for (int t = 0; t < NDT; ++t) {
-            dv[r][t] = E::mma(lds_read_tr_frag<T>(dt, LD, 32 * qr + 16 * m, 32 * t, lane), pf, dv[r][t]);
-            dk[r][t] = E::mma(lds_read_tr_frag<T>(qt, LD, 32 * qr + 16 * m, 32 * t, lane), sf, dk[r][t]);
+            const int at = (32 * qr + 16 * m) * DP + 32 * t;
+            dv[r][t] = E::mma(lds_read_tr_frag_sw<T>(dt + at, trl[t]), pf, dv[r][t]);
+            dk[r][t] = E::mma(lds_read_tr_frag_sw<T>(qt + at, trl[t]), sf, dk[r][t]);
           }
         }
       }
@@ -327,7 +330,7 @@ __global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT
   const int lq = lane & 31;
   const int g2 = lane >> 5;
 
-  int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
+  int64_t tile = xcd_tile(blockIdx.x, gridDim.x, xcd_chunk(a.uniform_tiles));
   if (tile >= a.total_tiles) return;
   const Sample* tab = reinterpret_cast<const Sample*>(a.table);
   const int H = a.num_heads;
@@ -672,20 +675,22 @@ __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(Bw
   const int lane = tid & 63;
   const int lq = lane & 31;
   const int g2 = lane >> 5;
-  const int P = a.parts;
   T* const q_w = &qw_lds[wave * 2 * 32 * QLD];
   T* const d_w = q_w + 32 * QLD;
 
-  int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
+  int64_t tile = xcd_tile(blockIdx.x, gridDim.x, xcd_chunk(a.uniform_tiles));
   if (tile >= a.total_tiles) return;
   const Sample* tab = reinterpret_cast<const Sample*>(a.table);
   const int H = a.num_heads;
   const int s_idx = find_sample(tile, tab, a.num_samples, a.uniform_tiles, [&](const Sample& s) {
-    return s.bias_mode == OOPS_BIAS_SHARED ? H * cdiv(s.Lq, 128) * cdiv(s.Lk, 64) * P : (int64_t)0;
+    return s.bias_mode == OOPS_BIAS_SHARED
+               ? H * cdiv(s.Lq, 128) * cdiv(s.Lk, 64) * parts_for(s.G, a.part_groups, a.parts)
+               : (int64_t)0;
   });
   if (s_idx < 0) return;
   const Sample& S = tab[__builtin_amdgcn_readfirstlane(s_idx)];
   const int64_t G = S.G;
+  const int P = parts_for(G, a.part_groups, a.parts);  // this sample's group ranges
   const int Lq = (int)S.Lq, Lk = (int)S.Lk;
   const int nkb = (int)cdiv(Lk, 64);
   const int nqb = (int)cdiv(Lq, 128);
@@ -964,7 +969,7 @@ hipError_t launch_dkv_fast(const oops_attn_geometry& geo, const Plan& plan, cons
     const bool pair = OOPS_DKV_ROWS == 2 && a.bias != nullptr && !plan.any_full && plan.dkv_tiles_r2 > 0;
     a.uniform_tiles = pair ? plan.dkv_uniform_r2 : plan.dkv_uniform;
     a.total_tiles = pair ? plan.dkv_tiles_r2 : plan.dkv_tiles;
-    const dim3 grid((unsigned)xcd_grid(a.total_tiles));
+    const dim3 grid((unsigned)xcd_grid(a.total_tiles, xcd_chunk(a.uniform_tiles)));
     if (pair)
       hipLaunchKernelGGL((attn_dkv_fast_kernel<T, DP, true, 2>), grid, dim3(256), 0, stream, a);
     else if (a.bias != nullptr)
@@ -985,7 +990,7 @@ hipError_t launch_dq_fast(const oops_attn_geometry& geo, const Plan& plan, const
     a.uniform_tiles = plan.fwd_uniform;
     a.total_tiles = plan.fwd_tiles;
     a.delta_in_dq = delta_in_dq ? 1 : 0;
-    const dim3 grid((unsigned)xcd_grid(plan.fwd_tiles));
+    const dim3 grid((unsigned)xcd_grid(plan.fwd_tiles, xcd_chunk(plan.fwd_uniform)));
     const bool full = a.dbias != nullptr && plan.any_full;
     auto go = [&](auto has_bias, auto masked, auto full_db) {
       hipLaunchKernelGGL((attn_dq_fast_kernel<T, DP, decltype(has_bias)::value, decltype(masked)::value,
@@ -1014,9 +1019,10 @@ hipError_t launch_dbias_fast(const oops_attn_geometry& geo, const Plan& plan, co
     BwdArgsT<T, T> a;
     fill_bwd_args(a, geo, plan, L);
     a.parts = plan.fast_parts;
+    a.part_groups = plan.fast_part_groups;
     a.uniform_tiles = plan.fast_sbias_uniform;
     a.total_tiles = plan.fast_sbias_tiles;
-    const dim3 grid((unsigned)xcd_grid(plan.fast_sbias_tiles));
+    const dim3 grid((unsigned)xcd_grid(plan.fast_sbias_tiles, xcd_chunk(plan.fast_sbias_uniform)));
     if (plan.masked_tiles)
       hipLaunchKernelGGL((attn_dbias_fast_kernel<T, DP, true>), grid, dim3(256), 0, stream, a);
     else

@@ -198,15 +198,36 @@ __device__ __forceinline__ int find_sample(int64_t& tile, const Sample* table, i
 
 __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// MI355X has 8 XCDs, each with its own L2; workgroup b of a launch runs on XCD
-// b % 8.  With a grid padded to a multiple of 8, xcd_tile maps b to a logical
-// tile so that each XCD processes one contiguous range of logical tiles.
-constexpr int kNumXcds = 8;
-__host__ __device__ __forceinline__ int64_t xcd_grid(int64_t tiles) {
-  return (tiles + kNumXcds - 1) / kNumXcds * kNumXcds;
+// Group ranges ("parts") of a sample's shared-dBias reduction when every part
+// should cover about part_groups groups: tiles of samples of different sizes
+// then cost about the same.
+__host__ __device__ __forceinline__ int parts_for(int64_t G, int64_t part_groups, int max_parts) {
+  int64_t p = (G + part_groups - 1) / part_groups;
+  if (p > max_parts) p = max_parts;
+  if (p > G) p = G;
+  return p < 1 ? 1 : (int)p;
 }
-__device__ __forceinline__ int64_t xcd_tile(int64_t block, int64_t grid) {
-  return (block % kNumXcds) * (grid / kNumXcds) + block / kNumXcds;
+
+// MI355X has 8 XCDs, each with its own L2; workgroup b of a launch runs on XCD
+// b % 8.  xcd_tile maps b to a logical tile.  chunk == 0 (tables whose
+// samples all have the same tile count): each XCD processes one contiguous
+// range of logical tiles, so neighbouring tiles (which share K/V rows and
+// bias blocks) meet in one L2.  chunk > 0 (ragged tables, where tiles of
+// different samples cost differently): runs of `chunk` consecutive tiles are
+// dealt to the XCDs in turn, so every XCD gets a like share of every sample
+// (a contiguous split would give the last XCD only the largest sample's
+// tiles).  xcd_grid pads the grid to what the mapping needs.
+constexpr int kNumXcds = 8;
+constexpr int kXcdChunk = 16;
+__host__ __device__ __forceinline__ int xcd_chunk(int64_t uniform_tiles) { return uniform_tiles ? 0 : kXcdChunk; }
+__host__ __device__ __forceinline__ int64_t xcd_grid(int64_t tiles, int chunk) {
+  const int64_t m = (int64_t)kNumXcds * (chunk > 0 ? chunk : 1);
+  return (tiles + m - 1) / m * m;
+}
+__device__ __forceinline__ int64_t xcd_tile(int64_t block, int64_t grid, int chunk) {
+  const int64_t x = block % kNumXcds, j = block / kNumXcds;
+  if (chunk == 0) return x * (grid / kNumXcds) + j;
+  return ((j / chunk) * kNumXcds + x) * chunk + j % chunk;
 }
 // Heads whose D-element rows together fill one 128-byte line.
 __host__ __forceinline__ int head_group(const oops_attn_geometry& geo) {

@@ -145,6 +145,31 @@ template <int DP>
 __device__ __forceinline__ int swz_off(int row, int col) {
   return row * DP + ((((col >> 3) ^ swz<DP>(row))) << 3) + (col & 7);
 }
+// Transposed fragment reads (lds_read_tr_frag) from a swizzled tile: the
+// lane-dependent part of the two element offsets, valid for every r0 that is
+// a multiple of 16 and, with 32-element rows, every c0 that is a multiple of
+// 32 (then the swizzle leaves r0 * DP + c0 unchanged; 64-element rows keep
+// one pair per 32-column half).
+struct TrLane {
+  int lo, hi;
+};
+template <int DP>
+__device__ __forceinline__ TrLane tr_lane(int lane, int c0) {
+  const int j = lane & 15;
+  const int grp = lane >> 4;
+  const int col = c0 + ((grp & 1) << 4) + ((j & 3) << 2);
+  const int row = ((grp >> 1) << 2) + (j >> 2);
+  return TrLane{swz_off<DP>(row, col) - c0, swz_off<DP>(row + 8, col) - c0};
+}
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::Frag lds_read_tr_frag_sw(const T* at, const TrLane& tl) {
+  const s16x4 lo = lds_read_tr4(at + tl.lo);
+  const s16x4 hi = lds_read_tr4(at + tl.hi);
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(typename Elem<T>::Frag, v);
+}
+
 // 16 bytes per lane from a buffer resource into 64 consecutive LDS slots
 // starting at lds (wave-uniform); an out-of-range offset writes zeros
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, const void* lds, uint32_t voff, uint32_t soff) {

@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
   // (head group, group g, head in group, query block): the query blocks of
   // one (g, head group) share K/V in one L2, and each XCD sees the bias of
   // only its head group.
-  int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
+  int64_t tile = xcd_tile(blockIdx.x, gridDim.x, xcd_chunk(a.uniform_tiles));
   if (tile >= a.total_tiles) return;
   const Sample* tab = reinterpret_cast<const Sample*>(a.table);
   const int H = a.num_heads;
@@ -483,7 +483,7 @@ bool launch_forward_fast(const oops_attn_geometry& geo, const Plan& plan, const 
     a.bf_sample_stride = plan.bf_sample_stride;
     a.bf_nqt = plan.bf_nqt;
     a.bf_nkt = plan.bf_nkt;
-    const dim3 grid((unsigned)xcd_grid(plan.fwd_tiles));
+    const dim3 grid((unsigned)xcd_grid(plan.fwd_tiles, xcd_chunk(plan.fwd_uniform)));
     auto go = [&](auto has_bias, auto masked) {
       hipLaunchKernelGGL((attn_fwd_fast_kernel<T, DP, decltype(has_bias)::value, decltype(masked)::value>), grid,
                          dim3(256), 0, stream, a);

@@ -56,6 +56,7 @@ struct BwdArgsT {
   int head_size;
   int vec_ok;
   int parts;
+  int64_t part_groups;  // > 0: per-sample parts, parts_for(G, part_groups, parts) (fast dBias)
   int head_group;
   float scale;
   const T* bias_frag;        // as in FwdArgsT
@@ -128,7 +129,8 @@ struct Plan {
   int64_t dbias_extent = 0;                      // floats
   int parts = 1;                                 // group ranges of the shared dBias reduction
   int64_t fast_sbias_tiles = 0, fast_sbias_uniform = 0;  // same, 64-key blocks (fast path)
-  int fast_parts = 1;
+  int fast_parts = 1;                            // largest per-sample part count (fast path)
+  int64_t fast_part_groups = 1;                  // groups per part the fast path aims at
   bool any_full = false, any_shared = false;
   bool any_pair_mask = false;                    // a mask that depends on the query
   bool masked_tiles = false;                     // some 64-key tile has masked or out-of-range keys
@@ -198,6 +200,7 @@ inline void fill_bwd_args(BwdArgsT<T, BT>& a, const oops_attn_geometry& geo, con
   a.head_size = geo.head_size;
   a.vec_ok = geo.vec_ok;
   a.parts = plan.parts;
+  a.part_groups = 0;
   a.head_group = head_group_of(geo);
   a.scale = geo.scale;
   a.bias_frag = static_cast<const T*>(L.bias_frag);

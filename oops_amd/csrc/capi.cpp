@@ -135,11 +135,30 @@ int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
     plan.parts = (int)std::max<int64_t>(parts, 1);
     plan.sbias_tiles = sbias_base * plan.parts;
     plan.sbias_uniform = u_sb && c_sb > 0 ? c_sb * plan.parts : 0;
-    int64_t fparts = cdiv(kTargetSharedBiasBlocks, std::max<int64_t>(sbias_base64, 1));
-    fparts = std::min<int64_t>({fparts, kMaxParts, min_shared_groups});
-    plan.fast_parts = (int)std::max<int64_t>(fparts, 1);
-    plan.fast_sbias_tiles = sbias_base64 * plan.fast_parts;
-    plan.fast_sbias_uniform = u_sb64 && c_sb64 > 0 ? c_sb64 * plan.fast_parts : 0;
+    // fast path: parts per sample, each covering about the same number of
+    // groups, with about kTargetSharedBiasBlocks workgroups in all
+    int64_t units = 0;
+    for (int s = 0; s < geo->num_samples; ++s) {
+      const Sample& S = tab[s];
+      if (S.bias_mode == OOPS_BIAS_SHARED) units += H * cdiv(S.Lq, 128) * cdiv(S.Lk, 64) * S.G;
+    }
+    plan.fast_part_groups = std::max<int64_t>(cdiv(units, kTargetSharedBiasBlocks), 1);
+    plan.fast_parts = 1;
+    plan.fast_sbias_tiles = 0;
+    int64_t c_f = -1;
+    bool u_f = true;
+    for (int s = 0; s < geo->num_samples; ++s) {
+      const Sample& S = tab[s];
+      int64_t c = 0;
+      if (S.bias_mode == OOPS_BIAS_SHARED) {
+        const int p = oops::parts_for(S.G, plan.fast_part_groups, kMaxParts);
+        c = H * cdiv(S.Lq, 128) * cdiv(S.Lk, 64) * p;
+        plan.fast_parts = std::max(plan.fast_parts, p);
+      }
+      plan.fast_sbias_tiles += c;
+      track(c, c_f, u_f);
+    }
+    plan.fast_sbias_uniform = u_f && c_f > 0 ? c_f : 0;
     int64_t c_red = -1;
     bool u_red = true;
     for (int s = 0; s < geo->num_samples; ++s) {
