@@ -113,6 +113,7 @@ def _vec_ok(table: Sequence[int], tensors: Sequence[Optional[Tensor]], bias: Opt
         _lib.T_Q_OFF, _lib.T_Q_SG, _lib.T_Q_SH, _lib.T_Q_SI,
         _lib.T_K_OFF, _lib.T_K_SG, _lib.T_K_SH, _lib.T_K_SI,
         _lib.T_V_OFF, _lib.T_V_SG, _lib.T_V_SH, _lib.T_V_SI,
+        _lib.T_DO_OFF, _lib.T_DO_SG, _lib.T_DO_SH, _lib.T_DO_SI,
     )  # fmt: skip
     bce = 16 // bias.element_size() if bias is not None else 1
     bcols = (_lib.T_B_OFF, _lib.T_B_SG, _lib.T_B_SH, _lib.T_B_SI)
@@ -143,6 +144,63 @@ def _geometry(q: Tensor, bias: Optional[Tensor], mask: Optional[Tensor], table: 
     geo.table_host = host.data_ptr()
     geo.table_device = dev.data_ptr()
     return geo, (host, dev)
+
+
+def _remap_dout(table: List[int], out: Tensor, dout: Tensor, num_heads: int) -> Optional[List[int]]:
+    """``table`` with its dO columns rewritten for ``dout``'s strides, or None.
+
+    The rows address the output (dense in some dimension order) as
+    ``off + g*s_g + h*s_h + i*s_i + d``.  Each of those terms is decomposed
+    into coordinates of the output's dimensions; when no row's index box
+    carries across a dimension, the same coordinates give dO's offsets with
+    dO's strides (zero strides of an expanded gradient included).  Returns
+    None when that does not hold or dO's last dimension is not unit-stride.
+    """
+
+    if dout.shape != out.shape or out.dim() == 0 or (dout.size(-1) > 1 and dout.stride(-1) != 1):
+        return None
+    sizes, ost, dst = out.shape, out.stride(), dout.stride()
+    order = sorted((d for d in range(out.dim()) if sizes[d] > 1), key=lambda d: -ost[d])
+    expect = 1
+    for d in reversed(order):  # dense, non-overlapping over the non-trivial dims
+        if ost[d] != expect:
+            return None
+        expect *= sizes[d]
+
+    def coords(x: int) -> Optional[List[int]]:
+        c = []
+        for d in order:
+            q, x = divmod(x, ost[d])
+            c.append(q)
+        return c if x == 0 else None
+
+    width = _lib.TABLE_WIDTH
+    new = list(table)
+    for s in range(len(table) // width):
+        row = table[s * width : (s + 1) * width]
+        counts = (1, row[_lib.T_GROUPS] - 1, num_heads - 1, row[_lib.T_LEN_Q] - 1)
+        terms = row[_lib.T_O_OFF : _lib.T_O_OFF + 4]
+        cols = []
+        span = [0] * len(order)
+        for value, n in zip(terms, counts):
+            if n == 0:
+                cols.append(0)
+                continue
+            c = coords(int(value))
+            if c is None:
+                return None
+            for k in range(len(order)):
+                span[k] += c[k] * n
+            cols.append(sum(ck * dst[d] for ck, d in zip(c, order)))
+        unit = coords(1)  # the head-dim step (d = 0 .. D-1)
+        if unit is None:
+            return None
+        for k in range(len(order)):
+            span[k] += unit[k] * (sizes[-1] - 1)
+        if any(span[k] >= sizes[d] for k, d in enumerate(order)):
+            return None
+        new[s * width + _lib.T_DO_OFF : s * width + _lib.T_DO_OFF + 4] = cols
+    return new
 
 
 def _ptr(t: Optional[Tensor]) -> Optional[int]:
@@ -223,8 +281,13 @@ def attention_backward(
     if dout.dtype != out.dtype:
         dout = dout.to(out.dtype)
     if dout.stride() != out.stride():
-        # the kernels read dO with the output's (= query's) layout
-        dout = torch.empty_strided(out.size(), out.stride(), dtype=out.dtype, device=out.device).copy_(dout)
+        # the kernels read dO through its own table columns: re-express them
+        # for dO's strides, or copy dO into the output's layout
+        remapped = _remap_dout(table, out, dout, num_heads)
+        if remapped is None:
+            dout = torch.empty_strided(out.size(), out.stride(), dtype=out.dtype, device=out.device).copy_(dout)
+        else:
+            table = remapped
     need_q, need_k, need_v, need_b = needs
 
     def like(t: Tensor, need: bool) -> Tensor:

@@ -150,3 +150,36 @@ def test_nested_contract_on_cpu():
         sizes = [(n, 1, 2, n, 8) for n in (3, 5)]
         odd = NestedTensor(ragged_dims=(0, 3), _sizes=sizes, _concat=torch.randn(34, 1, 2, 8))
         triangle_attention(odd, odd, odd)
+
+
+@pytest.mark.parametrize(
+    "make_dout, remapped",
+    [
+        (lambda s: torch.randn(s), True),  # contiguous (S, H, N, c): the usual upstream gradient
+        (lambda s: torch.randn(s[0], s[2], s[1], s[3]).permute(0, 2, 1, 3), True),  # the output's own layout
+        (lambda s: torch.randn(s[0], s[1], s[3], s[2]).transpose(-1, -2), False),  # head dim not unit-stride
+        (lambda s: torch.randn(1, 1, 1, 1).expand(s), False),  # expanded: copied
+    ],
+)
+def test_dout_table_remap(make_dout, remapped):
+    """The backward reads dO through its own table columns when its layout differs from the output's."""
+
+    from oops_amd import _lib
+    from oops_amd.attention import _core
+
+    s_, h, n, c = 5, 3, 7, 8
+    q = torch.randn(s_, n, h, c).permute(0, 2, 1, 3)  # head-major view of (S, N, H, c) memory
+    out = torch.empty_strided(q.size(), q.stride())
+    cols = (0, q.stride(0), q.stride(1), q.stride(2))
+    table = _core.table_row(groups=s_, len_q=n, len_k=n, q=cols, k=cols, v=cols)
+    dout = make_dout(q.shape)
+    new = _core._remap_dout(table, out, dout, h)
+    assert (new is not None) == remapped
+    if new is None:
+        return
+    off, sg, sh, si = new[_lib.T_DO_OFF : _lib.T_DO_OFF + 4]
+    g, hh, i, d = torch.meshgrid(*(torch.arange(x) for x in q.shape), indexing="ij")
+    flat = torch.as_strided(dout, (dout.untyped_storage().nbytes() // 4,), (1,), 0)
+    got = flat[dout.storage_offset() + off + g * sg + hh * sh + i * si + d]
+    torch.testing.assert_close(got, dout, rtol=0, atol=0)
+    assert new[: _lib.T_DO_OFF] == table[: _lib.T_DO_OFF]

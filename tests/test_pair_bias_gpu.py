@@ -243,3 +243,24 @@ def test_errors():
         pair_bias_attention(q, q, q, torch.ones(2, 5, device=DEV))
     with pytest.raises(OOpsUnsupportedError):  # bias batch mismatch
         pair_bias_attention(q, q, q, None, torch.randn(3, 2, 5, 5, device=DEV))
+
+
+@pytest.mark.parametrize("dout_layout", ["contiguous", "output"])
+def test_dout_layout_independent(dout_layout):
+    """dO in its own layout (read through remapped table columns) gives the same gradients, bit for bit."""
+
+    g = torch.Generator().manual_seed(11)
+    s_, n, h, c = 6, 70, 4, 32
+    q, k, v = (torch.randn(s_, n, h, c, generator=g).to(torch.bfloat16).permute(0, 2, 1, 3).to(DEV)
+               for _ in range(3))  # fmt: skip
+    mask = (torch.rand(s_, n, generator=g) > 0.2).to(DEV)
+    bias = torch.randn(1, h, n, n, generator=g).to(torch.bfloat16).to(DEV)
+    base = torch.randn(s_, h, n, c, generator=g).to(torch.bfloat16)
+    dout = base.to(DEV) if dout_layout == "contiguous" else base.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3).to(DEV)
+    results = []
+    for d in (dout, torch.empty_strided(q.shape, q.stride(), dtype=q.dtype, device=DEV).copy_(dout)):
+        leaves = [t.detach().clone().requires_grad_(True) for t in (q, k, v, bias)]
+        out = pair_bias_attention(leaves[0], leaves[1], leaves[2], mask, leaves[3])
+        results.append(torch.autograd.grad(out, leaves, d))
+    for got, want in zip(*results):
+        torch.testing.assert_close(got, want, rtol=0, atol=0)
