@@ -157,10 +157,26 @@ def measured_traffic(kernel):
 KERNEL_GEMMS = {"fwd": 2, "dq": 3, "dkv": 4, "dbias": 2}
 
 
-def _median_ms(fn, iters=10, warmup=3):
+def _median_ms(fn, iters=10, warmup=3, reps=3):
+    """ms per call of `iters` back-to-back calls (median of `reps` runs): the
+    host enqueues while the GPU works, as in a training loop."""
+
     import torch
 
-    return time_events(fn, iters, warmup, torch.cuda.current_stream())
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        fn()
+    runs = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        for _ in range(iters):
+            fn()
+        b.record(stream)
+        b.synchronize()
+        runs.append(a.elapsed_time(b) / iters)
+    return statistics.median(runs)
 
 
 def other_configs(device):

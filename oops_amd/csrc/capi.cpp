@@ -24,6 +24,11 @@ int fail(int code, const char* fmt, long long a = 0, long long b = 0) {
 constexpr int64_t kMaxGrid = (int64_t(1) << 31) - 1;
 constexpr int64_t kTargetSharedBiasBlocks = 2048;  // 8 workgroups per CU on 256 CUs
 constexpr int kMaxParts = 64;
+#ifndef OOPS_MIN_PART_GROUPS
+#define OOPS_MIN_PART_GROUPS 32
+#endif
+// a dBias part shorter than this spends more on its set-up and partial-sum store than on groups
+constexpr int64_t kMinPartGroups = OOPS_MIN_PART_GROUPS;
 constexpr size_t kMaxBiasFragBytes = size_t(1) << 30;
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -142,7 +147,7 @@ int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
       const Sample& S = tab[s];
       if (S.bias_mode == OOPS_BIAS_SHARED) units += H * cdiv(S.Lq, 128) * cdiv(S.Lk, 64) * S.G;
     }
-    plan.fast_part_groups = std::max<int64_t>(cdiv(units, kTargetSharedBiasBlocks), 1);
+    plan.fast_part_groups = std::max<int64_t>(cdiv(units, kTargetSharedBiasBlocks), kMinPartGroups);
     plan.fast_parts = 1;
     plan.fast_sbias_tiles = 0;
     int64_t c_f = -1;
