@@ -368,7 +368,7 @@ __global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT
   const int64_t lidx = S.l_off + ((int64_t)g * H + h) * Lq + q_lane;
   const float neg_lse = qv ? -a.lse[lidx] : 0.0f;
   Frag qf[NQF], df[NQF];
-  f32x16 ndelta;
+  float ndelta;  // -delta of this lane's query (subtracted from dP in the VALU)
   {
     // The wave's 32 query rows of Q and dO are read whole (DP/8 lanes per
     // row, 16-byte chunks), staged through a wave-private region of the K/V
@@ -448,8 +448,7 @@ __global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT
     } else {
       dl = qv ? a.delta[lidx] : 0.0f;
     }
-#pragma unroll
-    for (int j = 0; j < 16; ++j) ndelta[j] = -dl;
+    ndelta = -dl;
   }
   Frag ident[2];
   identity_frags<T>(ident, 1.0f / a.scale, lane);
@@ -558,7 +557,7 @@ __global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT
       } else {
         sacc = f32x16{};
       }
-      f32x16 pacc = ndelta;
+      f32x16 pacc = f32x16{};
 #pragma unroll
       for (int s = 0; s < NQF; ++s) {
         sacc = E::mma(lds_frag<T>(kt + (32 * t2 + lq) * LD + s * 16 + g2 * 8), qf[s], sacc);
@@ -572,7 +571,7 @@ __global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT
           const int kk = 32 * t2 + ((j >> 2) << 3) + (j & 3);
           p = ((lb >> kk) & 1) ? p : 0.0f;
         }
-        ds[j] = p * pacc[j];
+        ds[j] = p * (pacc[j] + ndelta);
       }
       if (FULL_DBIAS && dbrow) {
         const int k0 = t * 64 + 32 * t2;
