@@ -138,6 +138,58 @@ int oops_attn_backward(const oops_attn_geometry* geo, const void* q, const void*
                        const float* lse, const void* dout, void* dq, void* dk, void* dv, float* dbias, void* workspace,
                        size_t workspace_bytes, void* stream);
 
+/* ---- gated output stage: gated = sigmoid(single . W^T) (*) attention ----
+ *
+ * One row per query token over all prefixes; gate channel n = h * D + d.
+ * single [rows][C] (channels contiguous, row stride s_row), W [H*D][C]
+ * (row stride w_row), attention element (row, h, d) at
+ *     b * a_sb + s * a_sg + t * a_st + h * a_sh + d * a_sd
+ * with row = (b * groups + s) * tokens + t; gated, logits, grad and the two
+ * gradients are [rows][H*D] row-major.  Rounding follows the reference: the
+ * logits are rounded to dtype, the gate sigmoid(logits) is rounded to dtype
+ * before the product.  The output projection and the weight/single
+ * gradients are plain GEMMs left to the caller's BLAS.
+ *
+ * Reference interfaces replaced:
+ *   oops_gate_projection_forward <- Triton _gate_projection_forward /
+ *                          _gate_projection_inference and _launch_projection
+ *                          (oops/attention/gate/triton/kernel.py:117-286,
+ *                           oops/attention/gate/triton/generic.py:183-262)
+ *   oops_gate_multiply_forward   <- Triton _gate_forward and
+ *                          _attention_gate_multiply_forward_impl
+ *                          (kernel.py:39-66, generic.py:71-100)
+ *   oops_gate_multiply_backward  <- Triton _gate_backward and
+ *                          _attention_gate_multiply_backward_impl
+ *                          (kernel.py:69-114, generic.py:103-141) */
+typedef struct oops_gate_geometry {
+  int32_t dtype;    /* OOPS_F32 / OOPS_BF16 / OOPS_F16 of every operand */
+  int32_t heads;    /* H */
+  int32_t width;    /* D */
+  int32_t channels; /* C (projection only) */
+  int64_t rows;     /* tokens over all prefixes */
+  int64_t tokens;   /* tokens per (batch, group) prefix */
+  int64_t groups;   /* groups per batch element */
+  int64_t a_sb, a_sg, a_st, a_sh, a_sd; /* attention strides in elements */
+  int64_t s_row;    /* single row stride in elements */
+  int64_t w_row;    /* weight row stride in elements */
+} oops_gate_geometry;
+
+/* Fused gate projection (16-bit dtypes; C a multiple of 8, D a multiple of
+ * 16, a_sd = 1, 16-byte aligned rows): logits = single . W^T (MFMA, f32
+ * accumulation) and gated.  logits may be NULL (inference). */
+int oops_gate_projection_forward(const oops_gate_geometry* geo, const void* single, const void* weight,
+                                 const void* attention, void* gated, void* logits, void* stream);
+
+/* gated = round(sigmoid(logits)) * attention from precomputed logits (any dtype). */
+int oops_gate_multiply_forward(const oops_gate_geometry* geo, const void* attention, const void* logits,
+                               void* gated, void* stream);
+
+/* grad_attention = grad * g and grad_logits = sigmoid'(logits) * grad * attention,
+ * g = round(sigmoid(logits)), with the reference's roundings; either output may
+ * be NULL. */
+int oops_gate_multiply_backward(const oops_gate_geometry* geo, const void* attention, const void* logits,
+                                const void* grad, void* grad_attention, void* grad_logits, void* stream);
+
 /* Thread-local description of the last failure (empty string if none). */
 const char* oops_last_error(void);
 

@@ -5,6 +5,12 @@ is the drop-in for ``from oops import ...`` on the attention path.
 """
 
 from ._errors import OOpsUnsupportedError
-from .attention import pair_bias_attention, triangle_attention
+from .attention import gate_attention_output, gated_pair_bias_attention, pair_bias_attention, triangle_attention
 
-__all__ = ["OOpsUnsupportedError", "pair_bias_attention", "triangle_attention"]
+__all__ = [
+    "OOpsUnsupportedError",
+    "gate_attention_output",
+    "gated_pair_bias_attention",
+    "pair_bias_attention",
+    "triangle_attention",
+]

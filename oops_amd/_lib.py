@@ -18,7 +18,7 @@ F32, BF16, F16 = 0, 1, 2
 BIAS_NONE, BIAS_FULL, BIAS_SHARED = 0, 1, 2
 PHASE_DELTA, PHASE_DQ, PHASE_DKV, PHASE_DBIAS = 1, 2, 4, 8
 TABLE_WIDTH = 40
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # geometry table columns (enum oops_table_column)
 (
@@ -40,6 +40,9 @@ EXPORTED_SYMBOLS = (
     "oops_attn_forward_workspace_bytes",
     "oops_attn_backward_workspace_bytes",
     "oops_attn_backward",
+    "oops_gate_projection_forward",
+    "oops_gate_multiply_forward",
+    "oops_gate_multiply_backward",
     "oops_last_error",
     "oops_abi_version",
 )
@@ -60,6 +63,25 @@ class Geometry(ctypes.Structure):
         ("force_generic", ctypes.c_int32),
         ("table_host", ctypes.c_void_p),
         ("table_device", ctypes.c_void_p),
+    ]
+
+
+class GateGeometry(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("width", ctypes.c_int32),
+        ("channels", ctypes.c_int32),
+        ("rows", ctypes.c_int64),
+        ("tokens", ctypes.c_int64),
+        ("groups", ctypes.c_int64),
+        ("a_sb", ctypes.c_int64),
+        ("a_sg", ctypes.c_int64),
+        ("a_st", ctypes.c_int64),
+        ("a_sh", ctypes.c_int64),
+        ("a_sd", ctypes.c_int64),
+        ("s_row", ctypes.c_int64),
+        ("w_row", ctypes.c_int64),
     ]
 
 
@@ -95,6 +117,13 @@ def load() -> ctypes.CDLL:
         lib.oops_attn_backward_workspace_bytes.restype = sz
         lib.oops_attn_backward.argtypes = [geo, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
         lib.oops_attn_backward.restype = i32
+        gg = ctypes.POINTER(GateGeometry)
+        lib.oops_gate_projection_forward.argtypes = [gg, vp, vp, vp, vp, vp, vp]
+        lib.oops_gate_projection_forward.restype = i32
+        lib.oops_gate_multiply_forward.argtypes = [gg, vp, vp, vp, vp]
+        lib.oops_gate_multiply_forward.restype = i32
+        lib.oops_gate_multiply_backward.argtypes = [gg, vp, vp, vp, vp, vp, vp]
+        lib.oops_gate_multiply_backward.restype = i32
         lib.oops_last_error.argtypes = []
         lib.oops_last_error.restype = ctypes.c_char_p
         lib.oops_abi_version.argtypes = []

@@ -9,6 +9,7 @@
 #include <string>
 
 #include "attn_kernels.h"
+#include "gate_kernels.h"
 
 namespace {
 
@@ -219,11 +220,29 @@ int check_workspace(void* workspace, size_t ws_bytes, size_t need) {
   return OOPS_OK;
 }
 
+int check_gate(const oops_gate_geometry* g) {
+  if (g == nullptr) return fail(OOPS_EINVAL, "gate geometry is NULL");
+  if (g->dtype < OOPS_F32 || g->dtype > OOPS_F16) return fail(OOPS_EINVAL, "unknown dtype %lld", g->dtype);
+  if (g->heads <= 0 || g->width <= 0)
+    return fail(OOPS_EINVAL, "heads and width must be positive, got %lld and %lld", g->heads, g->width);
+  if (g->rows < 0 || g->tokens <= 0 || g->groups <= 0)
+    return fail(OOPS_EINVAL, "rows must be >= 0 and tokens, groups positive");
+  if (g->rows % g->tokens) return fail(OOPS_EINVAL, "rows (%lld) must be a multiple of tokens (%lld)", g->rows, g->tokens);
+  if ((int64_t)g->heads * g->width > (int64_t(1) << 20)) return fail(OOPS_EINVAL, "heads * width too large");
+  return OOPS_OK;
+}
+
+int gate_launch_result(hipError_t err, const char* what) {
+  if (err == hipSuccess) return OOPS_OK;
+  g_last_error = std::string(what) + " launch failed: " + hipGetErrorString(err);
+  return OOPS_ELAUNCH;
+}
+
 }  // namespace
 
 extern "C" {
 
-int oops_abi_version(void) { return 2; }
+int oops_abi_version(void) { return 3; }
 
 const char* oops_last_error(void) { return g_last_error.c_str(); }
 
@@ -282,6 +301,43 @@ int oops_attn_backward(const oops_attn_geometry* geo, const void* q, const void*
     return OOPS_ELAUNCH;
   }
   return OOPS_OK;
+}
+
+int oops_gate_projection_forward(const oops_gate_geometry* geo, const void* single, const void* weight,
+                                 const void* attention, void* gated, void* logits, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_gate(geo)) return rc;
+  if (geo->channels <= 0) return fail(OOPS_EINVAL, "channels must be positive, got %lld", geo->channels);
+  if (!single || !weight || !attention || !gated)
+    return fail(OOPS_EINVAL, "single, weight, attention and gated must be non-NULL");
+  if (!oops::gate_projection_ok(*geo, single, weight, attention, gated, logits))
+    return fail(OOPS_EINVAL,
+                "the fused gate projection needs 16-bit operands, channels %% 8 == 0, width %% 16 == 0, "
+                "unit-stride attention channels and 16-byte aligned rows");
+  return gate_launch_result(oops::launch_gate_projection(*geo, single, weight, attention, gated, logits,
+                                                         static_cast<hipStream_t>(stream)),
+                            "gate projection");
+}
+
+int oops_gate_multiply_forward(const oops_gate_geometry* geo, const void* attention, const void* logits,
+                               void* gated, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_gate(geo)) return rc;
+  if (!attention || !logits || !gated) return fail(OOPS_EINVAL, "attention, logits and gated must be non-NULL");
+  return gate_launch_result(
+      oops::launch_gate_multiply_forward(*geo, attention, logits, gated, static_cast<hipStream_t>(stream)),
+      "gate multiply forward");
+}
+
+int oops_gate_multiply_backward(const oops_gate_geometry* geo, const void* attention, const void* logits,
+                                const void* grad, void* grad_attention, void* grad_logits, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_gate(geo)) return rc;
+  if (!logits || !grad) return fail(OOPS_EINVAL, "logits and grad must be non-NULL");
+  if (grad_logits && !attention) return fail(OOPS_EINVAL, "grad_logits needs the attention values");
+  return gate_launch_result(oops::launch_gate_multiply_backward(*geo, attention, logits, grad, grad_attention,
+                                                                grad_logits, static_cast<hipStream_t>(stream)),
+                            "gate multiply backward");
 }
 
 }  // extern "C"

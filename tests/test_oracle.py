@@ -170,3 +170,85 @@ def test_pair_bias_vs_sdpa(mask_kind):
     tgrads = torch.autograd.grad(ref, (tq, tk, tv, tb), torch.tensor(do))
     for mine, theirs in zip(grads, tgrads):
         np.testing.assert_allclose(mine, theirs.numpy(), atol=1e-11)
+
+
+# ------------------------------------------------------------------ gate oracle
+
+
+def test_gate_docstring_example():
+    """The reference's own example (gate_attention_output.py:73-81): zero gate logits halve the values."""
+
+    from oracle import gate as gora
+
+    out, _, _ = gora.gate_attention_output_forward(np.ones((1, 1, 2)), np.zeros((1, 3)), np.zeros((2, 3)), np.ones((1, 2)))
+    assert out.tolist() == [[1.0]]
+
+
+def test_gate_vs_torch_autograd():
+    """Forward and all four gradients against torch autograd of the composition (float64)."""
+
+    from oracle import gate as gora
+
+    g = torch.Generator().manual_seed(0)
+    att = torch.randn(2, 3, 4, 5, 8, generator=g, dtype=torch.float64, requires_grad=True)  # (B, S, H, Q, D)
+    single = torch.randn(2, 3, 5, 7, generator=g, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(32, 7, generator=g, dtype=torch.float64, requires_grad=True)
+    wo = torch.randn(6, 32, generator=g, dtype=torch.float64, requires_grad=True)
+    flat = att.transpose(-3, -2).reshape(2, 3, 5, 32)
+    out = F.linear(torch.sigmoid(F.linear(single, w)) * flat, wo)
+    dy = torch.randn(out.shape, generator=g, dtype=torch.float64)
+    want = torch.autograd.grad(out, (att, single, w, wo), dy)
+    got_out, _, _ = gora.gate_attention_output_forward(att.detach().numpy(), single.detach().numpy(),
+                                                       w.detach().numpy(), wo.detach().numpy())
+    np.testing.assert_allclose(got_out, out.detach().numpy(), rtol=1e-12, atol=1e-12)
+    got = gora.gate_attention_output_backward(att.detach().numpy(), single.detach().numpy(), w.detach().numpy(),
+                                              wo.detach().numpy(), dy.numpy())
+    for a, b in zip(got, want):
+        np.testing.assert_allclose(a, b.numpy(), rtol=1e-10, atol=1e-10)
+
+
+def test_gate_finite_differences():
+    """The written-out derivative against central differences of the forward."""
+
+    from oracle import gate as gora
+
+    rng = np.random.default_rng(1)
+    att = rng.standard_normal((2, 3, 4))  # (H, Q, D)
+    single = rng.standard_normal((3, 5))
+    w = rng.standard_normal((8, 5))
+    wo = rng.standard_normal((2, 8))
+    dy = rng.standard_normal((3, 2))
+    grads = gora.gate_attention_output_backward(att, single, w, wo, dy)
+    eps = 1e-6
+    for i, x in enumerate((att, single, w, wo)):
+        fd = np.zeros_like(x)
+        for idx in np.ndindex(x.shape):
+            xp, xm = x.copy(), x.copy()
+            xp[idx] += eps
+            xm[idx] -= eps
+            args_p = [att, single, w, wo]
+            args_m = [att, single, w, wo]
+            args_p[i], args_m[i] = xp, xm
+            fp = (gora.gate_attention_output_forward(*args_p)[0] * dy).sum()
+            fm = (gora.gate_attention_output_forward(*args_m)[0] * dy).sum()
+            fd[idx] = (fp - fm) / (2 * eps)
+        np.testing.assert_allclose(grads[i], fd, rtol=1e-5, atol=1e-6)
+
+
+def test_gate_rounding_points_vs_torch_bf16():
+    """With bf16 rounding the oracle's stored intermediates equal torch's bf16 composition."""
+
+    from oracle import gate as gora
+
+    g = torch.Generator().manual_seed(2)
+    att = torch.randn(3, 4, 9, 16, generator=g).to(torch.bfloat16)
+    single = torch.randn(3, 9, 24, generator=g).to(torch.bfloat16)
+    w = torch.randn(64, 24, generator=g).to(torch.bfloat16)
+    wo = torch.randn(8, 64, generator=g).to(torch.bfloat16)
+    logits = torch.nn.functional.linear(single.float(), w.float()).to(torch.bfloat16)
+    gate = torch.sigmoid(logits.float()).to(torch.bfloat16)
+    gated = (gate.float() * att.transpose(-3, -2).reshape(3, 9, 64).float()).to(torch.bfloat16)
+    _, got_gated, got_logits = gora.gate_attention_output_forward(
+        att.double().numpy(), single.double().numpy(), w.double().numpy(), wo.double().numpy(), rounding="bf16")
+    np.testing.assert_array_equal(got_logits, logits.double().numpy())
+    np.testing.assert_array_equal(got_gated, gated.double().numpy())
