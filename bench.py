@@ -263,6 +263,68 @@ def other_configs(device):
     return res
 
 
+def gate_stage(device):
+    """The gated output stage (the row after attention) at config 4's MSA shape.
+
+    rows = S x N = 512 x 384 tokens, H = 8, D = 32 (gate width 256), single
+    C = 256, output width 256, bf16.  Reports the fused gate-projection kernel
+    (logits GEMM + sigmoid + product, HIP events on its launch stream) against
+    HBM, the backward elementwise kernel likewise, and the whole
+    gate_attention_output fwd+bwd (which adds the output projection and the
+    weight/single gradients as library GEMMs).
+    """
+
+    import torch
+
+    from oops_amd import gate_attention_output
+    from oops_amd.attention import gate as gate_mod
+
+    s_, n, h, d, c, o = 512, 384, 8, 32, 256, 256
+    g = torch.Generator().manual_seed(3)
+    att = torch.randn(s_, n, h, d, generator=g).to(torch.bfloat16).to(device).permute(0, 2, 1, 3)  # (S, H, N, D)
+    single = torch.randn(s_, n, c, generator=g).to(torch.bfloat16).to(device)
+    w = (torch.randn(h * d, c, generator=g) / c**0.5).to(torch.bfloat16).to(device)
+    wo = (torch.randn(o, h * d, generator=g) / (h * d) ** 0.5).to(torch.bfloat16).to(device)
+    dy = torch.randn(s_, n, o, generator=g).to(torch.bfloat16).to(device)
+    rows, width = s_ * n, h * d
+    att5 = att.transpose(-3, -2).unsqueeze(0)
+    single_rows = single.reshape(rows, c)
+    stream = torch.cuda.current_stream()
+    fwd = lambda: gate_mod.gate_forward(att5, single_rows, w, True)
+    _, logits = fwd()
+    fwd_ms = time_events(fwd, 20, 3, stream)
+    grad = torch.randn(rows, width, generator=g).to(torch.bfloat16).to(device)
+    bwd = lambda: gate_mod.gate_backward(grad, att5, logits, True, True)
+    bwd_ms = time_events(bwd, 20, 3, stream)
+    fwd_bytes = 2 * (rows * c + width * c + 3 * rows * width)  # single, W, attention read; gated, logits written
+    bwd_bytes = 2 * 5 * rows * width  # logits, grad, attention read; two gradients written
+    leaves = [t.requires_grad_(True) for t in (att, single, w, wo)]
+
+    def step():
+        out = gate_attention_output(*leaves)
+        torch.autograd.grad(out, leaves, dy)
+
+    step_ms = _median_ms(step)
+    return {
+        "workload": "gate_attention_output fwd+bwd, rows 512x384, H=8, D=32, C=256, O=256, bf16",
+        "ms_fwd_bwd": round(step_ms, 4),
+        "projection_kernel": {
+            "ms": round(fwd_ms, 4),
+            "bound": "hbm",
+            "achieved_gbps": round(fwd_bytes / fwd_ms / 1e6, 1),
+            "peak_gbps": 8000.0,
+            "frac": round(fwd_bytes / fwd_ms / 1e6 / 8000.0, 4),
+            "tflops": round(2 * rows * width * c / fwd_ms / 1e9, 1),
+        },
+        "backward_kernel": {
+            "ms": round(bwd_ms, 4),
+            "bound": "hbm",
+            "achieved_gbps": round(bwd_bytes / bwd_ms / 1e6, 1),
+            "frac": round(bwd_bytes / bwd_ms / 1e6 / 8000.0, 4),
+        },
+    }
+
+
 def cpu_baseline(budget_s=15.0):
     """The numpy oracle (float32) on a bounded sample of rows of the same workload."""
 
@@ -401,6 +463,9 @@ def main():
         _log("bench: configs 2, 4, 5")
         line["other_configs"] = other_configs(dev)
         _log("bench: " + json.dumps(line["other_configs"]))
+        _log("bench: gated output stage")
+        line["next_rows"] = {"gate_c4_shape": gate_stage(dev)}
+        _log("bench: " + json.dumps(line["next_rows"]))
     if not args.no_cpu:
         _log("bench: cpu baseline")
         line["cpu_baseline"] = cpu_baseline(args.cpu_budget)
