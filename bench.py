@@ -373,6 +373,11 @@ def main():
         action="store_true",
         help="only copy a 256 MiB device buffer 3 times (scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)",
     )
+    ap.add_argument(
+        "--gate-only",
+        action="store_true",
+        help="only measure the gated output stage at config 4's MSA shape (3 repetitions) and print its JSON",
+    )
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(
@@ -397,6 +402,11 @@ def main():
     _lib.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.gate_only:
+        for _ in range(3):
+            gate = gate_stage(dev)
+        print(json.dumps(gate))
+        return
     q, k, v, bias, dout = make_inputs(dev)
     torch.cuda.synchronize()
     _log("bench: warmup")
