@@ -263,6 +263,50 @@ def other_configs(device):
     return res
 
 
+def nested_msa(device):
+    """Ragged MSA pair-bias attention (the nested row after the headline path): samples with
+    (S_i, N_i) = (256, 384), (128, 256), (128, 512), H=8, c=32, bf16, group-outer packing
+    (elements (S_i, H, N_i, c)), a per-sequence key mask hiding ~15%, a shared pair bias per sample;
+    fwd+bwd of every operand.  Comparable with config 4's dense MSA rows."""
+
+    import torch
+
+    from oops_amd import pair_bias_attention
+
+    tests_dir = os.path.join(ROOT, "tests")
+    if tests_dir not in sys.path:
+        sys.path.insert(0, tests_dir)
+    from nested_standin import NestedTensor  # DanLing's NestedTensor is not installed here
+
+    g = torch.Generator().manual_seed(6)
+    shapes = ((256, 384), (128, 256), (128, 512))
+    h = 8
+    tmpl = NestedTensor([torch.empty(s_, h, n_, C) for s_, n_ in shapes], ragged_dims=(0, 2))
+    vals = [torch.randn(tmpl.concat.shape, generator=g).to(torch.bfloat16).to(device).requires_grad_(True)
+            for _ in range(3)]  # fmt: skip
+    btmpl = NestedTensor([torch.empty(1, h, n_, n_) for _, n_ in shapes], ragged_dims=(2, 3))
+    bvals = torch.randn(btmpl.concat.shape, generator=g).to(torch.bfloat16).to(device).requires_grad_(True)
+    mtmpl = NestedTensor([torch.empty(s_, 1, n_, dtype=torch.bool) for s_, n_ in shapes], ragged_dims=(0, 2))
+    mvals = torch.rand(mtmpl.concat.shape, generator=g) > 0.15
+    mask = mtmpl.packed_like(mvals.to(device))
+    q, k, v = (tmpl.packed_like(x) for x in vals)
+    bias = btmpl.packed_like(bvals)
+    dvals = torch.randn(tmpl.concat.shape, generator=g).to(torch.bfloat16).to(device)
+    leaves = [*vals, bvals]
+
+    def run():
+        out = pair_bias_attention(q, k, v, mask, bias).concat
+        torch.autograd.grad(out, leaves, dvals)
+
+    ms = _median_ms(run, iters=10, warmup=3)
+    flops = 14 * h * C * sum(s_ * n_**2 for s_, n_ in shapes)
+    return {
+        "workload": "nested pair_bias_attention fwd+bwd, (S_i, N_i) = (256,384),(128,256),(128,512), H=8, c=32, bf16",
+        "ms_fwd_bwd": round(ms, 4),
+        "tflops": round(flops / ms / 1e9, 2),
+    }
+
+
 def gate_stage(device):
     """The gated output stage (the row after attention) at config 4's MSA shape.
 
@@ -474,7 +518,7 @@ def main():
         line["other_configs"] = other_configs(dev)
         _log("bench: " + json.dumps(line["other_configs"]))
         _log("bench: gated output stage")
-        line["next_rows"] = {"gate_c4_shape": gate_stage(dev)}
+        line["next_rows"] = {"gate_c4_shape": gate_stage(dev), "nested_msa": nested_msa(dev)}
         _log("bench: " + json.dumps(line["next_rows"]))
     if not args.no_cpu:
         _log("bench: cpu baseline")

@@ -1,8 +1,9 @@
 """``pair_bias_attention``: head-major attention with an additive pair bias (MSA row attention).
 
-Drop-in for the reference's dense operator
+Drop-in for the reference's operator
 (oops/attention/pair_bias/pair_bias_attention.py:57-244 and the admission
-rules of oops/attention/flash/triton/problem.py:170-274):
+rules of oops/attention/flash/triton/problem.py:170-274); DanLing
+NestedTensor inputs go to ``pair_bias_nested`` (ragged MSA):
 
 * q/k/v ``(*prefix, S, H, Q|K, D)``; rank 3 omits prefix and group, rank 4
   the prefix; query and key lengths may differ.
@@ -29,6 +30,7 @@ from .. import _lib
 from .._errors import unsupported
 from . import _core
 from ._runtime import is_nested, require_no_forward_mode, require_same_device
+from .pair_bias_nested import nested_pair_bias_attention
 
 _OPERATOR = "pair_bias_attention"
 _HALF = (torch.float16, torch.bfloat16)
@@ -61,10 +63,18 @@ def pair_bias_attention(
     q, k, v and the bias (broadcast bias gradients are summed to its shape).
     """
 
-    if is_nested(query) or is_nested(key) or is_nested(value) or is_nested(mask) or is_nested(pair_bias):
-        if not (is_nested(query) and is_nested(key) and is_nested(value)):
+    if is_nested(query):
+        if not (is_nested(key) and is_nested(value)):
             raise ValueError("pair_bias_attention query, key, and value must all use NestedTensor")
-        raise unsupported(_OPERATOR, "serves dense tensors only in this build (nested MSA attention is not built)")
+        if mask is not None and not is_nested(mask):
+            raise ValueError("pair_bias_attention nested query/key/value require a NestedTensor mask")
+        if pair_bias is not None and not is_nested(pair_bias):
+            raise ValueError("pair_bias_attention nested query/key/value require a NestedTensor pair_bias")
+        return nested_pair_bias_attention(query, key, value, mask, pair_bias, scale)
+    if is_nested(key) or is_nested(value):
+        raise ValueError("pair_bias_attention query, key, and value must all use NestedTensor")
+    if is_nested(mask) or is_nested(pair_bias):
+        raise ValueError("pair_bias_attention dense query/key/value cannot use NestedTensor mask or pair_bias")
     require_no_forward_mode(_OPERATOR, query, key, value, pair_bias)
     if mask is not None and mask.dim() == query.dim():
         if mask.shape[-3] != 1:

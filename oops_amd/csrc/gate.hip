@@ -42,6 +42,7 @@ struct GateArgs {
   int64_t rows, tokens, groups;
   int64_t a_sb, a_sg, a_st, a_sh, a_sd;
   int64_t s_row, w_row;
+  int64_t tiles;  // projection: token tiles x channel tiles
   int heads, width, channels;
 };
 
@@ -103,8 +104,12 @@ __global__ __launch_bounds__(256) void gate_projection_kernel(GateArgs a) {
   const int N = a.heads * a.width;
   const int C = a.channels;
   const int nbn = (N + kBN - 1) / kBN;
-  const int bn = (int)(blockIdx.x % nbn);
-  const int64_t bm = blockIdx.x / nbn;
+  // the channel tiles of one token tile are neighbours in one XCD's range, so
+  // the token rows they share are fetched from HBM once and met in that L2
+  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x, 0);
+  if (tile >= a.tiles) return;
+  const int bn = (int)(tile % nbn);
+  const int64_t bm = tile / nbn;
   const int n0 = bn * kBN;
   const int64_t r = bm * kBM + wave * 32 + lq;  // this lane's token
   const bool rv = r < a.rows;
@@ -356,15 +361,17 @@ hipError_t launch_gate_projection(const oops_gate_geometry& g, const void* singl
   const int64_t N = (int64_t)g.heads * g.width;
   const int64_t blocks = ((g.rows + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
   if (blocks == 0) return hipSuccess;
+  a.tiles = blocks;
+  const int64_t grid = xcd_grid(blocks, 0);
   return by_dtype(g.dtype, [&](auto tag) -> hipError_t {
     using T = typename decltype(tag)::type;
     if constexpr (std::is_same<T, float>::value) {
       return hipErrorInvalidValue;
     } else {
       if (logits != nullptr)
-        hipLaunchKernelGGL((gate_projection_kernel<T, true>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((gate_projection_kernel<T, true>), dim3((unsigned)grid), dim3(256), 0, stream, a);
       else
-        hipLaunchKernelGGL((gate_projection_kernel<T, false>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((gate_projection_kernel<T, false>), dim3((unsigned)grid), dim3(256), 0, stream, a);
       return hipGetLastError();
     }
   });

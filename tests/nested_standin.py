@@ -14,7 +14,9 @@ test_triangle_attention.py:65-169):
 * ``.ragged_level_offsets(level)``: cumulative sizes of ragged dim ``level``.
 * ``.transpose(a, b)``: swaps two element dims as a view of the same packed
   storage (ragged dims and packing order are renamed, ``concat`` unchanged).
-* ``.packed_like(values)``: same topology over new packed values.
+* ``.packed_like(values)``: same topology over new packed values;
+  ``.packed_with_static_tail(values)`` the same with other static dims.
+* ``.element_sizes()``: each element's shape.
 * ``torch.unbind(nested)``: the elements as dense tensors (differentiable).
 """
 
@@ -68,6 +70,23 @@ class NestedTensor:
             raise ValueError(f"packed_like: values {tuple(values.shape)} != {tuple(self.concat.shape)}")
         return NestedTensor(
             ragged_dims=self.ragged_dims, packed_dim_order=self.packed_dim_order, _sizes=self._sizes, _concat=values
+        )
+
+    def packed_with_static_tail(self, values):
+        """Same ragged topology over packed values whose static (non-ragged) dims differ."""
+
+        nr = len(self.ragged_dims)
+        static_dims = self.packed_dim_order[nr:]
+        if values.shape[0] != self.concat.shape[0] or values.dim() - 1 != len(static_dims):
+            raise ValueError("packed_with_static_tail: packed axis or static rank differs")
+        sizes = []
+        for s in self._sizes:
+            s = list(s)
+            for d, n in zip(static_dims, values.shape[1:]):
+                s[d] = n
+            sizes.append(tuple(s))
+        return NestedTensor(
+            ragged_dims=self.ragged_dims, packed_dim_order=self.packed_dim_order, _sizes=sizes, _concat=values
         )
 
     def transpose(self, a, b):
