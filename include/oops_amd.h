@@ -190,6 +190,98 @@ int oops_gate_multiply_forward(const oops_gate_geometry* geo, const void* attent
 int oops_gate_multiply_backward(const oops_gate_geometry* geo, const void* attention, const void* logits,
                                 const void* grad, void* grad_attention, void* grad_logits, void* stream);
 
+/* ---- row LayerNorm: y = (x - mean) * rstd * weight + bias over `width` ----
+ *
+ * Replaces the reference's layer_norm forward/backward kernels
+ * (oops/normalization/layer_norm/triton/backend.py, layer_norm_forward_into)
+ * where the triangle multiplicative update normalizes its pair input
+ * (oops/pair/triangle_multiplication/triton/generic.py:102-108).  Statistics
+ * are float32 (biased variance); weight and bias are float32.  y rows are
+ * `y_row` elements apart; the columns width..y_row-1 are written as zero, so a
+ * padded y feeds 16-byte MFMA operand loads. */
+typedef struct oops_row_norm_geometry {
+  int32_t dtype; /* x and y */
+  int32_t width; /* 1..4096 */
+  int64_t rows;
+  int64_t x_row; /* x row stride in elements */
+  int64_t y_row; /* y row stride in elements (>= width) */
+  float eps;
+} oops_row_norm_geometry;
+
+int oops_layer_norm_rows_forward(const oops_row_norm_geometry* geo, const void* x, const float* weight,
+                                 const float* bias, void* y, float* mean, float* rstd, void* stream);
+/* Rows of float32 weight/bias gradient partials the backward writes (sum them). */
+size_t oops_layer_norm_rows_parts(const oops_row_norm_geometry* geo);
+/* grad_x (rows of x_row) from grad_y (rows of y_row); weight/bias gradient
+ * partials [parts][width] (either may be NULL). */
+int oops_layer_norm_rows_backward(const oops_row_norm_geometry* geo, const void* x, const float* weight,
+                                  const float* mean, const float* rstd, const void* grad_y, void* grad_x,
+                                  float* grad_weight_parts, float* grad_bias_parts, void* stream);
+
+/* ---- triangle multiplicative update (oops/pair/triangle_multiplication) ----
+ *
+ * G groups of P pair cells, C pair channels, H hidden channels; R = G * P.
+ * normalized pair xn [R][c_row] (LayerNorm of the pair, zero-padded to c_row,
+ * a multiple of 8); W = [left value; left gate; right value; right gate]
+ * [4H][c_row]; factors [2][G][H][P] (left, right), channel-major as the
+ * contraction reads them; combined [G][H][P]; normalized combined rows
+ * [R][h_row] (h_row a multiple of 8).  Projection biases and LayerNorm affine
+ * parameters are float32, NULL where absent; the mask is float32 [R].
+ *
+ *   oops_trimul_factors_forward  <- _gated_projection_forward
+ *       (triton/kernel.py:109-187, generic.py:351-407)
+ *   oops_trimul_factors_backward <- _gated_projection_backward
+ *       (kernel.py:190-364, generic.py:1022-1092)
+ *   oops_trimul_output_norm_*    <- _channel_major_layer_norm and
+ *       _layer_norm_transpose_backward (kernel.py:367-402, :550-628)
+ *   oops_trimul_output_forward   <- _gated_output_forward (kernel.py:405-467)
+ *   oops_trimul_output_backward  <- _gated_output_backward (kernel.py:470-547)
+ * The contraction itself is a batched GEMM, as in the reference
+ * (generic.py:505-543). */
+typedef struct oops_trimul_geometry {
+  int32_t dtype;    /* OOPS_BF16 / OOPS_F16 */
+  int32_t channels; /* C */
+  int32_t hidden;   /* H */
+  int32_t has_mask;
+  int64_t groups;    /* G */
+  int64_t positions; /* P */
+  int64_t c_row;     /* row stride of xn, W, W_gate and the gate gradients */
+  int64_t h_row;     /* row stride of the normalized combined rows and W_out */
+  float eps;         /* output LayerNorm epsilon */
+} oops_trimul_geometry;
+
+/* factors[f][g][h][p] = mask[r] * (xn W_v^T + b_v) * sigmoid(xn W_g^T + b_g). */
+int oops_trimul_factors_forward(const oops_trimul_geometry* geo, const void* normalized, const void* weight,
+                                const float* bias, const void* mask, void* factors, void* stream);
+/* Rows of float32 mask-gradient partials the factor backward writes (sum them). */
+size_t oops_trimul_mask_parts(const oops_trimul_geometry* geo);
+/* Recomputes the projections and writes grad_projection [4H][R] (value and
+ * gate logit gradients, W's row order) and, with a mask, mask-gradient
+ * partials [parts][R] (NULL to skip). */
+int oops_trimul_factors_backward(const oops_trimul_geometry* geo, const void* normalized, const void* weight,
+                                 const float* bias, const void* mask, const void* grad_factors,
+                                 void* grad_projection, float* grad_mask_parts, void* stream);
+/* LayerNorm over H of combined[g][:][p] -> normalized rows [R][h_row]; mean, rstd [R]. */
+int oops_trimul_output_norm_forward(const oops_trimul_geometry* geo, const void* combined, const float* weight,
+                                    const float* bias, void* normalized, float* mean, float* rstd, void* stream);
+size_t oops_trimul_output_norm_parts(const oops_trimul_geometry* geo);
+/* grad_normalized rows [R][H] -> grad_combined [G][H][P]; affine partials [parts][H]. */
+int oops_trimul_output_norm_backward(const oops_trimul_geometry* geo, const void* combined, const float* weight,
+                                     const float* mean, const float* rstd, const void* grad_normalized,
+                                     void* grad_combined, float* grad_weight_parts, float* grad_bias_parts,
+                                     void* stream);
+/* out [R][C] = (normalized W_out^T + b_out) * sigmoid(xn W_gate^T + b_gate);
+ * W_out [C][h_row], W_gate [C][c_row]. */
+int oops_trimul_output_forward(const oops_trimul_geometry* geo, const void* normalized, const void* pair_normalized,
+                               const void* output_weight, const void* gate_weight, const float* output_bias,
+                               const float* gate_bias, void* out, void* stream);
+/* Recomputes both projections; grad_value = grad_out * sigmoid(gate) and
+ * grad_gate = grad_out * value * sigmoid'(gate), rows [R][c_row] (padding zero). */
+int oops_trimul_output_backward(const oops_trimul_geometry* geo, const void* normalized,
+                                const void* pair_normalized, const void* output_weight, const void* gate_weight,
+                                const float* output_bias, const float* gate_bias, const void* grad_out,
+                                void* grad_value, void* grad_gate, void* stream);
+
 /* Thread-local description of the last failure (empty string if none). */
 const char* oops_last_error(void);
 

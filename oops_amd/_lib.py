@@ -18,7 +18,7 @@ F32, BF16, F16 = 0, 1, 2
 BIAS_NONE, BIAS_FULL, BIAS_SHARED = 0, 1, 2
 PHASE_DELTA, PHASE_DQ, PHASE_DKV, PHASE_DBIAS = 1, 2, 4, 8
 TABLE_WIDTH = 40
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # geometry table columns (enum oops_table_column)
 (
@@ -43,6 +43,17 @@ EXPORTED_SYMBOLS = (
     "oops_gate_projection_forward",
     "oops_gate_multiply_forward",
     "oops_gate_multiply_backward",
+    "oops_layer_norm_rows_forward",
+    "oops_layer_norm_rows_parts",
+    "oops_layer_norm_rows_backward",
+    "oops_trimul_factors_forward",
+    "oops_trimul_mask_parts",
+    "oops_trimul_factors_backward",
+    "oops_trimul_output_norm_forward",
+    "oops_trimul_output_norm_parts",
+    "oops_trimul_output_norm_backward",
+    "oops_trimul_output_forward",
+    "oops_trimul_output_backward",
     "oops_last_error",
     "oops_abi_version",
 )
@@ -85,6 +96,31 @@ class GateGeometry(ctypes.Structure):
     ]
 
 
+class RowNormGeometry(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("width", ctypes.c_int32),
+        ("rows", ctypes.c_int64),
+        ("x_row", ctypes.c_int64),
+        ("y_row", ctypes.c_int64),
+        ("eps", ctypes.c_float),
+    ]
+
+
+class TrimulGeometry(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("channels", ctypes.c_int32),
+        ("hidden", ctypes.c_int32),
+        ("has_mask", ctypes.c_int32),
+        ("groups", ctypes.c_int64),
+        ("positions", ctypes.c_int64),
+        ("c_row", ctypes.c_int64),
+        ("h_row", ctypes.c_int64),
+        ("eps", ctypes.c_float),
+    ]
+
+
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
 
@@ -124,6 +160,30 @@ def load() -> ctypes.CDLL:
         lib.oops_gate_multiply_forward.restype = i32
         lib.oops_gate_multiply_backward.argtypes = [gg, vp, vp, vp, vp, vp, vp]
         lib.oops_gate_multiply_backward.restype = i32
+        rg = ctypes.POINTER(RowNormGeometry)
+        lib.oops_layer_norm_rows_forward.argtypes = [rg, vp, vp, vp, vp, vp, vp, vp]
+        lib.oops_layer_norm_rows_forward.restype = i32
+        lib.oops_layer_norm_rows_parts.argtypes = [rg]
+        lib.oops_layer_norm_rows_parts.restype = sz
+        lib.oops_layer_norm_rows_backward.argtypes = [rg, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        lib.oops_layer_norm_rows_backward.restype = i32
+        tg = ctypes.POINTER(TrimulGeometry)
+        lib.oops_trimul_factors_forward.argtypes = [tg, vp, vp, vp, vp, vp, vp]
+        lib.oops_trimul_factors_forward.restype = i32
+        lib.oops_trimul_mask_parts.argtypes = [tg]
+        lib.oops_trimul_mask_parts.restype = sz
+        lib.oops_trimul_factors_backward.argtypes = [tg, vp, vp, vp, vp, vp, vp, vp, vp]
+        lib.oops_trimul_factors_backward.restype = i32
+        lib.oops_trimul_output_norm_forward.argtypes = [tg, vp, vp, vp, vp, vp, vp, vp]
+        lib.oops_trimul_output_norm_forward.restype = i32
+        lib.oops_trimul_output_norm_parts.argtypes = [tg]
+        lib.oops_trimul_output_norm_parts.restype = sz
+        lib.oops_trimul_output_norm_backward.argtypes = [tg, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        lib.oops_trimul_output_norm_backward.restype = i32
+        lib.oops_trimul_output_forward.argtypes = [tg, vp, vp, vp, vp, vp, vp, vp, vp]
+        lib.oops_trimul_output_forward.restype = i32
+        lib.oops_trimul_output_backward.argtypes = [tg, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        lib.oops_trimul_output_backward.restype = i32
         lib.oops_last_error.argtypes = []
         lib.oops_last_error.restype = ctypes.c_char_p
         lib.oops_abi_version.argtypes = []

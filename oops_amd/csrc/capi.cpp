@@ -10,6 +10,7 @@
 
 #include "attn_kernels.h"
 #include "gate_kernels.h"
+#include "trimul_kernels.h"
 
 namespace {
 
@@ -232,6 +233,34 @@ int check_gate(const oops_gate_geometry* g) {
   return OOPS_OK;
 }
 
+int check_row_norm(const oops_row_norm_geometry* g) {
+  if (g == nullptr) return fail(OOPS_EINVAL, "row-norm geometry is NULL");
+  if (g->dtype != OOPS_BF16 && g->dtype != OOPS_F16)
+    return fail(OOPS_EINVAL, "row LayerNorm serves bfloat16 and float16 (dtype %lld)", g->dtype);
+  if (g->width <= 0 || g->width > 4096) return fail(OOPS_EINVAL, "width must be in 1..4096, got %lld", g->width);
+  if (g->rows < 0) return fail(OOPS_EINVAL, "rows must be >= 0");
+  if (g->x_row < g->width || g->y_row < g->width)
+    return fail(OOPS_EINVAL, "row strides (%lld, %lld) must cover the width", g->x_row, g->y_row);
+  if (g->y_row > 4096) return fail(OOPS_EINVAL, "y row stride too large (%lld)", g->y_row);
+  return OOPS_OK;
+}
+
+int check_trimul(const oops_trimul_geometry* g) {
+  if (g == nullptr) return fail(OOPS_EINVAL, "triangle multiplication geometry is NULL");
+  if (g->dtype != OOPS_BF16 && g->dtype != OOPS_F16)
+    return fail(OOPS_EINVAL, "the triangle multiplication kernels serve bfloat16 and float16 (dtype %lld)", g->dtype);
+  if (g->channels <= 0 || g->channels > 1024 || g->hidden <= 0 || g->hidden > 1024)
+    return fail(OOPS_EINVAL, "channels and hidden must be in 1..1024, got %lld and %lld", g->channels, g->hidden);
+  if (g->groups < 0 || g->positions < 0) return fail(OOPS_EINVAL, "groups and positions must be >= 0");
+  if (g->c_row < g->channels || g->c_row % 8 || g->h_row < g->hidden || g->h_row % 8)
+    return fail(OOPS_EINVAL, "c_row and h_row must be multiples of 8 covering C and H (%lld, %lld)", g->c_row,
+                g->h_row);
+  if (g->groups * g->positions > (int64_t(1) << 40)) return fail(OOPS_EINVAL, "too many pair cells");
+  return OOPS_OK;
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
 int gate_launch_result(hipError_t err, const char* what) {
   if (err == hipSuccess) return OOPS_OK;
   g_last_error = std::string(what) + " launch failed: " + hipGetErrorString(err);
@@ -242,7 +271,7 @@ int gate_launch_result(hipError_t err, const char* what) {
 
 extern "C" {
 
-int oops_abi_version(void) { return 3; }
+int oops_abi_version(void) { return 4; }
 
 const char* oops_last_error(void) { return g_last_error.c_str(); }
 
@@ -338,6 +367,133 @@ int oops_gate_multiply_backward(const oops_gate_geometry* geo, const void* atten
   return gate_launch_result(oops::launch_gate_multiply_backward(*geo, attention, logits, grad, grad_attention,
                                                                 grad_logits, static_cast<hipStream_t>(stream)),
                             "gate multiply backward");
+}
+
+int oops_layer_norm_rows_forward(const oops_row_norm_geometry* geo, const void* x, const float* weight,
+                                 const float* bias, void* y, float* mean, float* rstd, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_row_norm(geo)) return rc;
+  if (!x || !y || !mean || !rstd) return fail(OOPS_EINVAL, "x, y, mean and rstd must be non-NULL");
+  return gate_launch_result(oops::launch_layer_norm_rows_forward(*geo, x, weight, bias, y, mean, rstd,
+                                                                 static_cast<hipStream_t>(stream)),
+                            "row LayerNorm forward");
+}
+
+size_t oops_layer_norm_rows_parts(const oops_row_norm_geometry* geo) {
+  if (check_row_norm(geo)) return 0;
+  return (size_t)oops::layer_norm_rows_parts(*geo);
+}
+
+int oops_layer_norm_rows_backward(const oops_row_norm_geometry* geo, const void* x, const float* weight,
+                                  const float* mean, const float* rstd, const void* grad_y, void* grad_x,
+                                  float* grad_weight_parts, float* grad_bias_parts, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_row_norm(geo)) return rc;
+  if (!x || !mean || !rstd || !grad_y || !grad_x)
+    return fail(OOPS_EINVAL, "x, mean, rstd, grad_y and grad_x must be non-NULL");
+  return gate_launch_result(oops::launch_layer_norm_rows_backward(*geo, x, weight, mean, rstd, grad_y, grad_x,
+                                                                  grad_weight_parts, grad_bias_parts,
+                                                                  static_cast<hipStream_t>(stream)),
+                            "row LayerNorm backward");
+}
+
+int oops_trimul_factors_forward(const oops_trimul_geometry* geo, const void* normalized, const void* weight,
+                                const float* bias, const void* mask, void* factors, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_trimul(geo)) return rc;
+  if (!normalized || !weight || !factors) return fail(OOPS_EINVAL, "normalized, weight and factors must be non-NULL");
+  if (geo->has_mask && !mask) return fail(OOPS_EINVAL, "has_mask is set but mask is NULL");
+  if (!aligned16(normalized) || !aligned16(weight) || !aligned16(factors) || (geo->has_mask && !aligned16(mask)))
+    return fail(OOPS_EINVAL, "normalized, weight, mask and factors must be 16-byte aligned");
+  return gate_launch_result(oops::launch_trimul_factors(*geo, normalized, weight, bias, mask, factors, nullptr,
+                                                        nullptr, nullptr, static_cast<hipStream_t>(stream)),
+                            "triangle multiplication factors");
+}
+
+size_t oops_trimul_mask_parts(const oops_trimul_geometry* geo) {
+  if (check_trimul(geo)) return 0;
+  return (size_t)oops::trimul_mask_parts(*geo);
+}
+
+int oops_trimul_factors_backward(const oops_trimul_geometry* geo, const void* normalized, const void* weight,
+                                 const float* bias, const void* mask, const void* grad_factors,
+                                 void* grad_projection, float* grad_mask_parts, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_trimul(geo)) return rc;
+  if (!normalized || !weight || !grad_factors || !grad_projection)
+    return fail(OOPS_EINVAL, "normalized, weight, grad_factors and grad_projection must be non-NULL");
+  if (geo->has_mask && !mask) return fail(OOPS_EINVAL, "has_mask is set but mask is NULL");
+  if (!aligned16(normalized) || !aligned16(weight) || !aligned16(grad_factors) || !aligned16(grad_projection) ||
+      (geo->has_mask && !aligned16(mask)))
+    return fail(OOPS_EINVAL, "operands must be 16-byte aligned");
+  return gate_launch_result(oops::launch_trimul_factors(*geo, normalized, weight, bias, mask, nullptr, grad_factors,
+                                                        grad_projection, grad_mask_parts,
+                                                        static_cast<hipStream_t>(stream)),
+                            "triangle multiplication factor backward");
+}
+
+int oops_trimul_output_norm_forward(const oops_trimul_geometry* geo, const void* combined, const float* weight,
+                                    const float* bias, void* normalized, float* mean, float* rstd, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_trimul(geo)) return rc;
+  if (!combined || !normalized || !mean || !rstd)
+    return fail(OOPS_EINVAL, "combined, normalized, mean and rstd must be non-NULL");
+  return gate_launch_result(oops::launch_trimul_output_norm_forward(*geo, combined, weight, bias, normalized, mean,
+                                                                    rstd, static_cast<hipStream_t>(stream)),
+                            "triangle multiplication output norm");
+}
+
+size_t oops_trimul_output_norm_parts(const oops_trimul_geometry* geo) {
+  if (check_trimul(geo)) return 0;
+  return (size_t)oops::trimul_output_norm_parts(*geo);
+}
+
+int oops_trimul_output_norm_backward(const oops_trimul_geometry* geo, const void* combined, const float* weight,
+                                     const float* mean, const float* rstd, const void* grad_normalized,
+                                     void* grad_combined, float* grad_weight_parts, float* grad_bias_parts,
+                                     void* stream) {
+  g_last_error.clear();
+  if (int rc = check_trimul(geo)) return rc;
+  if (!combined || !mean || !rstd || !grad_normalized || !grad_combined)
+    return fail(OOPS_EINVAL, "combined, mean, rstd, grad_normalized and grad_combined must be non-NULL");
+  return gate_launch_result(oops::launch_trimul_output_norm_backward(*geo, combined, weight, mean, rstd,
+                                                                     grad_normalized, grad_combined,
+                                                                     grad_weight_parts, grad_bias_parts,
+                                                                     static_cast<hipStream_t>(stream)),
+                            "triangle multiplication output norm backward");
+}
+
+int oops_trimul_output_forward(const oops_trimul_geometry* geo, const void* normalized, const void* pair_normalized,
+                               const void* output_weight, const void* gate_weight, const float* output_bias,
+                               const float* gate_bias, void* out, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_trimul(geo)) return rc;
+  if (!normalized || !pair_normalized || !output_weight || !gate_weight || !out)
+    return fail(OOPS_EINVAL, "normalized, pair_normalized, both weights and out must be non-NULL");
+  if (!aligned16(normalized) || !aligned16(pair_normalized) || !aligned16(output_weight) || !aligned16(gate_weight) ||
+      !aligned16(out))
+    return fail(OOPS_EINVAL, "operands must be 16-byte aligned");
+  return gate_launch_result(oops::launch_trimul_output(*geo, normalized, pair_normalized, output_weight, gate_weight,
+                                                       output_bias, gate_bias, out, nullptr, nullptr, nullptr,
+                                                       static_cast<hipStream_t>(stream)),
+                            "triangle multiplication output");
+}
+
+int oops_trimul_output_backward(const oops_trimul_geometry* geo, const void* normalized,
+                                const void* pair_normalized, const void* output_weight, const void* gate_weight,
+                                const float* output_bias, const float* gate_bias, const void* grad_out,
+                                void* grad_value, void* grad_gate, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_trimul(geo)) return rc;
+  if (!normalized || !pair_normalized || !output_weight || !gate_weight || !grad_out || !grad_value || !grad_gate)
+    return fail(OOPS_EINVAL, "operands and both gradients must be non-NULL");
+  if (!aligned16(normalized) || !aligned16(pair_normalized) || !aligned16(output_weight) || !aligned16(gate_weight) ||
+      !aligned16(grad_out) || !aligned16(grad_value) || !aligned16(grad_gate))
+    return fail(OOPS_EINVAL, "operands must be 16-byte aligned");
+  return gate_launch_result(oops::launch_trimul_output(*geo, normalized, pair_normalized, output_weight, gate_weight,
+                                                       output_bias, gate_bias, nullptr, grad_out, grad_value,
+                                                       grad_gate, static_cast<hipStream_t>(stream)),
+                            "triangle multiplication output backward");
 }
 
 }  // extern "C"

@@ -1,0 +1,989 @@
+// Triangle multiplicative update (gfx950) and the row LayerNorm it starts with.
+//
+// The update (oops/pair/triangle_multiplication/triton/generic.py:111-200):
+//
+//   xn       = LayerNorm_C(pair)                              row_norm_*_kernel
+//   left/right[h][p] = mask[p] * (xn W_v^T + b_v) * sigmoid(xn W_g^T + b_g)
+//                                                             trimul_factor_kernel
+//   combined = left . right^T (outgoing) or left^T . right   batched GEMM (host)
+//   nrm      = LayerNorm_H(combined) over the channel axis    trimul_out_norm_*_kernel
+//   out      = (nrm W_o^T + b_o) * sigmoid(xn W_og^T + b_og)  trimul_output_kernel
+//
+// row_norm: one row per 64/LPR lanes (LPR lanes per row, 8 elements per lane
+// and chunk, 16-byte accesses where the row layout allows); float32 statistics;
+// the backward writes per-wave float32 partials of the affine gradients.
+//
+// trimul_factor_kernel: one workgroup = 4 waves x 32 tokens and 64 hidden
+// channels of one factor, value and gate together (128 rows of W through a
+// two-buffer XOR-swizzled LDS tile).  The token is the MFMA row, so a lane's
+// accumulator holds 4 consecutive tokens of one channel: the channel-major
+// factor layout the contraction reads is written 8 bytes per lane.  The
+// backward recomputes both projections (K = C is short; re-reading saved
+// projections would cost more HBM traffic than the MFMA work) and writes the
+// value and gate-logit gradients channel-major, [4H][R], plus per-workgroup
+// mask-gradient partials.
+//
+// trimul_out_norm: 64 (or fewer, for wide H) positions of one group per
+// workgroup; the [H][positions] tile is staged through LDS so both the
+// channel-major combined tensor and the token-major normalized rows are read
+// and written with consecutive addresses.
+//
+// trimul_output_kernel: 4 waves x 32 tokens and 64 output channels; two
+// K loops (K = H over the normalized combined rows with W_o, K = C over xn
+// with W_og) into separate accumulators, the product in the epilogue, and a
+// v_permlane32_swap so each lane stores 16 consecutive channels of its token.
+// The backward recomputes both projections and writes the two gradients.
+#include <type_traits>
+
+#include "attn_fast_common.h"
+#include "trimul_kernels.h"
+
+namespace oops {
+
+using namespace fast;
+
+namespace {
+
+template <typename T>
+__device__ __forceinline__ float to_f(T x) {
+  return (float)x;
+}
+__device__ __forceinline__ float sigmoid_f(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e));
+}
+template <typename T>
+__device__ __forceinline__ float lo_f(uint32_t u) {
+  return to_f(__builtin_bit_cast(T, (uint16_t)(u & 0xffffu)));
+}
+template <typename T>
+__device__ __forceinline__ float hi_f(uint32_t u) {
+  return to_f(__builtin_bit_cast(T, (uint16_t)(u >> 16)));
+}
+template <typename T>
+__device__ __forceinline__ void unpack8(const uint4& u, float (&x)[8]) {
+  x[0] = lo_f<T>(u.x), x[1] = hi_f<T>(u.x), x[2] = lo_f<T>(u.y), x[3] = hi_f<T>(u.y);
+  x[4] = lo_f<T>(u.z), x[5] = hi_f<T>(u.z), x[6] = lo_f<T>(u.w), x[7] = hi_f<T>(u.w);
+}
+template <typename T>
+__device__ __forceinline__ uint4 pack8(const float (&x)[8]) {
+  return make_uint4(pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3]), pack2<T>(x[4], x[5]), pack2<T>(x[6], x[7]));
+}
+
+// ------------------------------------------------------------------ row LayerNorm
+struct RowNormArgs {
+  const void* x;
+  const float* w;
+  const float* b;
+  void* y;
+  float* mean;
+  float* rstd;
+  const void* dy;
+  void* dx;
+  float* dw;
+  float* db;
+  int64_t rows, x_row, y_row;
+  int width, lpr;
+  float eps;
+};
+
+template <typename T, int CH, bool VEC>
+__device__ __forceinline__ void load_chunks(const T* row, bool valid, int width, int lpr, int sub, float (&x)[CH][8]) {
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int col = (c * lpr + sub) * 8;
+    if (VEC && valid && col < width) {
+      unpack8<T>(*reinterpret_cast<const uint4*>(row + col), x[c]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[c][e] = valid && col + e < width ? to_f(row[col + e]) : 0.f;
+    }
+  }
+}
+
+__device__ __forceinline__ float group_sum(float s, int lpr) {
+  for (int o = lpr >> 1; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  return s;
+}
+
+template <typename T, int CH, bool VEC>
+__global__ __launch_bounds__(256) void row_norm_forward_kernel(RowNormArgs a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lpr = a.lpr, rpw = 64 / lpr;
+  const int sub = lane & (lpr - 1), rw = lane / lpr;
+  const int64_t row = ((int64_t)blockIdx.x * 4 + wave) * rpw + rw;
+  const bool rv = row < a.rows;
+  const int W = a.width;
+  const T* xr = static_cast<const T*>(a.x) + (rv ? row : 0) * a.x_row;
+  float x[CH][8];
+  load_chunks<T, CH, VEC>(xr, rv, W, lpr, sub, x);
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += x[c][e];
+  const float mean = group_sum(s, lpr) / (float)W;
+  float q = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int col = (c * lpr + sub) * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float d = col + e < W ? x[c][e] - mean : 0.f;
+      q += d * d;
+    }
+  }
+  const float rstd = rsqrtf(group_sum(q, lpr) / (float)W + a.eps);
+  if (!rv) return;
+  T* yr = static_cast<T*>(a.y) + row * a.y_row;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int col = (c * lpr + sub) * 8;
+    if (col >= a.y_row) continue;
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      o[e] = col + e < W ? (x[c][e] - mean) * rstd * (a.w ? a.w[col + e] : 1.f) + (a.b ? a.b[col + e] : 0.f) : 0.f;
+    if (VEC) {
+      *reinterpret_cast<uint4*>(yr + col) = pack8<T>(o);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (col + e < a.y_row) yr[col + e] = (T)o[e];
+    }
+  }
+  if (sub == 0) {
+    a.mean[row] = mean;
+    a.rstd[row] = rstd;
+  }
+}
+
+template <typename T, int CH, bool VEC>
+__global__ __launch_bounds__(256) void row_norm_backward_kernel(RowNormArgs a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lpr = a.lpr, rpw = 64 / lpr;
+  const int sub = lane & (lpr - 1), rw = lane / lpr;
+  const int W = a.width;
+  const float inv_w = 1.0f / (float)W;
+  float dw[CH][8], db[CH][8];
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dw[c][e] = db[c][e] = 0.f;
+  const int64_t step = (int64_t)gridDim.x * 4 * rpw;
+  for (int64_t base = ((int64_t)blockIdx.x * 4 + wave) * rpw; base < a.rows; base += step) {
+    const int64_t row = base + rw;
+    const bool rv = row < a.rows;
+    const int64_t rr = rv ? row : 0;
+    float x[CH][8], g[CH][8];
+    load_chunks<T, CH, VEC>(static_cast<const T*>(a.x) + rr * a.x_row, rv, W, lpr, sub, x);
+    load_chunks<T, CH, VEC>(static_cast<const T*>(a.dy) + rr * a.y_row, rv, W, lpr, sub, g);
+    const float mean = rv ? a.mean[rr] : 0.f, rstd = rv ? a.rstd[rr] : 0.f;
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int col = (c * lpr + sub) * 8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const bool in = col + e < W;
+        const float xh = in ? (x[c][e] - mean) * rstd : 0.f;
+        const float wdy = in ? g[c][e] * (a.w ? a.w[col + e] : 1.f) : 0.f;
+        x[c][e] = xh;
+        s1 += wdy;
+        s2 += wdy * xh;
+        dw[c][e] += g[c][e] * xh;
+        db[c][e] += g[c][e];
+      }
+    }
+    s1 = group_sum(s1, lpr) * inv_w;
+    s2 = group_sum(s2, lpr) * inv_w;
+    if (!rv) continue;
+    T* dxr = static_cast<T*>(a.dx) + row * a.x_row;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int col = (c * lpr + sub) * 8;
+      if (col >= W) continue;
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        o[e] = rstd * (g[c][e] * (a.w && col + e < W ? a.w[col + e] : 1.f) - s1 - x[c][e] * s2);
+      if (VEC) {
+        *reinterpret_cast<uint4*>(dxr + col) = pack8<T>(o);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (col + e < W) dxr[col + e] = (T)o[e];
+      }
+    }
+  }
+  // sum the rows this wave held, then one partial row per wave
+  for (int o = lpr; o < 64; o <<= 1) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        dw[c][e] += __shfl_xor(dw[c][e], o);
+        db[c][e] += __shfl_xor(db[c][e], o);
+      }
+  }
+  if (rw != 0) return;
+  const int64_t part = (int64_t)blockIdx.x * 4 + wave;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int col = (c * lpr + sub) * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (col + e >= W) continue;
+      if (a.dw) a.dw[part * W + col + e] = dw[c][e];
+      if (a.db) a.db[part * W + col + e] = db[c][e];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ factors
+struct FactorArgs {
+  const void* xn;
+  const void* w;
+  const float* bias;
+  const float* mask;
+  void* factors;
+  const void* grad_factors;
+  void* grad_proj;
+  float* mask_parts;
+  int64_t rows, positions, groups, c_row, tiles;
+  int H, cblocks;
+};
+
+constexpr int kFM = 128;  // tokens per workgroup (32 per wave)
+constexpr int kFK = 64;   // k per step
+
+template <typename T>
+__device__ __forceinline__ void load4(const T* p, bool vec, int64_t left, float (&x)[4]) {
+  if (vec) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    x[0] = lo_f<T>(u.x), x[1] = hi_f<T>(u.x), x[2] = lo_f<T>(u.y), x[3] = hi_f<T>(u.y);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = i < left ? to_f(p[i]) : 0.f;
+  }
+}
+
+template <typename T, bool BWD>
+__global__ __launch_bounds__(256) void trimul_factor_kernel(FactorArgs a) {
+  using E = Elem<T>;
+  using Frag = typename E::Frag;
+  constexpr int WT = 128 * kFK;
+  __shared__ __attribute__((aligned(16))) T w_lds[2 * WT];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, lq = lane & 31, g2 = lane >> 5;
+  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x, 0);
+  if (tile >= a.tiles) return;
+  const int nb = 2 * a.cblocks;
+  const int fc = (int)(tile % nb);
+  const int f = fc / a.cblocks, cb = fc - f * a.cblocks;
+  const int64_t r0 = (tile / nb) * kFM;
+  const int H = a.H;
+  const int K = (int)a.c_row;
+
+  // this lane's token rows as the MFMA A operand (8 k per lane and chunk)
+  const int64_t rows_left = a.rows - r0;
+  const int nrows = (int)(rows_left < kFM ? rows_left : kFM);
+  const __amdgpu_buffer_rsrc_t xr =
+      make_rsrc(static_cast<const T*>(a.xn) + r0 * a.c_row, (uint32_t)((int64_t)nrows * a.c_row * 2));
+  const bool rv = wave * 32 + lq < nrows;
+  const uint32_t x_lane = (uint32_t)((wave * 32 + lq) * a.c_row * 2);
+  auto load_x = [&](int k0, uint4 (&xf)[4]) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int k = k0 + 16 * c + 8 * g2;
+      xf[c] = buffer_load16(xr, rv && k < K ? x_lane + (uint32_t)(k * 2) : kOut);
+    }
+  };
+  // W rows: 0..63 value channels, 64..127 gate channels of block cb, factor f
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, (uint32_t)((int64_t)4 * H * a.c_row * 2));
+  uint32_t w_off[4];
+  bool w_ok[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int id = tid + 256 * j;
+    const int row = id >> 3, ch = id & 7;
+    const int hv = cb * 64 + (row & 63);
+    const int wrow = f * 2 * H + (row >= 64 ? H : 0) + hv;
+    w_ok[j] = hv < H;
+    w_off[j] = (uint32_t)((int64_t)wrow * a.c_row * 2 + ch * 16);
+  }
+  auto load_w = [&](int k0, uint4 (&wu)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ch = (tid + 256 * j) & 7;
+      wu[j] = buffer_load16(wr, w_ok[j] && k0 + ch * 8 < K ? w_off[j] + (uint32_t)(k0 * 2) : kOut);
+    }
+  };
+  auto store_w = [&](int buf, const uint4 (&wu)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int id = tid + 256 * j;
+      *reinterpret_cast<uint4*>(&w_lds[buf * WT + swz_off<kFK>(id >> 3, (id & 7) * 8)]) = wu[j];
+    }
+  };
+
+  f32x16 acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = f32x16{};
+  const int nsteps = (K + kFK - 1) / kFK;
+  uint4 xf[4], xn[4], wu[4];
+  load_w(0, wu);
+  load_x(0, xf);
+  store_w(0, wu);
+  __syncthreads();
+  for (int i = 0; i < nsteps; ++i) {
+    const int buf = i & 1;
+    const bool more = i + 1 < nsteps;
+    if (more) {
+      load_w((i + 1) * kFK, wu);
+      load_x((i + 1) * kFK, xn);
+    }
+    const T* wt = &w_lds[buf * WT];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const Frag afr = __builtin_bit_cast(Frag, xf[c]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        acc[t] = E::mma(afr, lds_frag<T>(wt + swz_off<kFK>(32 * t + lq, 16 * c + 8 * g2)), acc[t]);
+    }
+    if (more) store_w(buf ^ 1, wu);
+    lds_barrier();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) xf[c] = xn[c];
+  }
+
+  // ---- epilogue: tile t in {0, 1} holds value channel cb*64 + 32t + lq (tile t+2 its gate)
+  // for tokens r0 + 32 wave + 8q + 4 g2 + i
+  const int64_t P = a.positions, R = a.rows;
+  const bool vec4 = (P & 3) == 0;  // 4 tokens from a multiple of 4 share a group, 8-byte aligned
+  const float* mask = a.mask;
+  float mp[16];
+#pragma unroll
+  for (int v = 0; v < 16; ++v) mp[v] = 0.f;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int hv = cb * 64 + 32 * t + lq;
+    if (hv >= H) continue;
+    const float bv = a.bias ? a.bias[f * 2 * H + hv] : 0.f;
+    const float bg = a.bias ? a.bias[f * 2 * H + H + hv] : 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t r4 = r0 + wave * 32 + 8 * q + 4 * g2;
+      if (r4 >= R) continue;
+      const int64_t left = R - r4;
+      float keep[4] = {1.f, 1.f, 1.f, 1.f};
+      if (mask) {
+        if (vec4) {
+          const float4 m4 = *reinterpret_cast<const float4*>(mask + r4);
+          keep[0] = m4.x, keep[1] = m4.y, keep[2] = m4.z, keep[3] = m4.w;
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) keep[i] = i < left ? mask[r4 + i] : 0.f;
+        }
+      }
+      float v[4], s[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[i] = acc[t][4 * q + i] + bv;
+        s[i] = sigmoid_f(acc[t + 2][4 * q + i] + bg);
+      }
+      if constexpr (!BWD) {
+        T* out = static_cast<T*>(a.factors);
+        if (vec4) {
+          const int64_t g = r4 / P, p = r4 - g * P;
+          const int64_t off = ((f * a.groups + g) * H + hv) * P + p;
+          *reinterpret_cast<uint2*>(out + off) =
+              make_uint2(pack2<T>(v[0] * s[0] * keep[0], v[1] * s[1] * keep[1]),
+                         pack2<T>(v[2] * s[2] * keep[2], v[3] * s[3] * keep[3]));
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (i >= left) break;
+            const int64_t g = (r4 + i) / P, p = r4 + i - g * P;
+            out[((f * a.groups + g) * H + hv) * P + p] = (T)(v[i] * s[i] * keep[i]);
+          }
+        }
+      } else {
+        const T* gf = static_cast<const T*>(a.grad_factors);
+        float d[4];
+        if (vec4) {
+          const int64_t g = r4 / P, p = r4 - g * P;
+          load4<T>(gf + ((f * a.groups + g) * H + hv) * P + p, true, left, d);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            d[i] = 0.f;
+            if (i < left) {
+              const int64_t g = (r4 + i) / P, p = r4 + i - g * P;
+              d[i] = to_f(gf[((f * a.groups + g) * H + hv) * P + p]);
+            }
+          }
+        }
+        float dv[4], dg[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          dv[i] = d[i] * keep[i] * s[i];
+          dg[i] = d[i] * keep[i] * v[i] * s[i] * (1.f - s[i]);
+          mp[4 * q + i] += d[i] * v[i] * s[i];
+        }
+        T* gp = static_cast<T*>(a.grad_proj);
+        T* gv = gp + (int64_t)(f * 2 * H + hv) * R + r4;
+        T* gg = gp + (int64_t)(f * 2 * H + H + hv) * R + r4;
+        if (vec4) {
+          *reinterpret_cast<uint2*>(gv) = make_uint2(pack2<T>(dv[0], dv[1]), pack2<T>(dv[2], dv[3]));
+          *reinterpret_cast<uint2*>(gg) = make_uint2(pack2<T>(dg[0], dg[1]), pack2<T>(dg[2], dg[3]));
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (i < left) {
+              gv[i] = (T)dv[i];
+              gg[i] = (T)dg[i];
+            }
+        }
+      }
+    }
+  }
+  if constexpr (BWD) {
+    if (a.mask_parts == nullptr) return;
+    // sum over the 32 channels of the half-wave (lanes of one g2 share tokens)
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+      for (int o = 1; o < 32; o <<= 1) mp[v] += __shfl_xor(mp[v], o);
+    if (lq >= 16) return;
+    float val = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+      if (v == lq) val = mp[v];
+    const int64_t r = r0 + wave * 32 + 8 * (lq >> 2) + 4 * g2 + (lq & 3);
+    if (r < R) a.mask_parts[(int64_t)(f * a.cblocks + cb) * R + r] = val;
+  }
+}
+
+// ------------------------------------------------------------------ output LayerNorm (channel-major)
+struct OutNormArgs {
+  const void* comb;
+  const float* w;
+  const float* b;
+  void* nrm;
+  float* mean;
+  float* rstd;
+  const void* dn;
+  void* dcomb;
+  float* dw;
+  float* db;
+  int64_t groups, positions, h_row, pblocks;
+  int H, npb;
+  float eps;
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void trimul_out_norm_forward_kernel(OutNormArgs a) {
+  extern __shared__ float sm[];  // [H][npb + 1]
+  __shared__ float red[256];
+  const int npb = a.npb, ld = npb + 1, parts = 256 / npb, H = a.H;
+  const int64_t g = blockIdx.x / a.pblocks, p0 = (blockIdx.x % a.pblocks) * npb;
+  const int tid = threadIdx.x, pp = tid % npb, part = tid / npb;
+  const int64_t P = a.positions;
+  const int np = (int)(P - p0 < npb ? P - p0 : npb);
+  const bool pv = pp < np;
+  const T* cg = static_cast<const T*>(a.comb) + g * H * P + p0;
+  float s = 0.f;
+  for (int h = part; h < H; h += parts) {
+    const float v = pv ? to_f(cg[(int64_t)h * P + pp]) : 0.f;
+    sm[h * ld + pp] = v;
+    s += v;
+  }
+  red[tid] = s;
+  __syncthreads();
+  float mean = 0.f;
+  for (int j = 0; j < parts; ++j) mean += red[j * npb + pp];
+  mean /= (float)H;
+  __syncthreads();
+  float q = 0.f;
+  for (int h = part; h < H; h += parts) {
+    const float d = sm[h * ld + pp] - mean;
+    q += d * d;
+  }
+  red[tid] = q;
+  __syncthreads();
+  float var = 0.f;
+  for (int j = 0; j < parts; ++j) var += red[j * npb + pp];
+  const float rstd = rsqrtf(var / (float)H + a.eps);
+  for (int h = part; h < H; h += parts)
+    sm[h * ld + pp] = (sm[h * ld + pp] - mean) * rstd * (a.w ? a.w[h] : 1.f) + (a.b ? a.b[h] : 0.f);
+  if (part == 0 && pv) {
+    a.mean[g * P + p0 + pp] = mean;
+    a.rstd[g * P + p0 + pp] = rstd;
+  }
+  __syncthreads();
+  // rows g*P + p0 .. + np - 1 are consecutive: write them as one run
+  T* out = static_cast<T*>(a.nrm) + (g * P + p0) * a.h_row;
+  const int hr = (int)a.h_row;
+  const int total = np * hr;
+  for (int e = tid; e < total; e += 256) {
+    const int i = e / hr, h = e - i * hr;
+    out[e] = h < H ? (T)sm[h * ld + i] : (T)0.f;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void trimul_out_norm_backward_kernel(OutNormArgs a) {
+  extern __shared__ float sm[];  // x-hat [H][npb + 1], then grad [H][npb + 1]
+  __shared__ float red[2][256];
+  const int npb = a.npb, ld = npb + 1, parts = 256 / npb, H = a.H;
+  float* xs = sm;
+  float* gs = sm + H * ld;
+  const int64_t g = blockIdx.x / a.pblocks, p0 = (blockIdx.x % a.pblocks) * npb;
+  const int tid = threadIdx.x, pp = tid % npb, part = tid / npb;
+  const int64_t P = a.positions;
+  const int np = (int)(P - p0 < npb ? P - p0 : npb);
+  const bool pv = pp < np;
+  // grad rows [R][H] of this block's positions are consecutive
+  const T* dn = static_cast<const T*>(a.dn) + (g * P + p0) * H;
+  for (int e = tid; e < npb * H; e += 256) {
+    const int i = e / H, h = e - i * H;
+    gs[h * ld + i] = i < np ? to_f(dn[e]) : 0.f;
+  }
+  const float mean = pv ? a.mean[g * P + p0 + pp] : 0.f;
+  const float rstd = pv ? a.rstd[g * P + p0 + pp] : 0.f;
+  const T* cg = static_cast<const T*>(a.comb) + g * H * P + p0;
+  for (int h = part; h < H; h += parts) xs[h * ld + pp] = pv ? (to_f(cg[(int64_t)h * P + pp]) - mean) * rstd : 0.f;
+  __syncthreads();
+  float s1 = 0.f, s2 = 0.f;
+  for (int h = part; h < H; h += parts) {
+    const float wdy = gs[h * ld + pp] * (a.w ? a.w[h] : 1.f);
+    s1 += wdy;
+    s2 += wdy * xs[h * ld + pp];
+  }
+  red[0][tid] = s1;
+  red[1][tid] = s2;
+  __syncthreads();
+  s1 = s2 = 0.f;
+  for (int j = 0; j < parts; ++j) {
+    s1 += red[0][j * npb + pp];
+    s2 += red[1][j * npb + pp];
+  }
+  s1 /= (float)H;
+  s2 /= (float)H;
+  T* dc = static_cast<T*>(a.dcomb) + g * H * P + p0;
+  if (pv)
+    for (int h = part; h < H; h += parts) {
+      const float wdy = gs[h * ld + pp] * (a.w ? a.w[h] : 1.f);
+      dc[(int64_t)h * P + pp] = (T)(rstd * (wdy - s1 - xs[h * ld + pp] * s2));
+    }
+  for (int h = tid; h < H; h += 256) {
+    float sw = 0.f, sb = 0.f;
+    for (int i = 0; i < np; ++i) {
+      sw += gs[h * ld + i] * xs[h * ld + i];
+      sb += gs[h * ld + i];
+    }
+    if (a.dw) a.dw[(int64_t)blockIdx.x * H + h] = sw;
+    if (a.db) a.db[(int64_t)blockIdx.x * H + h] = sb;
+  }
+}
+
+// ------------------------------------------------------------------ gated output
+struct OutArgs {
+  const void* nrm;
+  const void* xn;
+  const void* wo;
+  const void* wg;
+  const float* bo;
+  const float* bg;
+  void* out;
+  const void* gout;
+  void* gval;
+  void* ggate;
+  int64_t rows, c_row, h_row, tiles;
+  int C, cblocks;
+};
+
+constexpr int kOM = 128;  // tokens per workgroup
+constexpr int kON = 64;   // output channels per workgroup
+constexpr int kOK = 64;   // k per step
+
+template <typename T, bool BWD>
+__global__ __launch_bounds__(256) void trimul_output_kernel(OutArgs a) {
+  using E = Elem<T>;
+  using Frag = typename E::Frag;
+  constexpr int WT = kON * kOK;
+  __shared__ __attribute__((aligned(16))) T w_lds[2 * WT];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, lq = lane & 31, g2 = lane >> 5;
+  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x, 0);
+  if (tile >= a.tiles) return;
+  const int cb = (int)(tile % a.cblocks);
+  const int64_t r0 = (tile / a.cblocks) * kOM;
+  const int c0 = cb * kON;
+  const int C = a.C;
+  const int64_t rows_left = a.rows - r0;
+  const int nrows = (int)(rows_left < kOM ? rows_left : kOM);
+  const bool rv = wave * 32 + lq < nrows;
+  const int wrows = C - c0 < kON ? C - c0 : kON;
+
+  f32x16 acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = f32x16{};
+
+  // acc[2 * phase + t]: phase 0 value (K = h_row, normalized rows x W_out),
+  // phase 1 gate logits (K = c_row, xn x W_gate)
+#pragma unroll
+  for (int phase = 0; phase < 2; ++phase) {
+    const int64_t stride = phase == 0 ? a.h_row : a.c_row;
+    const T* act = static_cast<const T*>(phase == 0 ? a.nrm : a.xn) + r0 * stride;
+    const T* wb = static_cast<const T*>(phase == 0 ? a.wo : a.wg) + (int64_t)c0 * stride;
+    const int K = (int)stride;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(act, (uint32_t)((int64_t)nrows * stride * 2));
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, (uint32_t)((int64_t)wrows * stride * 2));
+    const uint32_t x_lane = (uint32_t)((wave * 32 + lq) * stride * 2);
+    auto load_x = [&](int k0, uint4 (&xf)[4]) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int k = k0 + 16 * c + 8 * g2;
+        xf[c] = buffer_load16(xr, rv && k < K ? x_lane + (uint32_t)(k * 2) : kOut);
+      }
+    };
+    auto load_w = [&](int k0, uint4 (&wu)[2]) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int id = tid + 256 * j;
+        const int row = id >> 3, k = k0 + (id & 7) * 8;
+        wu[j] = buffer_load16(wr, row < wrows && k < K ? (uint32_t)((row * stride + k) * 2) : kOut);
+      }
+    };
+    auto store_w = [&](int buf, const uint4 (&wu)[2]) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int id = tid + 256 * j;
+        *reinterpret_cast<uint4*>(&w_lds[buf * WT + swz_off<kOK>(id >> 3, (id & 7) * 8)]) = wu[j];
+      }
+    };
+    const int nsteps = (K + kOK - 1) / kOK;
+    uint4 xf[4], xn[4], wu[2];
+    load_w(0, wu);
+    load_x(0, xf);
+    store_w(0, wu);
+    __syncthreads();
+    for (int i = 0; i < nsteps; ++i) {
+      const int buf = i & 1;
+      const bool more = i + 1 < nsteps;
+      if (more) {
+        load_w((i + 1) * kOK, wu);
+        load_x((i + 1) * kOK, xn);
+      }
+      const T* wt = &w_lds[buf * WT];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const Frag bfr = __builtin_bit_cast(Frag, xf[c]);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          acc[2 * phase + t] =
+              E::mma(lds_frag<T>(wt + swz_off<kOK>(32 * t + lq, 16 * c + 8 * g2)), bfr, acc[2 * phase + t]);
+      }
+      if (more) store_w(buf ^ 1, wu);
+      lds_barrier();
+#pragma unroll
+      for (int c = 0; c < 4; ++c) xf[c] = xn[c];
+    }
+  }
+
+  // ---- epilogue: lane (lq, g2) of tile t holds channels c0 + 32t + 8q + 4g2 + i of token r
+  if (!rv) return;
+  const int64_t r = r0 + wave * 32 + lq;
+  const bool vecc = (C & 7) == 0;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int n = c0 + 32 * t + 16 * g2;  // first of this lane's 16 channels after the swap
+    float v[16], s[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ch = c0 + 32 * t + 8 * q + 4 * g2 + i;
+        const bool in = ch < C;
+        v[4 * q + i] = acc[t][4 * q + i] + (in && a.bo ? a.bo[ch] : 0.f);
+        s[4 * q + i] = sigmoid_f(acc[2 + t][4 * q + i] + (in && a.bg ? a.bg[ch] : 0.f));
+      }
+    if constexpr (!BWD) {
+      uint32_t p[8];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        p[2 * q] = pack2<T>(v[4 * q] * s[4 * q], v[4 * q + 1] * s[4 * q + 1]);
+        p[2 * q + 1] = pack2<T>(v[4 * q + 2] * s[4 * q + 2], v[4 * q + 3] * s[4 * q + 3]);
+      }
+      const auto x0 = __builtin_amdgcn_permlane32_swap(p[0], p[4], false, false);
+      const auto x1 = __builtin_amdgcn_permlane32_swap(p[1], p[5], false, false);
+      const auto x2 = __builtin_amdgcn_permlane32_swap(p[2], p[6], false, false);
+      const auto x3 = __builtin_amdgcn_permlane32_swap(p[3], p[7], false, false);
+      const uint4 lo = make_uint4(x0[0], x1[0], x0[1], x1[1]);
+      const uint4 hi = make_uint4(x2[0], x3[0], x2[1], x3[1]);
+      T* orow = static_cast<T*>(a.out) + r * C;
+      if (vecc) {
+        if (n < C) *reinterpret_cast<uint4*>(orow + n) = lo;
+        if (n + 8 < C) *reinterpret_cast<uint4*>(orow + n + 8) = hi;
+      } else {
+        float e[8];
+        unpack8<T>(lo, e);
+        for (int j = 0; j < 8; ++j)
+          if (n + j < C) orow[n + j] = (T)e[j];
+        unpack8<T>(hi, e);
+        for (int j = 0; j < 8; ++j)
+          if (n + 8 + j < C) orow[n + 8 + j] = (T)e[j];
+      }
+    } else {
+      // grad_out for the lane's 16 post-swap channels, swapped back to the accumulator layout
+      const T* grow = static_cast<const T*>(a.gout) + r * C;
+      uint4 lo, hi;
+      if (vecc) {
+        lo = n < C ? *reinterpret_cast<const uint4*>(grow + n) : make_uint4(0, 0, 0, 0);
+        hi = n + 8 < C ? *reinterpret_cast<const uint4*>(grow + n + 8) : make_uint4(0, 0, 0, 0);
+      } else {
+        float e[8];
+        for (int j = 0; j < 8; ++j) e[j] = n + j < C ? to_f(grow[n + j]) : 0.f;
+        lo = pack8<T>(e);
+        for (int j = 0; j < 8; ++j) e[j] = n + 8 + j < C ? to_f(grow[n + 8 + j]) : 0.f;
+        hi = pack8<T>(e);
+      }
+      const auto y0 = __builtin_amdgcn_permlane32_swap(lo.x, lo.z, false, false);
+      const auto y1 = __builtin_amdgcn_permlane32_swap(lo.y, lo.w, false, false);
+      const auto y2 = __builtin_amdgcn_permlane32_swap(hi.x, hi.z, false, false);
+      const auto y3 = __builtin_amdgcn_permlane32_swap(hi.y, hi.w, false, false);
+      const uint32_t p[8] = {y0[0], y1[0], y2[0], y3[0], y0[1], y1[1], y2[1], y3[1]};
+      uint32_t pv[8], pg[8];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float d[4] = {lo_f<T>(p[2 * q]), hi_f<T>(p[2 * q]), lo_f<T>(p[2 * q + 1]), hi_f<T>(p[2 * q + 1])};
+        float dv[4], dg[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float sv = s[4 * q + i];
+          dv[i] = d[i] * sv;
+          dg[i] = d[i] * v[4 * q + i] * sv * (1.f - sv);
+        }
+        pv[2 * q] = pack2<T>(dv[0], dv[1]);
+        pv[2 * q + 1] = pack2<T>(dv[2], dv[3]);
+        pg[2 * q] = pack2<T>(dg[0], dg[1]);
+        pg[2 * q + 1] = pack2<T>(dg[2], dg[3]);
+      }
+      const int cr = (int)a.c_row;
+#pragma unroll
+      for (int which = 0; which < 2; ++which) {
+        const uint32_t* pp = which == 0 ? pv : pg;
+        const auto z0 = __builtin_amdgcn_permlane32_swap(pp[0], pp[4], false, false);
+        const auto z1 = __builtin_amdgcn_permlane32_swap(pp[1], pp[5], false, false);
+        const auto z2 = __builtin_amdgcn_permlane32_swap(pp[2], pp[6], false, false);
+        const auto z3 = __builtin_amdgcn_permlane32_swap(pp[3], pp[7], false, false);
+        T* drow = static_cast<T*>(which == 0 ? a.gval : a.ggate) + r * a.c_row;
+        if (n < cr) *reinterpret_cast<uint4*>(drow + n) = make_uint4(z0[0], z1[0], z0[1], z1[1]);
+        if (n + 8 < cr) *reinterpret_cast<uint4*>(drow + n + 8) = make_uint4(z2[0], z3[0], z2[1], z3[1]);
+      }
+    }
+  }
+}
+
+template <typename F>
+hipError_t by_half(int dtype, F&& f) {
+  if (dtype == OOPS_BF16) return f(__bf16{});
+  if (dtype == OOPS_F16) return f(_Float16{});
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ launchers
+namespace {
+struct RowPlan {
+  int lpr, ch, blocks;
+  bool vec;
+};
+RowPlan row_plan(const oops_row_norm_geometry& g, bool backward, const void* const* ptrs, int nptr) {
+  const int64_t span = g.y_row > g.width ? g.y_row : g.width;
+  const int64_t chunks = (span + 7) / 8;
+  int lpr = 1;
+  while (lpr < 64 && lpr < chunks) lpr *= 2;
+  int ch = 1;
+  while ((int64_t)ch * lpr < chunks) ch *= 2;
+  bool vec = g.width % 8 == 0 && g.x_row % 8 == 0 && g.y_row % 8 == 0;
+  for (int i = 0; i < nptr; ++i)
+    if (ptrs[i] && reinterpret_cast<uintptr_t>(ptrs[i]) % 16 != 0) vec = false;
+  const int rpw = 64 / lpr;
+  int64_t blocks = (g.rows + 4 * rpw - 1) / (4 * rpw);
+  if (backward && blocks > 1024) blocks = 1024;
+  return {lpr, ch, (int)blocks, vec};
+}
+
+template <typename T, int CH>
+hipError_t launch_rows(bool backward, bool vec, int blocks, const RowNormArgs& a, hipStream_t stream) {
+  if (backward) {
+    if (vec)
+      hipLaunchKernelGGL((row_norm_backward_kernel<T, CH, true>), dim3(blocks), dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((row_norm_backward_kernel<T, CH, false>), dim3(blocks), dim3(256), 0, stream, a);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((row_norm_forward_kernel<T, CH, true>), dim3(blocks), dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((row_norm_forward_kernel<T, CH, false>), dim3(blocks), dim3(256), 0, stream, a);
+  }
+  return hipGetLastError();
+}
+
+hipError_t run_rows(const oops_row_norm_geometry& g, bool backward, RowNormArgs& a, const RowPlan& pl,
+                    hipStream_t stream) {
+  a.rows = g.rows;
+  a.x_row = g.x_row;
+  a.y_row = g.y_row;
+  a.width = g.width;
+  a.lpr = pl.lpr;
+  a.eps = g.eps;
+  if (g.rows == 0) return hipSuccess;
+  return by_half(g.dtype, [&](auto tag) -> hipError_t {
+    using T = decltype(tag);
+    switch (pl.ch) {
+      case 1: return launch_rows<T, 1>(backward, pl.vec, pl.blocks, a, stream);
+      case 2: return launch_rows<T, 2>(backward, pl.vec, pl.blocks, a, stream);
+      case 4: return launch_rows<T, 4>(backward, pl.vec, pl.blocks, a, stream);
+      case 8: return launch_rows<T, 8>(backward, pl.vec, pl.blocks, a, stream);
+      default: return hipErrorInvalidValue;
+    }
+  });
+}
+}  // namespace
+
+hipError_t launch_layer_norm_rows_forward(const oops_row_norm_geometry& g, const void* x, const float* weight,
+                                          const float* bias, void* y, float* mean, float* rstd, hipStream_t stream) {
+  RowNormArgs a{};
+  a.x = x, a.w = weight, a.b = bias, a.y = y, a.mean = mean, a.rstd = rstd;
+  const void* ptrs[] = {x, y};
+  return run_rows(g, false, a, row_plan(g, false, ptrs, 2), stream);
+}
+
+int64_t layer_norm_rows_parts(const oops_row_norm_geometry& g) {
+  const void* ptrs[] = {nullptr};
+  return (int64_t)row_plan(g, true, ptrs, 0).blocks * 4;
+}
+
+hipError_t launch_layer_norm_rows_backward(const oops_row_norm_geometry& g, const void* x, const float* weight,
+                                           const float* mean, const float* rstd, const void* grad_y, void* grad_x,
+                                           float* grad_weight_parts, float* grad_bias_parts, hipStream_t stream) {
+  RowNormArgs a{};
+  a.x = x, a.w = weight, a.mean = const_cast<float*>(mean), a.rstd = const_cast<float*>(rstd);
+  a.dy = grad_y, a.dx = grad_x, a.dw = grad_weight_parts, a.db = grad_bias_parts;
+  const void* ptrs[] = {x, grad_y, grad_x};
+  return run_rows(g, true, a, row_plan(g, true, ptrs, 3), stream);
+}
+
+namespace {
+int64_t factor_cblocks(const oops_trimul_geometry& g) { return (g.hidden + 63) / 64; }
+}  // namespace
+
+int64_t trimul_mask_parts(const oops_trimul_geometry& g) { return 2 * factor_cblocks(g); }
+
+hipError_t launch_trimul_factors(const oops_trimul_geometry& g, const void* normalized, const void* weight,
+                                 const float* bias, const void* mask, void* factors, const void* grad_factors,
+                                 void* grad_projection, float* grad_mask_parts, hipStream_t stream) {
+  FactorArgs a{};
+  a.xn = normalized, a.w = weight, a.bias = bias, a.mask = g.has_mask ? static_cast<const float*>(mask) : nullptr;
+  a.factors = factors, a.grad_factors = grad_factors, a.grad_proj = grad_projection;
+  a.mask_parts = g.has_mask ? grad_mask_parts : nullptr;
+  a.rows = g.groups * g.positions, a.positions = g.positions, a.groups = g.groups, a.c_row = g.c_row;
+  a.H = g.hidden;
+  a.cblocks = (int)factor_cblocks(g);
+  const int64_t tiles = (a.rows + kFM - 1) / kFM * 2 * a.cblocks;
+  if (tiles == 0) return hipSuccess;
+  a.tiles = tiles;
+  const dim3 grid((unsigned)xcd_grid(tiles, 0));
+  const bool bwd = grad_factors != nullptr;
+  return by_half(g.dtype, [&](auto tag) -> hipError_t {
+    using T = decltype(tag);
+    if (bwd)
+      hipLaunchKernelGGL((trimul_factor_kernel<T, true>), grid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((trimul_factor_kernel<T, false>), grid, dim3(256), 0, stream, a);
+    return hipGetLastError();
+  });
+}
+
+namespace {
+// positions per output-norm workgroup: a divisor of 256 whose LDS tiles fit
+int out_norm_npb(int H, bool backward) {
+  const int tiles = backward ? 2 : 1;
+  int npb = 64;
+  while (npb > 1 && (int64_t)tiles * H * (npb + 1) * 4 > 64 * 1024) npb /= 2;
+  return npb;
+}
+}  // namespace
+
+int64_t trimul_output_norm_parts(const oops_trimul_geometry& g) {
+  const int npb = out_norm_npb(g.hidden, true);
+  return g.groups * ((g.positions + npb - 1) / npb);
+}
+
+namespace {
+hipError_t run_out_norm(const oops_trimul_geometry& g, OutNormArgs& a, bool backward, hipStream_t stream) {
+  a.groups = g.groups, a.positions = g.positions, a.h_row = g.h_row, a.H = g.hidden, a.eps = g.eps;
+  a.npb = out_norm_npb(g.hidden, backward);
+  a.pblocks = (g.positions + a.npb - 1) / a.npb;
+  const int64_t blocks = g.groups * a.pblocks;
+  if (blocks == 0) return hipSuccess;
+  const size_t lds = (size_t)(backward ? 2 : 1) * g.hidden * (a.npb + 1) * sizeof(float);
+  return by_half(g.dtype, [&](auto tag) -> hipError_t {
+    using T = decltype(tag);
+    if (backward)
+      hipLaunchKernelGGL((trimul_out_norm_backward_kernel<T>), dim3((unsigned)blocks), dim3(256), lds, stream, a);
+    else
+      hipLaunchKernelGGL((trimul_out_norm_forward_kernel<T>), dim3((unsigned)blocks), dim3(256), lds, stream, a);
+    return hipGetLastError();
+  });
+}
+}  // namespace
+
+hipError_t launch_trimul_output_norm_forward(const oops_trimul_geometry& g, const void* combined, const float* weight,
+                                             const float* bias, void* normalized, float* mean, float* rstd,
+                                             hipStream_t stream) {
+  OutNormArgs a{};
+  a.comb = combined, a.w = weight, a.b = bias, a.nrm = normalized, a.mean = mean, a.rstd = rstd;
+  return run_out_norm(g, a, false, stream);
+}
+
+hipError_t launch_trimul_output_norm_backward(const oops_trimul_geometry& g, const void* combined,
+                                              const float* weight, const float* mean, const float* rstd,
+                                              const void* grad_normalized, void* grad_combined,
+                                              float* grad_weight_parts, float* grad_bias_parts, hipStream_t stream) {
+  OutNormArgs a{};
+  a.comb = combined, a.w = weight, a.mean = const_cast<float*>(mean), a.rstd = const_cast<float*>(rstd);
+  a.dn = grad_normalized, a.dcomb = grad_combined, a.dw = grad_weight_parts, a.db = grad_bias_parts;
+  return run_out_norm(g, a, true, stream);
+}
+
+hipError_t launch_trimul_output(const oops_trimul_geometry& g, const void* normalized, const void* pair_normalized,
+                                const void* output_weight, const void* gate_weight, const float* output_bias,
+                                const float* gate_bias, void* out, const void* grad_out, void* grad_value,
+                                void* grad_gate, hipStream_t stream) {
+  OutArgs a{};
+  a.nrm = normalized, a.xn = pair_normalized, a.wo = output_weight, a.wg = gate_weight;
+  a.bo = output_bias, a.bg = gate_bias, a.out = out, a.gout = grad_out, a.gval = grad_value, a.ggate = grad_gate;
+  a.rows = g.groups * g.positions, a.c_row = g.c_row, a.h_row = g.h_row, a.C = g.channels;
+  a.cblocks = (g.channels + kON - 1) / kON;
+  const int64_t tiles = (a.rows + kOM - 1) / kOM * a.cblocks;
+  if (tiles == 0) return hipSuccess;
+  a.tiles = tiles;
+  const dim3 grid((unsigned)xcd_grid(tiles, 0));
+  const bool bwd = grad_out != nullptr;
+  return by_half(g.dtype, [&](auto tag) -> hipError_t {
+    using T = decltype(tag);
+    if (bwd)
+      hipLaunchKernelGGL((trimul_output_kernel<T, true>), grid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((trimul_output_kernel<T, false>), grid, dim3(256), 0, stream, a);
+    return hipGetLastError();
+  });
+}
+
+}  // namespace oops

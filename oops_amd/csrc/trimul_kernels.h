@@ -1,0 +1,36 @@
+// Triangle multiplicative update and row LayerNorm: launchers behind the
+// oops_layer_norm_* and oops_trimul_* C entry points.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "../../include/oops_amd.h"
+
+namespace oops {
+
+hipError_t launch_layer_norm_rows_forward(const oops_row_norm_geometry& g, const void* x, const float* weight,
+                                          const float* bias, void* y, float* mean, float* rstd, hipStream_t stream);
+hipError_t launch_layer_norm_rows_backward(const oops_row_norm_geometry& g, const void* x, const float* weight,
+                                           const float* mean, const float* rstd, const void* grad_y, void* grad_x,
+                                           float* grad_weight_parts, float* grad_bias_parts, hipStream_t stream);
+int64_t layer_norm_rows_parts(const oops_row_norm_geometry& g);
+
+hipError_t launch_trimul_factors(const oops_trimul_geometry& g, const void* normalized, const void* weight,
+                                 const float* bias, const void* mask, void* factors, const void* grad_factors,
+                                 void* grad_projection, float* grad_mask_parts, hipStream_t stream);
+int64_t trimul_mask_parts(const oops_trimul_geometry& g);
+
+hipError_t launch_trimul_output_norm_forward(const oops_trimul_geometry& g, const void* combined, const float* weight,
+                                             const float* bias, void* normalized, float* mean, float* rstd,
+                                             hipStream_t stream);
+hipError_t launch_trimul_output_norm_backward(const oops_trimul_geometry& g, const void* combined,
+                                              const float* weight, const float* mean, const float* rstd,
+                                              const void* grad_normalized, void* grad_combined,
+                                              float* grad_weight_parts, float* grad_bias_parts, hipStream_t stream);
+int64_t trimul_output_norm_parts(const oops_trimul_geometry& g);
+
+hipError_t launch_trimul_output(const oops_trimul_geometry& g, const void* normalized, const void* pair_normalized,
+                                const void* output_weight, const void* gate_weight, const float* output_bias,
+                                const float* gate_bias, void* out, const void* grad_out, void* grad_value,
+                                void* grad_gate, hipStream_t stream);
+
+}  // namespace oops

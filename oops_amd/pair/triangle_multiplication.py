@@ -1,0 +1,524 @@
+"""``triangle_multiplication``: the incoming / outgoing triangle multiplicative update.
+
+Drop-in for the reference's operator
+(oops/pair/triangle_multiplication/triangle_multiplication.py:42-443):
+
+    xn    = LayerNorm_C(pair)
+    left  = mask * (xn W_lv^T + b_lv) * sigmoid(xn W_lg^T + b_lg)     (right likewise)
+    X[i,j] = sum_k left[i,k] right[j,k]   (outgoing)  or  sum_k left[k,i] right[k,j]   (incoming)
+    out   = (LayerNorm_H(X) W_o^T + b_o) * sigmoid(xn W_og^T + b_og)
+
+per hidden channel and prefix element.  The pipeline is the reference's
+(triton/generic.py:111-200, 657-1092): the input LayerNorm, the two gated
+factor projections (one fused MFMA kernel writing the channel-major factors),
+the contraction as a batched GEMM per (group, channel) on the factors in
+place, the channel-major output LayerNorm and the fused gated output
+projection are HIP kernels behind the ``oops_layer_norm_rows_*`` /
+``oops_trimul_*`` C entry points; the backward recomputes the projections in
+the same kernels and uses library GEMMs for the weight and input gradients.
+Nested (DanLing) pairs run every ragged ``N_i x N_i`` block of the packed
+values through the same kernels, with one GEMM batch per element for the
+contraction.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Literal, Optional, Sequence
+
+import torch
+from torch import Tensor
+from torch.nn import functional as F
+
+from .. import _lib
+from .._errors import unsupported
+from ..attention._runtime import is_nested, require_no_forward_mode, require_same_device
+
+_OPERATOR = "triangle_multiplication"
+_KERNEL_DTYPES = (torch.bfloat16, torch.float16)
+_DTYPE_CODE = {torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
+MAX_FUSED_WIDTH = 1024
+
+_WEIGHT_NAMES = (
+    "input_norm_weight",
+    "input_norm_bias",
+    "left_value_weight",
+    "left_gate_weight",
+    "right_value_weight",
+    "right_gate_weight",
+    "output_norm_weight",
+    "output_norm_bias",
+    "output_weight",
+    "output_gate_weight",
+)
+_BIAS_NAMES = ("left_value_bias", "left_gate_bias", "right_value_bias", "right_gate_bias", "output_bias",
+               "output_gate_bias")  # fmt: skip
+
+
+def triangle_multiplication(
+    pair,
+    pair_mask=None,
+    *,
+    direction: Literal["incoming", "outgoing"] = "outgoing",
+    input_norm_weight: Tensor,
+    input_norm_bias: Tensor,
+    left_value_weight: Tensor,
+    left_gate_weight: Tensor,
+    right_value_weight: Tensor,
+    right_gate_weight: Tensor,
+    output_norm_weight: Tensor,
+    output_norm_bias: Tensor,
+    output_weight: Tensor,
+    output_gate_weight: Tensor,
+    left_value_bias: Optional[Tensor] = None,
+    left_gate_bias: Optional[Tensor] = None,
+    right_value_bias: Optional[Tensor] = None,
+    right_gate_bias: Optional[Tensor] = None,
+    output_bias: Optional[Tensor] = None,
+    output_gate_bias: Optional[Tensor] = None,
+    input_norm_eps: float = 1e-5,
+    output_norm_eps: float = 1e-5,
+):
+    r"""Incoming or outgoing triangle multiplicative update of pair features.
+
+    Args:
+        pair: dense ``(*prefix, N, N, C)`` or a DanLing ``NestedTensor`` with
+            ``(*prefix, N_i, N_i, C)`` elements.
+        pair_mask: optional multiplicative mask broadcastable to ``(*prefix, N, N)``
+            (or matching nested elements); floating masks are differentiable.
+        direction: ``"outgoing"`` (``X[i,j] = sum_k left[i,k] right[j,k]``) or
+            ``"incoming"`` (``X[i,j] = sum_k left[k,i] right[k,j]``).
+        input_norm_weight, input_norm_bias: ``(C,)``; output_norm_weight,
+            output_norm_bias: ``(H,)``; projections ``(H, C)``; output_weight
+            ``(C, H)``; output_gate_weight ``(C, C)``; optional biases of the
+            projections' output widths.
+
+    Returns the update with the pair's shape and dtype (no residual added).
+    """
+
+    if direction not in ("incoming", "outgoing"):
+        raise ValueError("direction must be 'incoming' or 'outgoing'")
+    weights = (input_norm_weight, input_norm_bias, left_value_weight, left_gate_weight, right_value_weight,
+               right_gate_weight, output_norm_weight, output_norm_bias, output_weight, output_gate_weight)  # fmt: skip
+    biases = (left_value_bias, left_gate_bias, right_value_bias, right_gate_bias, output_bias, output_gate_bias)
+    if is_nested(pair):
+        if pair_mask is not None and not is_nested(pair_mask):
+            raise ValueError("triangle_multiplication pair and pair_mask must both use the same NestedTensor layout")
+        return _nested(pair, pair_mask, direction, weights, biases, input_norm_eps, output_norm_eps)
+    if is_nested(pair_mask):
+        raise ValueError("triangle_multiplication pair and pair_mask must both use the same NestedTensor layout")
+    require_no_forward_mode(_OPERATOR, pair, pair_mask, *weights, *biases)
+    _check_shapes(pair, pair_mask, weights)
+    _check_bias_shapes(pair.shape[-1], weights[2].shape[0], biases)
+    require_same_device(_OPERATOR, pair, pair_mask, *weights, *biases)
+    pair, weights, biases = _prepare_autocast(pair, weights, biases)
+    n = pair.shape[-2]
+    grouped = pair.reshape(-1, n * n, pair.shape[-1])
+    mask = None
+    if pair_mask is not None:
+        mask = pair_mask.to(torch.float32) if not pair_mask.is_floating_point() else pair_mask
+        mask = mask.expand(pair.shape[:-1]).reshape(grouped.shape[:2])
+    blocks = [(0, n)]
+    out = _run(grouped, mask, blocks, direction, weights, biases, input_norm_eps, output_norm_eps)
+    return out.reshape(pair.shape)
+
+
+# ----------------------------------------------------------------- contracts
+
+
+def _broadcasts_to(shape, target) -> bool:
+    return len(shape) <= len(target) and all(s in (1, t) for s, t in zip(reversed(shape), reversed(target)))
+
+
+def _check_weight_shapes(pair_size: int, weights: Sequence[Tensor]) -> None:
+    """triangle_multiplication.py:426-443."""
+
+    hidden = weights[2].shape[0]
+    projection = (hidden, pair_size)
+    expected = ((pair_size,), (pair_size,), projection, projection, projection, projection, (hidden,), (hidden,),
+                (pair_size, hidden), (pair_size, pair_size))  # fmt: skip
+    for name, weight, shape in zip(_WEIGHT_NAMES, weights, expected):
+        if tuple(weight.shape) != shape:
+            raise ValueError(f"{name} must have shape {shape}; got {tuple(weight.shape)}")
+
+
+def _check_shapes(pair: Tensor, pair_mask: Optional[Tensor], weights) -> None:
+    """triangle_multiplication.py:403-415."""
+
+    if pair.dim() < 3:
+        raise ValueError(f"pair must have shape (..., N, N, pair_size); got rank {pair.dim()}")
+    if pair.shape[-2] != pair.shape[-3]:
+        raise ValueError(f"pair token dims must be square (N, N); got {tuple(pair.shape[-3:-1])}")
+    if pair_mask is not None and not _broadcasts_to(pair_mask.shape, pair.shape[:-1]):
+        raise ValueError(
+            f"pair_mask shape {tuple(pair_mask.shape)} must broadcast to pair[..., N, N] = {tuple(pair.shape[:-1])}"
+        )
+    _check_weight_shapes(pair.shape[-1], weights)
+
+
+def _check_bias_shapes(pair_size: int, hidden: int, biases) -> None:
+    """triangle_multiplication.py:396-400."""
+
+    widths = (hidden, hidden, hidden, hidden, pair_size, pair_size)
+    for name, bias, width in zip(_BIAS_NAMES, biases, widths):
+        if bias is not None and tuple(bias.shape) != (width,):
+            raise ValueError(f"{name} must have shape {(width,)}; got {tuple(bias.shape)}")
+
+
+def _prepare_autocast(pair: Tensor, weights, biases):
+    """Inside CUDA autocast the pair and projections take the autocast dtype
+    (triangle_multiplication.py:296-316)."""
+
+    if pair.is_cuda and torch.is_autocast_enabled("cuda"):
+        dtype = torch.get_autocast_dtype("cuda")
+        pair = pair.to(dtype)
+        weights = tuple(w.to(dtype) if i in (2, 3, 4, 5, 8, 9) else w for i, w in enumerate(weights))
+        biases = tuple(None if b is None else b.to(dtype) for b in biases)
+    return pair, weights, biases
+
+
+def _describe(t: Optional[Tensor]) -> Optional[str]:
+    return None if t is None else f"{tuple(t.shape)} {t.dtype} {t.device}"
+
+
+def _admit(pair: Tensor, weights, biases) -> None:
+    """Admission rules of supports_triangle_multiplication (triton/ops.py:68-103)."""
+
+    hidden = weights[2].shape[0]
+    affine = (weights[6], weights[7])
+    ok = (
+        pair.is_cuda
+        and pair.dtype in _KERNEL_DTYPES
+        and 0 < pair.shape[-1] <= MAX_FUSED_WIDTH
+        and 0 < hidden <= MAX_FUSED_WIDTH
+        and all(w.device == pair.device for w in weights)
+        and all(weights[i].dtype == pair.dtype for i in (2, 3, 4, 5, 8, 9))
+        and weights[0].dtype in (pair.dtype, torch.float32)
+        and weights[1].dtype == weights[0].dtype
+        and affine[0].dtype == affine[1].dtype
+        and affine[0].dtype in (pair.dtype, torch.float32)
+    )
+    if not ok:
+        raise unsupported(
+            _OPERATOR,
+            "requires a CUDA float16/bfloat16 pair, channel widths within the fused launch domain, and weights on "
+            "the pair's device in the pair's dtype (float32 allowed for the two LayerNorms)",
+            pair=_describe(pair),
+            hidden_size=hidden,
+            weight_dtypes=tuple(sorted({str(w.dtype) for w in weights})),
+        )
+    for name, b in zip(_BIAS_NAMES, biases):
+        if b is not None and b.dtype != pair.dtype:
+            raise unsupported(_OPERATOR, "requires projection biases in the pair's dtype", bias=name,
+                              operand=_describe(b))  # fmt: skip
+
+
+# ----------------------------------------------------------------- execution
+
+
+def _round8(x: int) -> int:
+    return (x + 7) // 8 * 8
+
+
+def _ptr(t: Optional[Tensor]) -> Optional[int]:
+    return None if t is None or t.numel() == 0 else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _long_k_matmul(a: Tensor, b: Tensor) -> Tensor:
+    """``a (M, K) @ b (K, N)`` for a long K (weight gradients over every pair cell).
+
+    Split into up to 64 K-chunks as one batched GEMM with float32 outputs, the
+    chunks summed in float32 and rounded once: the library's single GEMM of
+    this shape leaves most of the GPU idle.
+    """
+
+    k = a.shape[1]
+    chunks = min(64, k // 1024)
+    if chunks < 2:
+        return a.float().mm(b.float()).to(a.dtype)
+    main = k // chunks * chunks
+    step = main // chunks
+    a_c = a[:, :main].unflatten(1, (chunks, step)).transpose(0, 1)  # (chunks, M, step), strided view
+    b_c = b[:main].view(chunks, step, b.shape[1]) if b.is_contiguous() else b[:main].reshape(chunks, step, -1)
+    out = torch.bmm(a_c, b_c, out_dtype=torch.float32).sum(0)
+    if main < k:
+        out = out + a[:, main:].float().mm(b[main:].float())
+    return out.to(a.dtype)
+
+
+def _geometry(pair: Tensor, hidden: int, has_mask: bool, eps: float) -> _lib.TrimulGeometry:
+    g = _lib.TrimulGeometry()
+    g.dtype = _DTYPE_CODE[pair.dtype]
+    g.channels = pair.shape[-1]
+    g.hidden = hidden
+    g.has_mask = int(has_mask)
+    g.groups, g.positions = pair.shape[0], pair.shape[1]
+    g.c_row = _round8(g.channels)
+    g.h_row = _round8(hidden)
+    g.eps = float(eps)
+    return g
+
+
+def _row_geometry(dtype, rows: int, width: int, x_row: int, y_row: int, eps: float) -> _lib.RowNormGeometry:
+    g = _lib.RowNormGeometry()
+    g.dtype = _DTYPE_CODE[dtype]
+    g.width, g.rows, g.x_row, g.y_row, g.eps = width, rows, x_row, y_row, float(eps)
+    return g
+
+
+def _contract(factors: Tensor, out: Tensor, blocks, direction: str, grad: bool = False, grad_out=None) -> None:
+    """Per (group, channel) and ragged block: out = L R^T (outgoing) or L^T R (incoming)."""
+
+    G, H = factors.shape[1], factors.shape[2]
+    with torch.autocast("cuda", enabled=False):
+        for off, n in blocks:
+            cells = slice(off, off + n * n)
+            left = factors[0, :, :, cells].reshape(G * H, n, n)
+            right = factors[1, :, :, cells].reshape(G * H, n, n)
+            if not grad:
+                res = torch.bmm(left, right.transpose(1, 2)) if direction == "outgoing" else torch.bmm(
+                    left.transpose(1, 2), right)  # fmt: skip
+                out[:, :, cells].copy_(res.view(G, H, n * n))
+                continue
+            dx = grad_out[:, :, cells].reshape(G * H, n, n)
+            if direction == "outgoing":  # X = L R^T: dL = dX R, dR = dX^T L
+                d_left, d_right = torch.bmm(dx, right), torch.bmm(dx.transpose(1, 2), left)
+            else:  # X = L^T R: dL = R dX^T, dR = L dX
+                d_left, d_right = torch.bmm(right, dx.transpose(1, 2)), torch.bmm(left, dx)
+            out[0, :, :, cells].copy_(d_left.view(G, H, n * n))
+            out[1, :, :, cells].copy_(d_right.view(G, H, n * n))
+
+
+class _TriangleMultiplication(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, pair, mask, blocks, direction, eps_in, eps_out, *params):
+        lib = _lib.load()
+        in_w, in_b, wlv, wlg, wrv, wrg, on_w, on_b, wo, wog = params[:10]
+        blv, blg, brv, brg, bo, bog = params[10:]
+        G, P, C = pair.shape
+        H = wlv.shape[0]
+        R = G * P
+        dtype, dev = pair.dtype, pair.device
+        x = pair.resolve_neg().contiguous()
+        geo = _geometry(x, H, mask is not None, eps_out)
+        cp, hp = geo.c_row, geo.h_row
+        stream = _stream(dev)
+        f32 = lambda t: None if t is None else t.detach().resolve_neg().float().contiguous()  # noqa: E731
+        in_w32, in_b32, on_w32, on_b32 = f32(in_w), f32(in_b), f32(on_w), f32(on_b)
+        # projection weights concatenated and zero-padded to the 16-byte row the kernels load
+        w_cat = F.pad(torch.cat([w.detach().resolve_neg() for w in (wlv, wlg, wrv, wrg)]), (0, cp - C)).contiguous()
+        b_list = (blv, blg, brv, brg)
+        b_cat = None
+        if any(b is not None for b in b_list):
+            b_cat = torch.cat([torch.zeros(H, device=dev) if b is None else f32(b) for b in b_list]).contiguous()
+        wo_p = F.pad(wo.detach().resolve_neg(), (0, hp - H)).contiguous()
+        wog_p = F.pad(wog.detach().resolve_neg(), (0, cp - C)).contiguous()
+        bo32, bog32 = f32(bo), f32(bog)
+        mask32 = None if mask is None else mask.detach().resolve_neg().float().contiguous()
+
+        with torch.cuda.device(dev):
+            xn = torch.empty(R, cp, dtype=dtype, device=dev)
+            mean_in = torch.empty(R, dtype=torch.float32, device=dev)
+            rstd_in = torch.empty_like(mean_in)
+            rg = _row_geometry(dtype, R, C, C, cp, eps_in)
+            _lib.check(lib.oops_layer_norm_rows_forward(ctypes.byref(rg), _ptr(x), _ptr(in_w32), _ptr(in_b32),
+                                                        _ptr(xn), _ptr(mean_in), _ptr(rstd_in), stream),
+                       "triangle_multiplication input LayerNorm")  # fmt: skip
+            factors = torch.empty(2, G, H, P, dtype=dtype, device=dev)
+            _lib.check(lib.oops_trimul_factors_forward(ctypes.byref(geo), _ptr(xn), _ptr(w_cat), _ptr(b_cat),
+                                                       _ptr(mask32), _ptr(factors), stream),
+                       "triangle_multiplication factors")  # fmt: skip
+            combined = torch.empty(G, H, P, dtype=dtype, device=dev)
+            _contract(factors, combined, blocks, direction)
+            nrm = torch.empty(R, hp, dtype=dtype, device=dev)
+            mean_out = torch.empty(R, dtype=torch.float32, device=dev)
+            rstd_out = torch.empty_like(mean_out)
+            _lib.check(lib.oops_trimul_output_norm_forward(ctypes.byref(geo), _ptr(combined), _ptr(on_w32),
+                                                           _ptr(on_b32), _ptr(nrm), _ptr(mean_out), _ptr(rstd_out),
+                                                           stream),
+                       "triangle_multiplication output LayerNorm")  # fmt: skip
+            out = torch.empty(G, P, C, dtype=dtype, device=dev)
+            _lib.check(lib.oops_trimul_output_forward(ctypes.byref(geo), _ptr(nrm), _ptr(xn), _ptr(wo_p),
+                                                      _ptr(wog_p), _ptr(bo32), _ptr(bog32), _ptr(out), stream),
+                       "triangle_multiplication output")  # fmt: skip
+
+        ctx.save_for_backward(x, xn, mean_in, rstd_in, in_w32, w_cat, b_cat, mask32, factors, combined, nrm,
+                              mean_out, rstd_out, on_w32, wo_p, wog_p, bo32, bog32)  # fmt: skip
+        ctx.blocks, ctx.direction, ctx.eps_in, ctx.eps_out = blocks, direction, eps_in, eps_out
+        ctx.param_meta = [(None if p is None else (p.dtype, p.shape)) for p in params]
+        ctx.mask_dtype = None if mask is None else mask.dtype
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        lib = _lib.load()
+        (x, xn, mean_in, rstd_in, in_w32, w_cat, b_cat, mask32, factors, combined, nrm, mean_out, rstd_out, on_w32,
+         wo_p, wog_p, bo32, bog32) = ctx.saved_tensors  # fmt: skip
+        G, P, C = x.shape
+        H = factors.shape[2]
+        R = G * P
+        dtype, dev = x.dtype, x.device
+        geo = _geometry(x, H, mask32 is not None, ctx.eps_out)
+        cp, hp = geo.c_row, geo.h_row
+        stream = _stream(dev)
+        dout = dout.resolve_neg().to(dtype).contiguous()
+        needs = ctx.needs_input_grad
+        with torch.cuda.device(dev):
+            g_val = torch.empty(R, cp, dtype=dtype, device=dev)
+            g_gate = torch.empty(R, cp, dtype=dtype, device=dev)
+            _lib.check(lib.oops_trimul_output_backward(ctypes.byref(geo), _ptr(nrm), _ptr(xn), _ptr(wo_p),
+                                                       _ptr(wog_p), _ptr(bo32), _ptr(bog32), _ptr(dout),
+                                                       _ptr(g_val), _ptr(g_gate), stream),
+                       "triangle_multiplication output backward")  # fmt: skip
+            gv, gg = g_val[:, :C], g_gate[:, :C]
+            wo, wog = wo_p[:, :H], wog_p[:, :C]
+            d_nrm = gv.mm(wo).contiguous()  # (R, H)
+            d_xn = gg.mm(wog)  # (R, C)
+            d_wo = _long_k_matmul(gv.t(), nrm[:, :H])
+            d_wog = _long_k_matmul(gg.t(), xn[:, :C])
+            d_bo = gv.float().sum(0)
+            d_bog = gg.float().sum(0)
+
+            d_comb = torch.empty(G, H, P, dtype=dtype, device=dev)
+            parts = lib.oops_trimul_output_norm_parts(ctypes.byref(geo))
+            on_w_parts = torch.empty(parts, H, dtype=torch.float32, device=dev)
+            on_b_parts = torch.empty_like(on_w_parts)
+            _lib.check(lib.oops_trimul_output_norm_backward(ctypes.byref(geo), _ptr(combined), _ptr(on_w32),
+                                                            _ptr(mean_out), _ptr(rstd_out), _ptr(d_nrm),
+                                                            _ptr(d_comb), _ptr(on_w_parts), _ptr(on_b_parts),
+                                                            stream),
+                       "triangle_multiplication output LayerNorm backward")  # fmt: skip
+            d_factors = torch.empty_like(factors)
+            _contract(factors, d_factors, ctx.blocks, ctx.direction, grad=True, grad_out=d_comb)
+            d_proj = torch.empty(4 * H, R, dtype=dtype, device=dev)
+            want_mask = mask32 is not None and needs[1]
+            mparts = torch.empty(lib.oops_trimul_mask_parts(ctypes.byref(geo)), R, dtype=torch.float32,
+                                 device=dev) if want_mask else None  # fmt: skip
+            _lib.check(lib.oops_trimul_factors_backward(ctypes.byref(geo), _ptr(xn), _ptr(w_cat), _ptr(b_cat),
+                                                        _ptr(mask32), _ptr(d_factors), _ptr(d_proj), _ptr(mparts),
+                                                        stream),
+                       "triangle_multiplication factor backward")  # fmt: skip
+            w4 = w_cat[:, :C]
+            d_xn = torch.addmm(d_xn, d_proj.t(), w4)
+            d_w4 = _long_k_matmul(d_proj, xn[:, :C])  # (4H, C)
+            d_b4 = d_proj.float().sum(1)
+
+            d_x = torch.empty(G, P, C, dtype=dtype, device=dev)
+            rg = _row_geometry(dtype, R, C, C, C, ctx.eps_in)
+            rparts = lib.oops_layer_norm_rows_parts(ctypes.byref(rg))
+            in_w_parts = torch.empty(rparts, C, dtype=torch.float32, device=dev)
+            in_b_parts = torch.empty_like(in_w_parts)
+            d_xn = d_xn.contiguous()
+            _lib.check(lib.oops_layer_norm_rows_backward(ctypes.byref(rg), _ptr(x), _ptr(in_w32), _ptr(mean_in),
+                                                         _ptr(rstd_in), _ptr(d_xn), _ptr(d_x), _ptr(in_w_parts),
+                                                         _ptr(in_b_parts), stream),
+                       "triangle_multiplication input LayerNorm backward")  # fmt: skip
+
+        meta = ctx.param_meta
+
+        def cast(i, g):
+            return None if meta[i] is None or not needs[6 + i] else g.to(meta[i][0])
+
+        d_w4s = d_w4.split(H)
+        d_b4s = d_b4.split(H)
+        grads = [
+            cast(0, in_w_parts.sum(0)), cast(1, in_b_parts.sum(0)),
+            cast(2, d_w4s[0]), cast(3, d_w4s[1]), cast(4, d_w4s[2]), cast(5, d_w4s[3]),
+            cast(6, on_w_parts.sum(0)), cast(7, on_b_parts.sum(0)), cast(8, d_wo), cast(9, d_wog),
+            cast(10, d_b4s[0]), cast(11, d_b4s[1]), cast(12, d_b4s[2]), cast(13, d_b4s[3]),
+            cast(14, d_bo), cast(15, d_bog),
+        ]  # fmt: skip
+        d_mask = mparts.sum(0).view(G, P).to(ctx.mask_dtype) if want_mask else None
+        return (d_x if needs[0] else None, d_mask, None, None, None, None, *grads)
+
+
+def _run(grouped: Tensor, mask: Optional[Tensor], blocks, direction, weights, biases, eps_in, eps_out) -> Tensor:
+    _admit(grouped, weights, biases)
+    return _TriangleMultiplication.apply(grouped, mask, blocks, direction, float(eps_in), float(eps_out), *weights,
+                                         *biases)  # fmt: skip
+
+
+# ----------------------------------------------------------------- nested
+
+
+def _offsets(nested, level=None):
+    t = nested.packed_offsets(dtype=torch.int64) if level is None else nested.ragged_level_offsets(level, dtype=torch.int64)
+    return [int(v) for v in t.tolist()]
+
+
+def _nested(pair, pair_mask, direction, weights, biases, eps_in, eps_out):
+    """Canonical nested pairs (triangle_multiplication.py:170-223, :319-393)."""
+
+    values = pair.concat
+    require_no_forward_mode(_OPERATOR, values, None if pair_mask is None else pair_mask.concat, *weights, *biases)
+    if not pair.batch_first:
+        raise ValueError("triangle_multiplication NestedTensor batch must be the leading logical dimension")
+    if pair.dim() < 4:
+        raise ValueError(
+            "triangle_multiplication nested pair elements must have shape (*prefix, N_i, N_i, pair_size); "
+            f"got logical rank {pair.dim()}"
+        )
+    pr = pair.dim() - 4
+    token_dims = (pr, pr + 1)
+    if tuple(pair.packed_dim_order) != (*token_dims, *range(pr), pr + 2):
+        raise unsupported(_OPERATOR, "requires token-pair-major nested (*prefix, N_i, N_i, pair_size) packing",
+                          packed_dim_order=pair.packed_dim_order)  # fmt: skip
+    if tuple(pair.ragged_dims) != token_dims:
+        raise unsupported(_OPERATOR, "requires both nested token axes to be declared ragged",
+                          ragged_dims=pair.ragged_dims)  # fmt: skip
+    if values.dim() != pr + 2 or values.shape[-1] <= 0:
+        raise ValueError(
+            "triangle_multiplication nested pair elements must retain their static prefix and channel axis"
+        )
+    C = values.shape[-1]
+    _check_weight_shapes(C, weights)
+    _check_bias_shapes(C, weights[2].shape[0], biases)
+    rows, packed = _offsets(pair, 0), _offsets(pair)
+    if len(rows) <= 1:
+        raise unsupported(_OPERATOR, "does not serve an empty NestedTensor batch")
+    sizes = [b - a for a, b in zip(rows[:-1], rows[1:])]
+    if any(n <= 0 for n in sizes):
+        raise unsupported(_OPERATOR, "requires every nested pair element to have N > 0")
+    if any(b - a != n * n for a, b, n in zip(packed[:-1], packed[1:], sizes)):
+        raise ValueError("triangle_multiplication pair token dims must be square (N, N) per sample")
+    if packed[-1] != values.shape[0]:
+        raise ValueError(
+            f"triangle_multiplication pair packed layout covers {packed[-1]} positions, "
+            f"but packed values contain {values.shape[0]}"
+        )
+    prefix = tuple(values.shape[1:-1])
+    mask_values = None
+    if pair_mask is not None:
+        if not pair_mask.batch_first or pair_mask.dim() != pair.dim() - 1:
+            raise ValueError(
+                "triangle_multiplication nested pair_mask elements must have shape (*prefix, N_i, N_i) "
+                "with a leading wrapper batch"
+            )
+        if tuple(pair_mask.packed_dim_order) != (*token_dims, *range(pr)):
+            raise unsupported(_OPERATOR, "requires token-pair-major nested (*prefix, N_i, N_i) mask packing",
+                              packed_dim_order=pair_mask.packed_dim_order)  # fmt: skip
+        if tuple(pair_mask.ragged_dims) != token_dims:
+            raise unsupported(_OPERATOR, "requires both nested pair_mask token axes to be declared ragged",
+                              ragged_dims=pair_mask.ragged_dims)  # fmt: skip
+        mask_values = pair_mask.concat
+        if tuple(mask_values.shape[1:]) != prefix:
+            raise unsupported(_OPERATOR, "requires a nested pair_mask with the pair's complete static prefix")
+        if _offsets(pair_mask, 0) != rows or _offsets(pair_mask) != packed:
+            raise ValueError("triangle_multiplication pair_mask layout must match the pair layout per sample")
+    require_same_device(_OPERATOR, values, mask_values, *weights, *biases)
+    values, weights, biases = _prepare_autocast(values, weights, biases)
+    # (cells, *prefix, C) -> (prefix groups, cells, C): each static prefix element is one group
+    pr_n = len(prefix)
+    grouped = values.permute(*range(1, pr_n + 1), 0, pr_n + 1).reshape(-1, values.shape[0], C)
+    mask = None
+    if mask_values is not None:
+        m = mask_values.to(torch.float32) if not mask_values.is_floating_point() else mask_values
+        mask = m.permute(*range(1, pr_n + 1), 0).reshape(-1, values.shape[0])
+    blocks = [(a, n) for a, n in zip(packed[:-1], sizes)]
+    out = _run(grouped, mask, blocks, direction, weights, biases, eps_in, eps_out)
+    out = out.reshape(*prefix, values.shape[0], C).permute(pr_n, *range(pr_n), pr_n + 1)
+    return pair.packed_like(out.contiguous())

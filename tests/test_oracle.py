@@ -252,3 +252,110 @@ def test_gate_rounding_points_vs_torch_bf16():
         att.double().numpy(), single.double().numpy(), w.double().numpy(), wo.double().numpy(), rounding="bf16")
     np.testing.assert_array_equal(got_logits, logits.double().numpy())
     np.testing.assert_array_equal(got_gated, gated.double().numpy())
+
+
+# ------------------------------------------------------------------ triangle multiplicative update
+
+from oracle import trimul as otm  # noqa: E402
+
+
+def _trimul_case(seed, n=5, c=6, h=4, prefix=(2,), biases=True):
+    g = np.random.default_rng(seed)
+    pair = g.standard_normal((*prefix, n, n, c))
+    mask = (g.random((*prefix, n, n)) > 0.2).astype(np.float64) * g.uniform(0.5, 1.5, (*prefix, n, n))
+    weights = (
+        g.standard_normal(c), g.standard_normal(c),
+        g.standard_normal((h, c)) / c**0.5, g.standard_normal((h, c)) / c**0.5,
+        g.standard_normal((h, c)) / c**0.5, g.standard_normal((h, c)) / c**0.5,
+        g.standard_normal(h), g.standard_normal(h),
+        g.standard_normal((c, h)) / h**0.5, g.standard_normal((c, c)) / c**0.5,
+    )  # fmt: skip
+    bs = tuple(0.2 * g.standard_normal(w) for w in (h, h, h, h, c, c)) if biases else (None,) * 6
+    return pair, mask, weights, bs
+
+
+def _trimul_torch(pair, mask, weights, biases, direction):
+    """The reference test's own formulation (test_triangle_multiplication.py:166-198) in torch."""
+
+    iw, ib, wlv, wlg, wrv, wrg, ow, ob, wo, wog = weights
+    blv, blg, brv, brg, bo, bog = biases
+    normalized = F.layer_norm(pair, (pair.shape[-1],), iw, ib, 1e-5)
+    left = F.linear(normalized, wlv, blv) * torch.sigmoid(F.linear(normalized, wlg, blg))
+    right = F.linear(normalized, wrv, brv) * torch.sigmoid(F.linear(normalized, wrg, brg))
+    if mask is not None:
+        left = left * mask.unsqueeze(-1)
+        right = right * mask.unsqueeze(-1)
+    left, right = left.movedim(-1, -3), right.movedim(-1, -3)
+    combined = left @ right.transpose(-1, -2) if direction == "outgoing" else left.transpose(-1, -2) @ right
+    combined = combined.movedim(-3, -1)
+    update = F.layer_norm(combined, (combined.shape[-1],), ow, ob, 1e-5)
+    return F.linear(update, wo, bo) * torch.sigmoid(F.linear(normalized, wog, bog))
+
+
+def test_trimul_docstring_example():
+    """oops/pair/triangle_multiplication/triangle_multiplication.py:128-145: a constant pair with identity
+    weights and zero biases normalizes to zero, so every factor and the update are zero."""
+
+    c = 16
+    eye, ones, zeros = np.eye(c), np.ones(c), np.zeros(c)
+    weights = (ones, zeros, eye, eye, eye, eye, ones, zeros, eye, eye)
+    out = otm.triangle_multiplication_forward(np.ones((2, 2, c)), None, weights)
+    assert out.shape == (2, 2, c)
+    np.testing.assert_array_equal(out, np.zeros((2, 2, c)))
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+@pytest.mark.parametrize("biases", [True, False])
+def test_trimul_vs_torch_autograd(direction, biases):
+    pair, mask, weights, bs = _trimul_case(3 + biases, biases=biases)
+    want_out = otm.triangle_multiplication_forward(pair, mask, weights, bs, direction)
+    t = lambda x: None if x is None else torch.tensor(x, dtype=torch.float64, requires_grad=True)  # noqa: E731
+    tp, tm = t(pair), t(mask)
+    tw, tb = [t(w) for w in weights], [t(b) for b in bs]
+    out = _trimul_torch(tp, tm, tw, tb, direction)
+    np.testing.assert_allclose(out.detach().numpy(), want_out, rtol=1e-10, atol=1e-12)
+    dy = np.random.default_rng(9).standard_normal(out.shape)
+    leaves = [tp, tm, *tw, *[b for b in tb if b is not None]]
+    grads = torch.autograd.grad(out, leaves, torch.tensor(dy))
+    d_pair, d_mask, d_w, d_b = otm.triangle_multiplication_backward(pair, mask, weights, bs, dy, direction)
+    mine = [d_pair, d_mask, *d_w, *[b for b in d_b if b is not None]]
+    assert len(mine) == len(grads)
+    for got, ref in zip(mine, grads):
+        np.testing.assert_allclose(got, ref.numpy(), rtol=1e-9, atol=1e-10)
+
+
+def test_trimul_broadcast_mask_gradient():
+    """A mask broadcast over the prefix gets the prefix-summed gradient."""
+
+    pair, mask, weights, bs = _trimul_case(5, prefix=(3,))
+    mask1 = mask[:1]
+    dy = np.random.default_rng(2).standard_normal(pair.shape)
+    _, d_m, _, _ = otm.triangle_multiplication_backward(pair, mask1, weights, bs, dy)
+    _, d_full, _, _ = otm.triangle_multiplication_backward(pair, np.broadcast_to(mask1, mask.shape), weights, bs, dy)
+    assert d_m.shape == mask1.shape
+    np.testing.assert_allclose(d_m, d_full.sum(0, keepdims=True), rtol=1e-12)
+
+
+def test_trimul_finite_differences():
+    pair, mask, weights, bs = _trimul_case(7, n=4, c=5, h=3, prefix=())
+    dy = np.random.default_rng(1).standard_normal(pair.shape)
+    d_pair, d_mask, d_w, d_b = otm.triangle_multiplication_backward(pair, mask, weights, bs, dy, "incoming")
+
+    def f(p=pair, m=mask, w=weights, b=bs):
+        return (otm.triangle_multiplication_forward(p, m, w, b, "incoming") * dy).sum()
+
+    eps = 1e-6
+    rng = np.random.default_rng(0)
+    checks = [("pair", pair, d_pair, lambda x: f(p=x)), ("mask", mask, d_mask, lambda x: f(m=x))]
+    for i in (0, 2, 7, 9):
+        checks.append((f"w{i}", weights[i], d_w[i],
+                       lambda x, i=i: f(w=tuple(x if j == i else w for j, w in enumerate(weights)))))  # fmt: skip
+    checks.append(("b_og", bs[5], d_b[5], lambda x: f(b=(*bs[:5], x))))
+    for name, x0, grad, fn in checks:
+        for _ in range(3):
+            idx = tuple(rng.integers(0, s) for s in x0.shape)
+            xp, xm = x0.copy(), x0.copy()
+            xp[idx] += eps
+            xm[idx] -= eps
+            fd = (fn(xp) - fn(xm)) / (2 * eps)
+            assert abs(fd - grad[idx]) < 1e-5 * max(1.0, abs(fd)), (name, idx, fd, grad[idx])

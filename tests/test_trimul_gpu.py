@@ -1,0 +1,201 @@
+"""GPU parity of triangle_multiplication against the float64 oracle (oracle/trimul.py).
+
+Mirrors the reference's cases (tests/pair/triangle_multiplication/
+test_triangle_multiplication.py:305-330): odd channel and hidden widths
+(C = 17, 65, H = 12, 24, 96), both directions, with and without projection
+biases, float and bool masks, prefixes, strided and broadcast masks, nested
+ragged pairs with and without a static prefix, and an AlphaFold-sized
+C = H = 128 pair.  Forward values use the oracle with the reference's
+storage roundings; gradients (pair, mask, every weight and bias) are checked
+against the oracle's float64 derivative with the reference's gradient
+criterion (error within tol x the gradient tensor's largest magnitude).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from accuracy import assert_close
+from nested_standin import NestedTensor
+from oops_amd import OOpsUnsupportedError, triangle_multiplication
+from oracle import trimul as otm
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+_ROUNDING = {torch.bfloat16: "bf16", torch.float16: "f16"}
+_NAMES = ("input_norm_weight", "input_norm_bias", "left_value_weight", "left_gate_weight", "right_value_weight",
+          "right_gate_weight", "output_norm_weight", "output_norm_bias", "output_weight", "output_gate_weight")
+_BIAS = ("left_value_bias", "left_gate_bias", "right_value_bias", "right_gate_bias", "output_bias",
+         "output_gate_bias")  # fmt: skip
+
+
+# the reference's gradient criterion for this operator
+# (tests/pair/triangle_multiplication/test_triangle_multiplication.py:36-40, :458-464):
+# |got - want| <= tol * max(1, max |want|) over each gradient tensor
+_GRAD_TOL = {torch.bfloat16: 5e-2, torch.float16: 3e-2}
+
+
+def _assert_grad_close(got, want, dtype, what):
+    got = got.detach().double().cpu().numpy()
+    err = np.abs(got - want).max()
+    scale = max(1.0, float(np.abs(want).max()))
+    assert err <= _GRAD_TOL[dtype] * scale, f"{what}: max-abs {err:.3g} against {_GRAD_TOL[dtype]} x {scale:.3g}"
+
+
+def _np(t):
+    return None if t is None else t.detach().double().cpu().numpy()
+
+
+def _params(dtype, c, h, seed, biases=True, norm_dtype=None):
+    g = torch.Generator().manual_seed(seed)
+    nd = norm_dtype or dtype
+
+    def r(*shape, scale=1.0, dt=dtype):
+        return (torch.randn(*shape, generator=g) * scale).to(dt).to(DEV).requires_grad_(True)
+
+    weights = (r(c, dt=nd), r(c, dt=nd), r(h, c, scale=c**-0.5), r(h, c, scale=c**-0.5), r(h, c, scale=c**-0.5),
+               r(h, c, scale=c**-0.5), r(h, dt=nd), r(h, dt=nd), r(c, h, scale=h**-0.5), r(c, c, scale=c**-0.5))  # fmt: skip
+    bs = tuple(r(w, scale=0.2) for w in (h, h, h, h, c, c)) if biases else (None,) * 6
+    return weights, bs
+
+
+def _call(pair, mask, weights, bs, direction):
+    kw = dict(zip(_NAMES, weights))
+    kw.update({k: v for k, v in zip(_BIAS, bs)})
+    return triangle_multiplication(pair, mask, direction=direction, **kw)
+
+
+def _check(pair, mask, weights, bs, direction, dtype, grads=True, mask_grad=False):
+    out = _call(pair, mask, weights, bs, direction)
+    assert out.shape == pair.shape and out.dtype == dtype
+    np_w, np_b = [_np(w) for w in weights], [_np(b) for b in bs]
+    want = otm.triangle_multiplication_forward(_np(pair), _np(mask), np_w, np_b, direction,
+                                               rounding=_ROUNDING[dtype])  # fmt: skip
+    assert_close(out, want, dtype, "out")
+    if not grads:
+        return
+    dy = torch.randn(out.shape, generator=torch.Generator().manual_seed(11)).to(dtype).to(DEV)
+    leaves = [pair, *weights, *[b for b in bs if b is not None]] + ([mask] if mask_grad else [])
+    got = torch.autograd.grad(out, leaves, dy)
+    d_pair, d_mask, d_w, d_b = otm.triangle_multiplication_backward(_np(pair), _np(mask), np_w, np_b, _np(dy),
+                                                                    direction)  # fmt: skip
+    want_g = [d_pair, *d_w, *[b for b in d_b if b is not None]] + ([d_mask] if mask_grad else [])
+    names = ["pair", *_NAMES, *[n for n, b in zip(_BIAS, bs) if b is not None]] + (["mask"] if mask_grad else [])
+    for name, g_, w_ in zip(names, got, want_g):
+        assert g_.shape == tuple(w_.shape), name
+        _assert_grad_close(g_, w_, dtype, "d" + name)
+
+
+@pytest.mark.parametrize(
+    "dtype,c,h,n,prefix,direction,biases",
+    [
+        (torch.bfloat16, 32, 32, 16, (2,), "outgoing", True),
+        (torch.bfloat16, 32, 32, 16, (2,), "incoming", True),
+        (torch.float16, 8, 12, 9, (), "outgoing", False),
+        (torch.bfloat16, 17, 24, 7, (), "outgoing", True),
+        (torch.float16, 65, 96, 17, (), "incoming", True),
+        (torch.bfloat16, 128, 128, 19, (2, 3), "outgoing", False),
+        (torch.bfloat16, 128, 128, 64, (1,), "incoming", True),
+    ],
+)
+def test_trimul_dense(dtype, c, h, n, prefix, direction, biases):
+    g = torch.Generator().manual_seed(c + h + n)
+    pair = torch.randn(*prefix, n, n, c, generator=g).to(dtype).to(DEV).requires_grad_(True)
+    mask = (torch.rand(*prefix, n, n, generator=g) > 0.2).to(DEV)
+    weights, bs = _params(dtype, c, h, seed=n, biases=biases)
+    _check(pair, mask, weights, bs, direction, dtype)
+
+
+def test_trimul_float_mask_gradient_and_broadcast():
+    """A fractional float mask broadcast over the prefix: its gradient is summed over the prefix."""
+
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(4)
+    pair = torch.randn(3, 12, 12, 32, generator=g).to(dtype).to(DEV).requires_grad_(True)
+    mask = torch.rand(1, 12, 12, generator=g).to(DEV).requires_grad_(True)
+    weights, bs = _params(dtype, 32, 48, seed=5)
+    _check(pair, mask, weights, bs, "incoming", dtype, mask_grad=True)
+
+
+def test_trimul_no_mask_fp32_norm_weights():
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(6)
+    pair = torch.randn(2, 10, 10, 24, generator=g).to(dtype).to(DEV).requires_grad_(True)
+    weights, bs = _params(dtype, 24, 40, seed=6, norm_dtype=torch.float32)
+    _check(pair, None, weights, bs, "outgoing", dtype)
+
+
+def test_trimul_strided_pair():
+    """A non-contiguous pair view (the reference's 'strided' layout)."""
+
+    dtype = torch.float16
+    g = torch.Generator().manual_seed(8)
+    base = torch.randn(11, 11, 40, 2, generator=g).to(dtype).to(DEV)
+    pair = base[..., 0].requires_grad_(False)
+    assert not pair.is_contiguous()
+    weights, bs = _params(dtype, 40, 32, seed=8)
+    out = _call(pair, None, weights, bs, "outgoing")
+    want = otm.triangle_multiplication_forward(_np(pair), None, [_np(w) for w in weights], [_np(b) for b in bs],
+                                               "outgoing", rounding="f16")  # fmt: skip
+    assert_close(out, want, dtype, "out")
+
+
+@pytest.mark.parametrize("prefix,direction", [((), "outgoing"), ((2,), "incoming")])
+def test_trimul_nested(prefix, direction):
+    dtype = torch.bfloat16
+    lengths = (5, 12, 9)
+    c, h = 32, 48
+    pr = len(prefix)
+    tmpl = NestedTensor([torch.empty(*prefix, n, n, c) for n in lengths], ragged_dims=(pr, pr + 1))
+    g = torch.Generator().manual_seed(3)
+    values = torch.randn(tmpl.concat.shape, generator=g).to(dtype).to(DEV).requires_grad_(True)
+    pair = tmpl.packed_like(values)
+    mtmpl = NestedTensor([torch.empty(*prefix, n, n) for n in lengths], ragged_dims=(pr, pr + 1))
+    mask = mtmpl.packed_like((torch.rand(mtmpl.concat.shape, generator=g) > 0.2).float().to(DEV))
+    weights, bs = _params(dtype, c, h, seed=3)
+    out = _call(pair, mask, weights, bs, direction)
+    assert isinstance(out, NestedTensor) and out.concat.shape == values.shape
+    dy = torch.randn(values.shape, generator=g).to(dtype).to(DEV)
+    got = torch.autograd.grad(out.concat, [values, weights[2], weights[8]], dy)
+    np_w, np_b = [_np(w) for w in weights], [_np(b) for b in bs]
+    d_pairs, d_wlv, d_wo = [], 0.0, 0.0
+    dys = out.packed_like(dy).unbind()
+    for i, (pe, me, oe, de) in enumerate(zip(pair.unbind(), mask.unbind(), out.unbind(), dys)):
+        want = otm.triangle_multiplication_forward(_np(pe), _np(me), np_w, np_b, direction, rounding="bf16")
+        assert_close(oe, want, dtype, f"out[{i}]")
+        dp, _, dw, _ = otm.triangle_multiplication_backward(_np(pe), _np(me), np_w, np_b, _np(de), direction)
+        d_pairs.append(torch.from_numpy(dp))
+        d_wlv, d_wo = d_wlv + dw[2], d_wo + dw[8]
+    _assert_grad_close(got[0], torch.cat([pair._pack(d) for d in d_pairs]).numpy(), dtype, "dpair")
+    _assert_grad_close(got[1], d_wlv, dtype, "d_left_value_weight")
+    _assert_grad_close(got[2], d_wo, dtype, "d_output_weight")
+
+
+def test_trimul_alphafold_size():
+    """N = 256, C = H = 128, bf16: forward against the oracle on the full pair; gradients of the pair
+    and the output projection against the oracle."""
+
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(12)
+    n = 256
+    pair = torch.randn(n, n, 128, generator=g).to(dtype).to(DEV).requires_grad_(True)
+    mask = (torch.rand(n, n, generator=g) > 0.1).to(DEV)
+    weights, bs = _params(dtype, 128, 128, seed=12)
+    _check(pair, mask, weights, bs, "outgoing", dtype)
+
+
+def test_trimul_errors():
+    weights, bs = _params(torch.bfloat16, 16, 8, seed=1)
+    pair = torch.randn(4, 4, 16, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        _call(pair, None, weights, bs, "sideways")
+    with pytest.raises(ValueError):
+        _call(pair[:, :3], None, weights, bs, "outgoing")
+    with pytest.raises(ValueError):
+        _call(pair, torch.ones(5, 4, device=DEV), weights, bs, "outgoing")
+    with pytest.raises(ValueError):
+        _call(pair, None, (weights[0][:-1], *weights[1:]), bs, "outgoing")
+    fw, fb = _params(torch.float64, 16, 8, seed=1)
+    with pytest.raises(OOpsUnsupportedError):
+        _call(pair.double(), None, fw, fb, "outgoing")
