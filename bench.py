@@ -307,6 +307,57 @@ def nested_msa(device):
     }
 
 
+def trimul_stage(device, n=512, c=128, h=128):
+    """triangle_multiplication (outgoing) fwd+bwd on one (N, N, C) pair, C = H = 128, bf16, a key-padding
+    style mask, projection biases; the row after attention in the Pairformer block.  Reports the whole
+    fwd+bwd and the algorithmic GEMM rate (projections, contraction, output)."""
+
+    import torch
+
+    from oops_amd import triangle_multiplication
+
+    g = torch.Generator().manual_seed(13)
+    dt = torch.bfloat16
+
+    def r(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=g) * scale).to(dt).to(device).requires_grad_(True)
+
+    pair = r(1, n, n, c)
+    mask = torch.ones(1, n, n, device=device)
+    mask[:, :, n - n // 8 :] = 0
+    mask[:, n - n // 8 :, :] = 0
+    w = dict(
+        input_norm_weight=r(c), input_norm_bias=r(c),
+        left_value_weight=r(h, c, scale=c**-0.5), left_gate_weight=r(h, c, scale=c**-0.5),
+        right_value_weight=r(h, c, scale=c**-0.5), right_gate_weight=r(h, c, scale=c**-0.5),
+        output_norm_weight=r(h), output_norm_bias=r(h),
+        output_weight=r(c, h, scale=h**-0.5), output_gate_weight=r(c, c, scale=c**-0.5),
+        left_value_bias=r(h), left_gate_bias=r(h), right_value_bias=r(h), right_gate_bias=r(h),
+        output_bias=r(c), output_gate_bias=r(c),
+    )  # fmt: skip
+    leaves = [pair, *w.values()]
+    dy = torch.randn(1, n, n, c, generator=g).to(dt).to(device)
+
+    def fwd():
+        return triangle_multiplication(pair, mask, direction="outgoing", **w)
+
+    def step():
+        torch.autograd.grad(fwd(), leaves, dy)
+
+    ms = _median_ms(step, iters=10, warmup=3)
+    with torch.no_grad():
+        ms_fwd = _median_ms(fwd, iters=10, warmup=3)
+    rows = n * n
+    fwd_flops = 2 * rows * c * 4 * h + 2 * h * n**3 + 2 * rows * (h + c) * c
+    flops = 3 * fwd_flops  # backward: two products per forward product
+    return {
+        "workload": f"triangle_multiplication outgoing fwd+bwd, N={n}, C=H={c}, bf16, mask, biases",
+        "ms_fwd_bwd": round(ms, 4),
+        "ms_fwd": round(ms_fwd, 4),
+        "tflops_fwd_bwd": round(flops / ms / 1e9, 2),
+    }
+
+
 def gate_stage(device):
     """The gated output stage (the row after attention) at config 4's MSA shape.
 
@@ -418,6 +469,11 @@ def main():
         help="only copy a 256 MiB device buffer 3 times (scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)",
     )
     ap.add_argument(
+        "--trimul-only",
+        action="store_true",
+        help="only measure triangle_multiplication (N=512, C=H=128, 3 repetitions) and print its JSON",
+    )
+    ap.add_argument(
         "--gate-only",
         action="store_true",
         help="only measure the gated output stage at config 4's MSA shape (3 repetitions) and print its JSON",
@@ -446,6 +502,11 @@ def main():
     _lib.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.trimul_only:
+        for _ in range(3):
+            res = trimul_stage(dev)
+        print(json.dumps(res))
+        return
     if args.gate_only:
         for _ in range(3):
             gate = gate_stage(dev)
@@ -518,7 +579,8 @@ def main():
         line["other_configs"] = other_configs(dev)
         _log("bench: " + json.dumps(line["other_configs"]))
         _log("bench: gated output stage")
-        line["next_rows"] = {"gate_c4_shape": gate_stage(dev), "nested_msa": nested_msa(dev)}
+        line["next_rows"] = {"gate_c4_shape": gate_stage(dev), "nested_msa": nested_msa(dev),
+                             "trimul_n512": trimul_stage(dev)}
         _log("bench: " + json.dumps(line["next_rows"]))
     if not args.no_cpu:
         _log("bench: cpu baseline")

@@ -91,11 +91,36 @@ __device__ __forceinline__ void load_chunks(const T* row, bool valid, int width,
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int col = (c * lpr + sub) * 8;
-    if (VEC && valid && col < width) {
-      unpack8<T>(*reinterpret_cast<const uint4*>(row + col), x[c]);
-    } else {
+    if constexpr (VEC) {
+      // width % 8 == 0: a chunk is wholly inside or outside the row
+      if (valid && col < width) {
+        unpack8<T>(*reinterpret_cast<const uint4*>(row + col), x[c]);
+      } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[c][e] = valid && col + e < width ? to_f(row[col + e]) : 0.f;
+        for (int e = 0; e < 8; ++e) x[c][e] = 0.f;
+      }
+    } else {
+      // clamped (always in-bounds) loads, selected afterwards: no divergent branches around loads
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int cc = col + e < width ? col + e : width - 1;
+        const float v = to_f(row[cc]);
+        x[c][e] = valid && col + e < width ? v : 0.f;
+      }
+    }
+  }
+}
+
+// per-column affine parameters for a lane's chunks (clamped indices; 1 / 0 when absent)
+template <int CH>
+__device__ __forceinline__ void load_affine(const float* p, float none, int width, int lpr, int sub, float (&v)[CH][8]) {
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int col = (c * lpr + sub) * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int cc = col + e < width ? col + e : width - 1;
+      v[c][e] = p ? p[cc] : none;
     }
   }
 }
@@ -110,50 +135,56 @@ __global__ __launch_bounds__(256) void row_norm_forward_kernel(RowNormArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lpr = a.lpr, rpw = 64 / lpr;
   const int sub = lane & (lpr - 1), rw = lane / lpr;
-  const int64_t row = ((int64_t)blockIdx.x * 4 + wave) * rpw + rw;
-  const bool rv = row < a.rows;
   const int W = a.width;
-  const T* xr = static_cast<const T*>(a.x) + (rv ? row : 0) * a.x_row;
-  float x[CH][8];
-  load_chunks<T, CH, VEC>(xr, rv, W, lpr, sub, x);
-  float s = 0.f;
+  float wv[CH][8], bv[CH][8];
+  load_affine<CH>(a.w, 1.f, W, lpr, sub, wv);
+  load_affine<CH>(a.b, 0.f, W, lpr, sub, bv);
+  // a bounded grid walks the rows: many rows per wave keep the loads of
+  // successive rows in flight (one short row per wave leaves HBM idle)
+  const int64_t step = (int64_t)gridDim.x * 4 * rpw;
+  for (int64_t base = ((int64_t)blockIdx.x * 4 + wave) * rpw; base < a.rows; base += step) {
+    const int64_t row = base + rw;
+    const bool rv = row < a.rows;
+    float x[CH][8];
+    load_chunks<T, CH, VEC>(static_cast<const T*>(a.x) + (rv ? row : 0) * a.x_row, rv, W, lpr, sub, x);
+    float s = 0.f;
 #pragma unroll
-  for (int c = 0; c < CH; ++c)
+    for (int c = 0; c < CH; ++c)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) s += x[c][e];
-  const float mean = group_sum(s, lpr) / (float)W;
-  float q = 0.f;
+      for (int e = 0; e < 8; ++e) s += x[c][e];
+    const float mean = group_sum(s, lpr) / (float)W;
+    float q = 0.f;
 #pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int col = (c * lpr + sub) * 8;
+    for (int c = 0; c < CH; ++c) {
+      const int col = (c * lpr + sub) * 8;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float d = col + e < W ? x[c][e] - mean : 0.f;
-      q += d * d;
+      for (int e = 0; e < 8; ++e) {
+        const float d = col + e < W ? x[c][e] - mean : 0.f;
+        q += d * d;
+      }
     }
-  }
-  const float rstd = rsqrtf(group_sum(q, lpr) / (float)W + a.eps);
-  if (!rv) return;
-  T* yr = static_cast<T*>(a.y) + row * a.y_row;
+    const float rstd = rsqrtf(group_sum(q, lpr) / (float)W + a.eps);
+    if (!rv) continue;
+    T* yr = static_cast<T*>(a.y) + row * a.y_row;
 #pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int col = (c * lpr + sub) * 8;
-    if (col >= a.y_row) continue;
-    float o[8];
+    for (int c = 0; c < CH; ++c) {
+      const int col = (c * lpr + sub) * 8;
+      if (col >= a.y_row) continue;
+      float o[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      o[e] = col + e < W ? (x[c][e] - mean) * rstd * (a.w ? a.w[col + e] : 1.f) + (a.b ? a.b[col + e] : 0.f) : 0.f;
-    if (VEC) {
-      *reinterpret_cast<uint4*>(yr + col) = pack8<T>(o);
-    } else {
+      for (int e = 0; e < 8; ++e) o[e] = col + e < W ? (x[c][e] - mean) * rstd * wv[c][e] + bv[c][e] : 0.f;
+      if (VEC) {
+        *reinterpret_cast<uint4*>(yr + col) = pack8<T>(o);
+      } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (col + e < a.y_row) yr[col + e] = (T)o[e];
+        for (int e = 0; e < 8; ++e)
+          if (col + e < a.y_row) yr[col + e] = (T)o[e];
+      }
     }
-  }
-  if (sub == 0) {
-    a.mean[row] = mean;
-    a.rstd[row] = rstd;
+    if (sub == 0) {
+      a.mean[row] = mean;
+      a.rstd[row] = rstd;
+    }
   }
 }
 
@@ -164,6 +195,8 @@ __global__ __launch_bounds__(256) void row_norm_backward_kernel(RowNormArgs a) {
   const int sub = lane & (lpr - 1), rw = lane / lpr;
   const int W = a.width;
   const float inv_w = 1.0f / (float)W;
+  float wv[CH][8];
+  load_affine<CH>(a.w, 1.f, W, lpr, sub, wv);
   float dw[CH][8], db[CH][8];
 #pragma unroll
   for (int c = 0; c < CH; ++c)
@@ -186,7 +219,7 @@ __global__ __launch_bounds__(256) void row_norm_backward_kernel(RowNormArgs a) {
       for (int e = 0; e < 8; ++e) {
         const bool in = col + e < W;
         const float xh = in ? (x[c][e] - mean) * rstd : 0.f;
-        const float wdy = in ? g[c][e] * (a.w ? a.w[col + e] : 1.f) : 0.f;
+        const float wdy = in ? g[c][e] * wv[c][e] : 0.f;
         x[c][e] = xh;
         s1 += wdy;
         s2 += wdy * xh;
@@ -205,7 +238,7 @@ __global__ __launch_bounds__(256) void row_norm_backward_kernel(RowNormArgs a) {
       float o[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        o[e] = rstd * (g[c][e] * (a.w && col + e < W ? a.w[col + e] : 1.f) - s1 - x[c][e] * s2);
+        o[e] = rstd * (g[c][e] * wv[c][e] - s1 - x[c][e] * s2);
       if (VEC) {
         *reinterpret_cast<uint4*>(dxr + col) = pack8<T>(o);
       } else {
@@ -814,7 +847,7 @@ RowPlan row_plan(const oops_row_norm_geometry& g, bool backward, const void* con
     if (ptrs[i] && reinterpret_cast<uintptr_t>(ptrs[i]) % 16 != 0) vec = false;
   const int rpw = 64 / lpr;
   int64_t blocks = (g.rows + 4 * rpw - 1) / (4 * rpw);
-  if (backward && blocks > 1024) blocks = 1024;
+  if (blocks > 1024) blocks = 1024;  // both kernels walk the rows with a bounded grid
   return {lpr, ch, (int)blocks, vec};
 }
 

@@ -274,7 +274,28 @@ def _contract(factors: Tensor, out: Tensor, blocks, direction: str, grad: bool =
     """Per (group, channel) and ragged block: out = L R^T (outgoing) or L^T R (incoming)."""
 
     G, H = factors.shape[1], factors.shape[2]
+    whole = len(blocks) == 1 and blocks[0][1] ** 2 == factors.shape[3]
     with torch.autocast("cuda", enabled=False):
+        if whole and not grad:
+            n = blocks[0][1]
+            left, right = factors[0].view(G * H, n, n), factors[1].view(G * H, n, n)
+            if direction == "outgoing":
+                torch.bmm(left, right.transpose(1, 2), out=out.view(G * H, n, n))
+            else:
+                torch.bmm(left.transpose(1, 2), right, out=out.view(G * H, n, n))
+            return
+        if whole:
+            n = blocks[0][1]
+            left, right = factors[0].view(G * H, n, n), factors[1].view(G * H, n, n)
+            dx = grad_out.view(G * H, n, n)
+            d_left, d_right = out[0].view(G * H, n, n), out[1].view(G * H, n, n)
+            if direction == "outgoing":
+                torch.bmm(dx, right, out=d_left)
+                torch.bmm(dx.transpose(1, 2), left, out=d_right)
+            else:
+                torch.bmm(right, dx.transpose(1, 2), out=d_left)
+                torch.bmm(left, dx, out=d_right)
+            return
         for off, n in blocks:
             cells = slice(off, off + n * n)
             left = factors[0, :, :, cells].reshape(G * H, n, n)
@@ -307,17 +328,31 @@ class _TriangleMultiplication(torch.autograd.Function):
         geo = _geometry(x, H, mask is not None, eps_out)
         cp, hp = geo.c_row, geo.h_row
         stream = _stream(dev)
-        f32 = lambda t: None if t is None else t.detach().resolve_neg().float().contiguous()  # noqa: E731
-        in_w32, in_b32, on_w32, on_b32 = f32(in_w), f32(in_b), f32(on_w), f32(on_b)
-        # projection weights concatenated and zero-padded to the 16-byte row the kernels load
-        w_cat = F.pad(torch.cat([w.detach().resolve_neg() for w in (wlv, wlg, wrv, wrg)]), (0, cp - C)).contiguous()
-        b_list = (blv, blg, brv, brg)
-        b_cat = None
-        if any(b is not None for b in b_list):
-            b_cat = torch.cat([torch.zeros(H, device=dev) if b is None else f32(b) for b in b_list]).contiguous()
-        wo_p = F.pad(wo.detach().resolve_neg(), (0, hp - H)).contiguous()
-        wog_p = F.pad(wog.detach().resolve_neg(), (0, cp - C)).contiguous()
-        bo32, bog32 = f32(bo), f32(bog)
+        # the small float32 parameters (projection and output biases, both LayerNorm affines) in one
+        # buffer: one concatenation and one conversion instead of a launch per parameter
+        small = (("b4", (blv, blg, brv, brg), H), ("bo", (bo,), C), ("bog", (bog,), C), ("in_w", (in_w,), C),
+                 ("in_b", (in_b,), C), ("on_w", (on_w,), H), ("on_b", (on_b,), H))  # fmt: skip
+        pieces, spans, off = [], {}, 0
+        for name, tensors, n in small:
+            if all(t is None for t in tensors):
+                spans[name] = None
+                continue
+            for t in tensors:
+                pieces.append(torch.zeros(n, device=dev) if t is None else t.detach().resolve_neg().reshape(-1))
+            spans[name] = (off, off + n * len(tensors))
+            off += n * len(tensors)
+        buf = torch.cat(pieces).float()
+        view = lambda name: None if spans[name] is None else buf[spans[name][0] : spans[name][1]]  # noqa: E731
+        b_cat, bo32, bog32 = view("b4"), view("bo"), view("bog")
+        in_w32, in_b32, on_w32, on_b32 = view("in_w"), view("in_b"), view("on_w"), view("on_b")
+
+        def padded(w: Tensor, width: int) -> Tensor:
+            w = w.detach().resolve_neg()
+            return (F.pad(w, (0, width - w.shape[1])) if width != w.shape[1] else w).contiguous()
+
+        # projection weights concatenated and zero-padded to the 16-byte rows the kernels load
+        w_cat = padded(torch.cat([w.detach() for w in (wlv, wlg, wrv, wrg)]), cp)
+        wo_p, wog_p = padded(wo, hp), padded(wog, cp)
         mask32 = None if mask is None else mask.detach().resolve_neg().float().contiguous()
 
         with torch.cuda.device(dev):
@@ -380,13 +415,13 @@ class _TriangleMultiplication(torch.autograd.Function):
             d_xn = gg.mm(wog)  # (R, C)
             d_wo = _long_k_matmul(gv.t(), nrm[:, :H])
             d_wog = _long_k_matmul(gg.t(), xn[:, :C])
-            d_bo = gv.float().sum(0)
-            d_bog = gg.float().sum(0)
+            d_bo = gv.sum(0, dtype=torch.float32)
+            d_bog = gg.sum(0, dtype=torch.float32)
 
             d_comb = torch.empty(G, H, P, dtype=dtype, device=dev)
             parts = lib.oops_trimul_output_norm_parts(ctypes.byref(geo))
-            on_w_parts = torch.empty(parts, H, dtype=torch.float32, device=dev)
-            on_b_parts = torch.empty_like(on_w_parts)
+            on_parts = torch.empty(2, parts, H, dtype=torch.float32, device=dev)
+            on_w_parts, on_b_parts = on_parts[0], on_parts[1]
             _lib.check(lib.oops_trimul_output_norm_backward(ctypes.byref(geo), _ptr(combined), _ptr(on_w32),
                                                             _ptr(mean_out), _ptr(rstd_out), _ptr(d_nrm),
                                                             _ptr(d_comb), _ptr(on_w_parts), _ptr(on_b_parts),
@@ -405,13 +440,13 @@ class _TriangleMultiplication(torch.autograd.Function):
             w4 = w_cat[:, :C]
             d_xn = torch.addmm(d_xn, d_proj.t(), w4)
             d_w4 = _long_k_matmul(d_proj, xn[:, :C])  # (4H, C)
-            d_b4 = d_proj.float().sum(1)
+            d_b4 = d_proj.sum(1, dtype=torch.float32)
 
             d_x = torch.empty(G, P, C, dtype=dtype, device=dev)
             rg = _row_geometry(dtype, R, C, C, C, ctx.eps_in)
             rparts = lib.oops_layer_norm_rows_parts(ctypes.byref(rg))
-            in_w_parts = torch.empty(rparts, C, dtype=torch.float32, device=dev)
-            in_b_parts = torch.empty_like(in_w_parts)
+            in_parts = torch.empty(2, rparts, C, dtype=torch.float32, device=dev)
+            in_w_parts, in_b_parts = in_parts[0], in_parts[1]
             d_xn = d_xn.contiguous()
             _lib.check(lib.oops_layer_norm_rows_backward(ctypes.byref(rg), _ptr(x), _ptr(in_w32), _ptr(mean_in),
                                                          _ptr(rstd_in), _ptr(d_xn), _ptr(d_x), _ptr(in_w_parts),
@@ -423,12 +458,13 @@ class _TriangleMultiplication(torch.autograd.Function):
         def cast(i, g):
             return None if meta[i] is None or not needs[6 + i] else g.to(meta[i][0])
 
+        in_ab, on_ab = in_parts.sum(1), on_parts.sum(1)
         d_w4s = d_w4.split(H)
         d_b4s = d_b4.split(H)
         grads = [
-            cast(0, in_w_parts.sum(0)), cast(1, in_b_parts.sum(0)),
+            cast(0, in_ab[0]), cast(1, in_ab[1]),
             cast(2, d_w4s[0]), cast(3, d_w4s[1]), cast(4, d_w4s[2]), cast(5, d_w4s[3]),
-            cast(6, on_w_parts.sum(0)), cast(7, on_b_parts.sum(0)), cast(8, d_wo), cast(9, d_wog),
+            cast(6, on_ab[0]), cast(7, on_ab[1]), cast(8, d_wo), cast(9, d_wog),
             cast(10, d_b4s[0]), cast(11, d_b4s[1]), cast(12, d_b4s[2]), cast(13, d_b4s[3]),
             cast(14, d_bo), cast(15, d_bog),
         ]  # fmt: skip
