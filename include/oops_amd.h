@@ -200,7 +200,7 @@ int oops_gate_multiply_backward(const oops_gate_geometry* geo, const void* atten
  * `y_row` elements apart; the columns width..y_row-1 are written as zero, so a
  * padded y feeds 16-byte MFMA operand loads. */
 typedef struct oops_row_norm_geometry {
-  int32_t dtype; /* x and y */
+  int32_t dtype; /* x and y: OOPS_F32 / OOPS_BF16 / OOPS_F16 */
   int32_t width; /* 1..4096 */
   int64_t rows;
   int64_t x_row; /* x row stride in elements */

@@ -6,12 +6,14 @@ is the drop-in for ``from oops import ...`` on the attention path.
 
 from ._errors import OOpsUnsupportedError
 from .attention import gate_attention_output, gated_pair_bias_attention, pair_bias_attention, triangle_attention
+from .normalization import layer_norm
 from .pair import triangle_multiplication
 
 __all__ = [
     "OOpsUnsupportedError",
     "gate_attention_output",
     "gated_pair_bias_attention",
+    "layer_norm",
     "pair_bias_attention",
     "triangle_attention",
     "triangle_multiplication",

@@ -235,8 +235,8 @@ int check_gate(const oops_gate_geometry* g) {
 
 int check_row_norm(const oops_row_norm_geometry* g) {
   if (g == nullptr) return fail(OOPS_EINVAL, "row-norm geometry is NULL");
-  if (g->dtype != OOPS_BF16 && g->dtype != OOPS_F16)
-    return fail(OOPS_EINVAL, "row LayerNorm serves bfloat16 and float16 (dtype %lld)", g->dtype);
+  if (g->dtype != OOPS_BF16 && g->dtype != OOPS_F16 && g->dtype != OOPS_F32)
+    return fail(OOPS_EINVAL, "unknown dtype %lld", g->dtype);
   if (g->width <= 0 || g->width > 4096) return fail(OOPS_EINVAL, "width must be in 1..4096, got %lld", g->width);
   if (g->rows < 0) return fail(OOPS_EINVAL, "rows must be >= 0");
   if (g->x_row < g->width || g->y_row < g->width)

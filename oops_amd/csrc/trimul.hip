@@ -68,6 +68,26 @@ template <typename T>
 __device__ __forceinline__ uint4 pack8(const float (&x)[8]) {
   return make_uint4(pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3]), pack2<T>(x[4], x[5]), pack2<T>(x[6], x[7]));
 }
+// 8 consecutive elements of a 16-byte aligned run: one 16-byte access for 16-bit
+// types, two for float32
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float (&x)[8]) {
+  if constexpr (sizeof(T) == 4) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w, x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
+  } else {
+    unpack8<T>(*reinterpret_cast<const uint4*>(p), x);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const float (&x)[8]) {
+  if constexpr (sizeof(T) == 4) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(x[0], x[1], x[2], x[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(x[4], x[5], x[6], x[7]);
+  } else {
+    *reinterpret_cast<uint4*>(p) = pack8<T>(x);
+  }
+}
 
 // ------------------------------------------------------------------ row LayerNorm
 struct RowNormArgs {
@@ -94,7 +114,7 @@ __device__ __forceinline__ void load_chunks(const T* row, bool valid, int width,
     if constexpr (VEC) {
       // width % 8 == 0: a chunk is wholly inside or outside the row
       if (valid && col < width) {
-        unpack8<T>(*reinterpret_cast<const uint4*>(row + col), x[c]);
+        load8<T>(row + col, x[c]);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[c][e] = 0.f;
@@ -174,7 +194,7 @@ __global__ __launch_bounds__(256) void row_norm_forward_kernel(RowNormArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = col + e < W ? (x[c][e] - mean) * rstd * wv[c][e] + bv[c][e] : 0.f;
       if (VEC) {
-        *reinterpret_cast<uint4*>(yr + col) = pack8<T>(o);
+        store8<T>(yr + col, o);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e)
@@ -240,7 +260,7 @@ __global__ __launch_bounds__(256) void row_norm_backward_kernel(RowNormArgs a) {
       for (int e = 0; e < 8; ++e)
         o[e] = rstd * (g[c][e] * wv[c][e] - s1 - x[c][e] * s2);
       if (VEC) {
-        *reinterpret_cast<uint4*>(dxr + col) = pack8<T>(o);
+        store8<T>(dxr + col, o);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e)
@@ -514,7 +534,35 @@ struct OutNormArgs {
   float eps;
 };
 
-template <typename T>
+// VEC (P % 8 == 0, and for the backward H % 8 == 0): 16-byte global accesses,
+// 8 positions of one channel or 8 channels of one position per lane; else one
+// element per lane.
+template <typename T, bool VEC>
+__device__ __forceinline__ void stage_channel_major(const T* cg, int64_t P, int H, int np, int npb, int ld, float* sm) {
+  const int tid = threadIdx.x;
+  if constexpr (VEC) {
+    const int cpl = npb / 8;
+    for (int idx = tid; idx < H * cpl; idx += 256) {
+      const int h = idx / cpl, p = (idx - h * cpl) * 8;
+      float v[8];
+      if (p < np) {
+        unpack8<T>(*reinterpret_cast<const uint4*>(cg + (int64_t)h * P + p), v);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sm[h * ld + p + e] = v[e];
+    }
+  } else {
+    for (int idx = tid; idx < H * npb; idx += 256) {
+      const int h = idx / npb, p = idx - h * npb;
+      sm[h * ld + p] = p < np ? to_f(cg[(int64_t)h * P + p]) : 0.f;
+    }
+  }
+}
+
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void trimul_out_norm_forward_kernel(OutNormArgs a) {
   extern __shared__ float sm[];  // [H][npb + 1]
   __shared__ float red[256];
@@ -524,13 +572,10 @@ __global__ __launch_bounds__(256) void trimul_out_norm_forward_kernel(OutNormArg
   const int64_t P = a.positions;
   const int np = (int)(P - p0 < npb ? P - p0 : npb);
   const bool pv = pp < np;
-  const T* cg = static_cast<const T*>(a.comb) + g * H * P + p0;
+  stage_channel_major<T, VEC>(static_cast<const T*>(a.comb) + g * H * P + p0, P, H, np, npb, ld, sm);
+  __syncthreads();
   float s = 0.f;
-  for (int h = part; h < H; h += parts) {
-    const float v = pv ? to_f(cg[(int64_t)h * P + pp]) : 0.f;
-    sm[h * ld + pp] = v;
-    s += v;
-  }
+  for (int h = part; h < H; h += parts) s += sm[h * ld + pp];
   red[tid] = s;
   __syncthreads();
   float mean = 0.f;
@@ -557,17 +602,28 @@ __global__ __launch_bounds__(256) void trimul_out_norm_forward_kernel(OutNormArg
   // rows g*P + p0 .. + np - 1 are consecutive: write them as one run
   T* out = static_cast<T*>(a.nrm) + (g * P + p0) * a.h_row;
   const int hr = (int)a.h_row;
-  const int total = np * hr;
-  for (int e = tid; e < total; e += 256) {
-    const int i = e / hr, h = e - i * hr;
-    out[e] = h < H ? (T)sm[h * ld + i] : (T)0.f;
+  if constexpr (VEC) {
+    const int cpr = hr / 8;  // h_row is a multiple of 8
+    for (int idx = tid; idx < np * cpr; idx += 256) {
+      const int i = idx / cpr, h = (idx - i * cpr) * 8;
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = h + e < H ? sm[(h + e) * ld + i] : 0.f;
+      *reinterpret_cast<uint4*>(out + (int64_t)i * hr + h) = pack8<T>(o);
+    }
+  } else {
+    for (int e = tid; e < np * hr; e += 256) {
+      const int i = e / hr, h = e - i * hr;
+      out[e] = h < H ? (T)sm[h * ld + i] : (T)0.f;
+    }
   }
 }
 
-template <typename T>
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void trimul_out_norm_backward_kernel(OutNormArgs a) {
   extern __shared__ float sm[];  // x-hat [H][npb + 1], then grad [H][npb + 1]
   __shared__ float red[2][256];
+  __shared__ float stat[3][64];  // rstd, s1, s2 per position
   const int npb = a.npb, ld = npb + 1, parts = 256 / npb, H = a.H;
   float* xs = sm;
   float* gs = sm + H * ld;
@@ -578,37 +634,75 @@ __global__ __launch_bounds__(256) void trimul_out_norm_backward_kernel(OutNormAr
   const bool pv = pp < np;
   // grad rows [R][H] of this block's positions are consecutive
   const T* dn = static_cast<const T*>(a.dn) + (g * P + p0) * H;
-  for (int e = tid; e < npb * H; e += 256) {
-    const int i = e / H, h = e - i * H;
-    gs[h * ld + i] = i < np ? to_f(dn[e]) : 0.f;
+  if constexpr (VEC) {
+    const int cpr = H / 8;
+    for (int idx = tid; idx < npb * cpr; idx += 256) {
+      const int i = idx / cpr, h = (idx - i * cpr) * 8;
+      float v[8];
+      if (i < np) {
+        unpack8<T>(*reinterpret_cast<const uint4*>(dn + (int64_t)i * H + h), v);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) gs[(h + e) * ld + i] = v[e];
+    }
+  } else {
+    for (int e = tid; e < npb * H; e += 256) {
+      const int i = e / H, h = e - i * H;
+      gs[h * ld + i] = i < np ? to_f(dn[e]) : 0.f;
+    }
   }
-  const float mean = pv ? a.mean[g * P + p0 + pp] : 0.f;
-  const float rstd = pv ? a.rstd[g * P + p0 + pp] : 0.f;
-  const T* cg = static_cast<const T*>(a.comb) + g * H * P + p0;
-  for (int h = part; h < H; h += parts) xs[h * ld + pp] = pv ? (to_f(cg[(int64_t)h * P + pp]) - mean) * rstd : 0.f;
+  stage_channel_major<T, VEC>(static_cast<const T*>(a.comb) + g * H * P + p0, P, H, np, npb, ld, xs);
+  if (tid < npb) {
+    const bool v = tid < np;
+    stat[0][tid] = v ? a.rstd[g * P + p0 + tid] : 0.f;
+    red[0][tid] = v ? a.mean[g * P + p0 + tid] : 0.f;  // the mean, until the x-hat pass below
+  }
+  __syncthreads();
+  const float mean = red[0][pp], rstd = stat[0][pp];
   __syncthreads();
   float s1 = 0.f, s2 = 0.f;
   for (int h = part; h < H; h += parts) {
+    const float xh = (xs[h * ld + pp] - mean) * rstd;
+    xs[h * ld + pp] = pv ? xh : 0.f;
     const float wdy = gs[h * ld + pp] * (a.w ? a.w[h] : 1.f);
     s1 += wdy;
-    s2 += wdy * xs[h * ld + pp];
+    s2 += wdy * xh;
   }
   red[0][tid] = s1;
   red[1][tid] = s2;
   __syncthreads();
-  s1 = s2 = 0.f;
-  for (int j = 0; j < parts; ++j) {
-    s1 += red[0][j * npb + pp];
-    s2 += red[1][j * npb + pp];
+  if (tid < npb) {
+    float t1 = 0.f, t2 = 0.f;
+    for (int j = 0; j < parts; ++j) {
+      t1 += red[0][j * npb + tid];
+      t2 += red[1][j * npb + tid];
+    }
+    stat[1][tid] = t1 / (float)H;
+    stat[2][tid] = t2 / (float)H;
   }
-  s1 /= (float)H;
-  s2 /= (float)H;
+  __syncthreads();
   T* dc = static_cast<T*>(a.dcomb) + g * H * P + p0;
-  if (pv)
+  if constexpr (VEC) {
+    const int cpl = npb / 8;
+    for (int idx = tid; idx < H * cpl; idx += 256) {
+      const int h = idx / cpl, p = (idx - h * cpl) * 8;
+      if (p >= np) continue;
+      const float wh = a.w ? a.w[h] : 1.f;
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        o[e] = stat[0][p + e] * (gs[h * ld + p + e] * wh - stat[1][p + e] - xs[h * ld + p + e] * stat[2][p + e]);
+      *reinterpret_cast<uint4*>(dc + (int64_t)h * P + p) = pack8<T>(o);
+    }
+  } else if (pv) {
     for (int h = part; h < H; h += parts) {
       const float wdy = gs[h * ld + pp] * (a.w ? a.w[h] : 1.f);
-      dc[(int64_t)h * P + pp] = (T)(rstd * (wdy - s1 - xs[h * ld + pp] * s2));
+      dc[(int64_t)h * P + pp] = (T)(rstd * (wdy - stat[1][pp] - xs[h * ld + pp] * stat[2][pp]));
     }
+  }
   for (int h = tid; h < H; h += 256) {
     float sw = 0.f, sb = 0.f;
     for (int i = 0; i < np; ++i) {
@@ -867,6 +961,12 @@ hipError_t launch_rows(bool backward, bool vec, int blocks, const RowNormArgs& a
   return hipGetLastError();
 }
 
+template <typename F>
+hipError_t by_any(int dtype, F&& f) {
+  if (dtype == OOPS_F32) return f(float{});
+  return by_half(dtype, f);
+}
+
 hipError_t run_rows(const oops_row_norm_geometry& g, bool backward, RowNormArgs& a, const RowPlan& pl,
                     hipStream_t stream) {
   a.rows = g.rows;
@@ -876,7 +976,7 @@ hipError_t run_rows(const oops_row_norm_geometry& g, bool backward, RowNormArgs&
   a.lpr = pl.lpr;
   a.eps = g.eps;
   if (g.rows == 0) return hipSuccess;
-  return by_half(g.dtype, [&](auto tag) -> hipError_t {
+  return by_any(g.dtype, [&](auto tag) -> hipError_t {
     using T = decltype(tag);
     switch (pl.ch) {
       case 1: return launch_rows<T, 1>(backward, pl.vec, pl.blocks, a, stream);
@@ -966,12 +1066,18 @@ hipError_t run_out_norm(const oops_trimul_geometry& g, OutNormArgs& a, bool back
   const int64_t blocks = g.groups * a.pblocks;
   if (blocks == 0) return hipSuccess;
   const size_t lds = (size_t)(backward ? 2 : 1) * g.hidden * (a.npb + 1) * sizeof(float);
+  const bool vec = g.positions % 8 == 0 && a.npb >= 8 && (!backward || g.hidden % 8 == 0);
   return by_half(g.dtype, [&](auto tag) -> hipError_t {
     using T = decltype(tag);
-    if (backward)
-      hipLaunchKernelGGL((trimul_out_norm_backward_kernel<T>), dim3((unsigned)blocks), dim3(256), lds, stream, a);
+    const dim3 grid((unsigned)blocks);
+    if (backward && vec)
+      hipLaunchKernelGGL((trimul_out_norm_backward_kernel<T, true>), grid, dim3(256), lds, stream, a);
+    else if (backward)
+      hipLaunchKernelGGL((trimul_out_norm_backward_kernel<T, false>), grid, dim3(256), lds, stream, a);
+    else if (vec)
+      hipLaunchKernelGGL((trimul_out_norm_forward_kernel<T, true>), grid, dim3(256), lds, stream, a);
     else
-      hipLaunchKernelGGL((trimul_out_norm_forward_kernel<T>), dim3((unsigned)blocks), dim3(256), lds, stream, a);
+      hipLaunchKernelGGL((trimul_out_norm_forward_kernel<T, false>), grid, dim3(256), lds, stream, a);
     return hipGetLastError();
   });
 }

@@ -1,0 +1,169 @@
+"""``layer_norm``: LayerNorm over the last dimension on the HIP row kernels.
+
+Drop-in for the reference's operator
+(oops/normalization/layer_norm/layer_norm.py:30-148): dense or DanLing
+nested input whose normalized (final) axis is static and physically last,
+float16 / bfloat16 / float32 activations, optional affine parameters in the
+activation dtype (or float32 over half activations).  Forward and backward run
+in ``row_norm_*_kernel`` behind ``oops_layer_norm_rows_forward/backward``
+(float32 statistics, biased variance); the affine gradients are float32
+per-wave partials summed once and returned in the parameters' dtype.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Iterable, Optional, Union
+
+import torch
+from torch import Tensor
+
+from .. import _lib
+from .._errors import unsupported
+from ..attention._runtime import is_nested, require_no_forward_mode, require_same_device
+
+_OPERATOR = "layer_norm"
+_HALF = (torch.float16, torch.bfloat16)
+_DTYPE_CODE = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
+MAX_WIDTH = 4096
+
+
+def layer_norm(
+    input,
+    normalized_shape: Union[int, Iterable[int]],
+    weight: Optional[Tensor] = None,
+    bias: Optional[Tensor] = None,
+    eps: float = 1e-5,
+):
+    r"""Normalize the final feature dimension.
+
+    Args:
+        input: CUDA float16 / bfloat16 / float32 ``(..., C)`` tensor, or a
+            nested tensor whose final feature axis is static and physically last.
+        normalized_shape: ``C`` or ``(C,)`` with ``1 <= C <= 4096``.
+        weight, bias: optional ``(C,)`` affine parameters in the activation
+            dtype, or float32 for half activations.
+        eps: added to the variance before the reciprocal square root.
+
+    Returns the normalized values with the input's shape, dtype and topology.
+    """
+
+    if is_nested(input):
+        return _nested(input, normalized_shape, weight, bias, eps)
+    require_no_forward_mode(_OPERATOR, input, weight, bias)
+    require_same_device(_OPERATOR, input, weight, bias)
+    shape = (normalized_shape,) if isinstance(normalized_shape, int) else tuple(normalized_shape)
+    if len(shape) != 1:
+        raise unsupported(_OPERATOR, "normalizes over the final dimension only", normalized_shape=shape,
+                          input_shape=tuple(input.shape))  # fmt: skip
+    width = shape[0]
+    if torch.is_autocast_enabled("cuda") and input.dtype not in _HALF and any(
+        t is not None and t.is_floating_point() and t.dtype != input.dtype for t in (weight, bias)
+    ):
+        raise unsupported(_OPERATOR, "does not reimplement autocast promotion for a float32 activation with half "
+                          "affine", input_dtype=input.dtype)  # fmt: skip
+    affine_dtypes = {t.dtype for t in (weight, bias) if t is not None}
+    ok = (
+        input.is_cuda
+        and input.dtype in _DTYPE_CODE
+        and input.dim() >= 1
+        and input.shape[-1] == width
+        and 0 < width <= MAX_WIDTH
+        and input.numel() > 0
+        and all(t is None or tuple(t.shape) == (width,) for t in (weight, bias))
+        and len(affine_dtypes) <= 1
+        and affine_dtypes <= {input.dtype, torch.float32}
+        and (input.dtype in _HALF or affine_dtypes <= {torch.float32})
+    )
+    if not ok:
+        raise unsupported(
+            _OPERATOR,
+            "requires a CUDA half/float32 activation with a matching contiguous affine row",
+            input_dtype=input.dtype,
+            device=input.device,
+            normalized_size=width,
+            weight_dtype=None if weight is None else weight.dtype,
+            bias_dtype=None if bias is None else bias.dtype,
+        )
+    return _LayerNorm.apply(input, weight, bias, float(eps))
+
+
+def _nested(input, normalized_shape, weight, bias, eps):
+    """layer_norm.py:113-143: the packed values carry the static final axis."""
+
+    if is_nested(weight) or is_nested(bias):
+        raise ValueError("layer_norm NestedTensor input requires dense affine parameters")
+    if input.dim() < 2 or not input.ragged_dims:
+        raise unsupported(_OPERATOR, "requires a NestedTensor with explicit packed element topology",
+                          ragged_dims=input.ragged_dims)  # fmt: skip
+    last = input.dim() - 2
+    if last in tuple(input.ragged_dims) or tuple(input.packed_dim_order)[-1] != last:
+        raise unsupported(_OPERATOR, "requires the final logical element dimension to be static and physically last",
+                          ragged_dims=input.ragged_dims, packed_dim_order=input.packed_dim_order)  # fmt: skip
+    if input.concat.dim() < 1:
+        raise unsupported(_OPERATOR, "requires packed values with a retained static final dimension")
+    return input.packed_like(layer_norm(input.concat, normalized_shape, weight, bias, eps))
+
+
+def _geometry(dtype, rows: int, width: int, x_row: int, eps: float) -> _lib.RowNormGeometry:
+    g = _lib.RowNormGeometry()
+    g.dtype = _DTYPE_CODE[dtype]
+    g.width, g.rows, g.x_row, g.y_row, g.eps = width, rows, x_row, width, float(eps)
+    return g
+
+
+def _ptr(t: Optional[Tensor]) -> Optional[int]:
+    return None if t is None or t.numel() == 0 else t.data_ptr()
+
+
+class _LayerNorm(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, bias, eps):
+        lib = _lib.load()
+        width = x.shape[-1]
+        rows = x.numel() // width
+        x2 = x.resolve_neg().reshape(rows, width)
+        if x2.stride(1) != 1 or (rows > 1 and x2.stride(0) < width):
+            x2 = x2.contiguous()
+        f32 = lambda t: None if t is None else t.detach().resolve_neg().float().contiguous()  # noqa: E731
+        w32, b32 = f32(weight), f32(bias)
+        y = torch.empty(rows, width, dtype=x.dtype, device=x.device)
+        mean = torch.empty(rows, dtype=torch.float32, device=x.device)
+        rstd = torch.empty_like(mean)
+        geo = _geometry(x.dtype, rows, width, x2.stride(0) if rows > 1 else width, eps)
+        with torch.cuda.device(x.device):
+            rc = lib.oops_layer_norm_rows_forward(ctypes.byref(geo), _ptr(x2), _ptr(w32), _ptr(b32), _ptr(y),
+                                                  _ptr(mean), _ptr(rstd), torch.cuda.current_stream().cuda_stream)
+        _lib.check(rc, "layer_norm forward")
+        ctx.save_for_backward(x2, w32, mean, rstd)
+        ctx.eps = eps
+        ctx.shape = x.shape
+        ctx.dtypes = (None if weight is None else weight.dtype, None if bias is None else bias.dtype)
+        return y.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, dy):
+        lib = _lib.load()
+        x2, w32, mean, rstd = ctx.saved_tensors
+        rows, width = x2.shape
+        dy2 = dy.resolve_neg().to(x2.dtype).reshape(rows, width).contiguous()
+        dx = torch.empty(rows, width, dtype=x2.dtype, device=x2.device)
+        geo = _geometry(x2.dtype, rows, width, x2.stride(0) if rows > 1 else width, ctx.eps)
+        geo.y_row = width
+        parts = lib.oops_layer_norm_rows_parts(ctypes.byref(geo))
+        need_w, need_b = ctx.needs_input_grad[1], ctx.needs_input_grad[2]
+        acc = torch.empty(2, parts, width, dtype=torch.float32, device=x2.device) if need_w or need_b else None
+        # grad_x is written with x's row stride: give it x's layout when x is a row view
+        if x2.stride(0) != width and rows > 1:
+            dx = torch.empty_strided(x2.shape, x2.stride(), dtype=x2.dtype, device=x2.device)
+        with torch.cuda.device(x2.device):
+            rc = lib.oops_layer_norm_rows_backward(ctypes.byref(geo), _ptr(x2), _ptr(w32), _ptr(mean), _ptr(rstd),
+                                                   _ptr(dy2), _ptr(dx), None if acc is None else acc[0].data_ptr(),
+                                                   None if acc is None else acc[1].data_ptr(),
+                                                   torch.cuda.current_stream().cuda_stream)  # fmt: skip
+        _lib.check(rc, "layer_norm backward")
+        sums = acc.sum(1) if acc is not None else None
+        dw = sums[0].to(ctx.dtypes[0]) if need_w else None
+        db = sums[1].to(ctx.dtypes[1]) if need_b else None
+        return dx.reshape(ctx.shape), dw, db, None

@@ -1,0 +1,91 @@
+"""GPU parity of layer_norm against the float64 oracle (oracle/layer_norm.py).
+
+Follows the reference's layer_norm contract (oops/normalization/layer_norm/
+layer_norm.py:30-148): float16 / bfloat16 / float32 activations, widths from 1
+to 4096 (odd and non-multiple-of-8 widths take the element path), affine in
+the activation dtype, float32 over half, or absent; strided rows; nested
+values.  Values and the input gradient are compared elementwise; the affine
+gradients (sums over every row) with the tolerance scaled by their largest
+magnitude, as the reference's gradient checks do.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from accuracy import assert_close
+from nested_standin import NestedTensor
+from oops_amd import OOpsUnsupportedError, layer_norm
+from oracle import layer_norm as oln
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _np(t):
+    return None if t is None else t.detach().double().cpu().numpy()
+
+
+def _grad_close(got, want, dtype, what):
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    err = np.abs(_np(got) - want).max()
+    assert err <= tol * max(1.0, float(np.abs(want).max())), f"{what}: {err:.3g}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("width", [1, 17, 128, 384, 4096])
+@pytest.mark.parametrize("affine", ["same", "f32", "none"])
+def test_layer_norm(dtype, width, affine):
+    if affine == "f32" and dtype == torch.float32:
+        pytest.skip("same as 'same'")
+    g = torch.Generator().manual_seed(width)
+    rows = 3000 if width <= 384 else 200
+    x = (torch.randn(rows, width, generator=g) * 2 + 0.5).to(dtype).to(DEV).requires_grad_(True)
+    wdt = torch.float32 if affine == "f32" else dtype
+    w = b = None
+    if affine != "none":
+        w = torch.randn(width, generator=g).to(wdt).to(DEV).requires_grad_(True)
+        b = torch.randn(width, generator=g).to(wdt).to(DEV).requires_grad_(True)
+    y = layer_norm(x, width, w, b)
+    assert y.shape == x.shape and y.dtype == dtype
+    assert_close(y, oln.layer_norm_forward(_np(x), _np(w), _np(b)), dtype, "y")
+    dy = torch.randn(rows, width, generator=g).to(dtype).to(DEV)
+    leaves = [x] + ([w, b] if w is not None else [])
+    got = torch.autograd.grad(y, leaves, dy)
+    dx, dw, db = oln.layer_norm_backward(_np(x), _np(dy), _np(w))
+    assert_close(got[0], dx, dtype, "dx")
+    if w is not None:
+        assert got[1].dtype == wdt and got[2].dtype == wdt
+        _grad_close(got[1], dw, dtype, "dweight")
+        _grad_close(got[2], db, dtype, "dbias")
+
+
+def test_layer_norm_strided_and_prefix():
+    g = torch.Generator().manual_seed(2)
+    base = torch.randn(4, 50, 96, generator=g).to(torch.bfloat16).to(DEV)
+    x = base[:, :, :64].requires_grad_(False)  # rows 96 elements apart
+    w = torch.randn(64, generator=g).to(DEV)
+    y = layer_norm(x, (64,), w, None)
+    assert_close(y, oln.layer_norm_forward(_np(x), _np(w)), torch.bfloat16, "y")
+
+
+def test_layer_norm_nested():
+    tmpl = NestedTensor([torch.empty(n, 3, 32) for n in (5, 9)], ragged_dims=(0,))
+    g = torch.Generator().manual_seed(4)
+    vals = torch.randn(tmpl.concat.shape, generator=g).to(torch.bfloat16).to(DEV)
+    out = layer_norm(tmpl.packed_like(vals), 32)
+    assert isinstance(out, NestedTensor)
+    assert_close(out.concat, oln.layer_norm_forward(_np(vals)), torch.bfloat16, "nested")
+
+
+def test_layer_norm_errors():
+    x = torch.randn(4, 8, device=DEV)
+    with pytest.raises(OOpsUnsupportedError):
+        layer_norm(x, (2, 4))
+    with pytest.raises(OOpsUnsupportedError):
+        layer_norm(x.double(), 8)
+    with pytest.raises(OOpsUnsupportedError):
+        layer_norm(x, 8, torch.ones(8, device=DEV, dtype=torch.bfloat16))  # half affine over float32
+    with pytest.raises(OOpsUnsupportedError):
+        layer_norm(torch.randn(4, 5000, device=DEV), 5000)

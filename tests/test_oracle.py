@@ -359,3 +359,21 @@ def test_trimul_finite_differences():
             xm[idx] -= eps
             fd = (fn(xp) - fn(xm)) / (2 * eps)
             assert abs(fd - grad[idx]) < 1e-5 * max(1.0, abs(fd)), (name, idx, fd, grad[idx])
+
+
+# ------------------------------------------------------------------ layer_norm
+
+from oracle import layer_norm as oln  # noqa: E402
+
+
+@pytest.mark.parametrize("width", [1, 7, 64])
+def test_layer_norm_vs_torch(width):
+    g = np.random.default_rng(width)
+    x = g.standard_normal((3, 5, width)) * 3 + 1
+    w, b, dy = g.standard_normal(width), g.standard_normal(width), g.standard_normal((3, 5, width))
+    tx, tw, tb = (torch.tensor(a, requires_grad=True) for a in (x, w, b))
+    out = F.layer_norm(tx, (width,), tw, tb, 1e-5)
+    np.testing.assert_allclose(oln.layer_norm_forward(x, w, b), out.detach().numpy(), rtol=1e-12, atol=1e-12)
+    got = oln.layer_norm_backward(x, dy, w)
+    for mine, ref in zip(got, torch.autograd.grad(out, (tx, tw, tb), torch.tensor(dy))):
+        np.testing.assert_allclose(mine, ref.numpy(), rtol=1e-10, atol=1e-10)
