@@ -255,12 +255,16 @@ int oops_trimul_factors_forward(const oops_trimul_geometry* geo, const void* nor
                                 const float* bias, const void* mask, void* factors, void* stream);
 /* Rows of float32 mask-gradient partials the factor backward writes (sum them). */
 size_t oops_trimul_mask_parts(const oops_trimul_geometry* geo);
+/* Rows of float32 projection-bias-gradient partials the factor backward writes. */
+size_t oops_trimul_bias_parts(const oops_trimul_geometry* geo);
 /* Recomputes the projections and writes grad_projection [4H][R] (value and
- * gate logit gradients, W's row order) and, with a mask, mask-gradient
- * partials [parts][R] (NULL to skip). */
+ * gate logit gradients, W's row order), with a mask the mask-gradient
+ * partials [mask_parts][R], and the projection-bias-gradient partials
+ * [bias_parts][4H] (either partial pointer NULL to skip). */
 int oops_trimul_factors_backward(const oops_trimul_geometry* geo, const void* normalized, const void* weight,
                                  const float* bias, const void* mask, const void* grad_factors,
-                                 void* grad_projection, float* grad_mask_parts, void* stream);
+                                 void* grad_projection, float* grad_mask_parts, float* grad_bias_parts,
+                                 void* stream);
 /* LayerNorm over H of combined[g][:][p] -> normalized rows [R][h_row]; mean, rstd [R]. */
 int oops_trimul_output_norm_forward(const oops_trimul_geometry* geo, const void* combined, const float* weight,
                                     const float* bias, void* normalized, float* mean, float* rstd, void* stream);

@@ -18,7 +18,7 @@ F32, BF16, F16 = 0, 1, 2
 BIAS_NONE, BIAS_FULL, BIAS_SHARED = 0, 1, 2
 PHASE_DELTA, PHASE_DQ, PHASE_DKV, PHASE_DBIAS = 1, 2, 4, 8
 TABLE_WIDTH = 40
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # geometry table columns (enum oops_table_column)
 (
@@ -48,6 +48,7 @@ EXPORTED_SYMBOLS = (
     "oops_layer_norm_rows_backward",
     "oops_trimul_factors_forward",
     "oops_trimul_mask_parts",
+    "oops_trimul_bias_parts",
     "oops_trimul_factors_backward",
     "oops_trimul_output_norm_forward",
     "oops_trimul_output_norm_parts",
@@ -172,7 +173,9 @@ def load() -> ctypes.CDLL:
         lib.oops_trimul_factors_forward.restype = i32
         lib.oops_trimul_mask_parts.argtypes = [tg]
         lib.oops_trimul_mask_parts.restype = sz
-        lib.oops_trimul_factors_backward.argtypes = [tg, vp, vp, vp, vp, vp, vp, vp, vp]
+        lib.oops_trimul_bias_parts.argtypes = [tg]
+        lib.oops_trimul_bias_parts.restype = sz
+        lib.oops_trimul_factors_backward.argtypes = [tg, vp, vp, vp, vp, vp, vp, vp, vp, vp]
         lib.oops_trimul_factors_backward.restype = i32
         lib.oops_trimul_output_norm_forward.argtypes = [tg, vp, vp, vp, vp, vp, vp, vp]
         lib.oops_trimul_output_norm_forward.restype = i32

@@ -271,7 +271,7 @@ int gate_launch_result(hipError_t err, const char* what) {
 
 extern "C" {
 
-int oops_abi_version(void) { return 4; }
+int oops_abi_version(void) { return 5; }
 
 const char* oops_last_error(void) { return g_last_error.c_str(); }
 
@@ -406,7 +406,7 @@ int oops_trimul_factors_forward(const oops_trimul_geometry* geo, const void* nor
   if (!aligned16(normalized) || !aligned16(weight) || !aligned16(factors) || (geo->has_mask && !aligned16(mask)))
     return fail(OOPS_EINVAL, "normalized, weight, mask and factors must be 16-byte aligned");
   return gate_launch_result(oops::launch_trimul_factors(*geo, normalized, weight, bias, mask, factors, nullptr,
-                                                        nullptr, nullptr, static_cast<hipStream_t>(stream)),
+                                                        nullptr, nullptr, nullptr, static_cast<hipStream_t>(stream)),
                             "triangle multiplication factors");
 }
 
@@ -415,9 +415,15 @@ size_t oops_trimul_mask_parts(const oops_trimul_geometry* geo) {
   return (size_t)oops::trimul_mask_parts(*geo);
 }
 
+size_t oops_trimul_bias_parts(const oops_trimul_geometry* geo) {
+  if (check_trimul(geo)) return 0;
+  return (size_t)oops::trimul_bias_parts(*geo);
+}
+
 int oops_trimul_factors_backward(const oops_trimul_geometry* geo, const void* normalized, const void* weight,
                                  const float* bias, const void* mask, const void* grad_factors,
-                                 void* grad_projection, float* grad_mask_parts, void* stream) {
+                                 void* grad_projection, float* grad_mask_parts, float* grad_bias_parts,
+                                 void* stream) {
   g_last_error.clear();
   if (int rc = check_trimul(geo)) return rc;
   if (!normalized || !weight || !grad_factors || !grad_projection)
@@ -427,7 +433,7 @@ int oops_trimul_factors_backward(const oops_trimul_geometry* geo, const void* no
       (geo->has_mask && !aligned16(mask)))
     return fail(OOPS_EINVAL, "operands must be 16-byte aligned");
   return gate_launch_result(oops::launch_trimul_factors(*geo, normalized, weight, bias, mask, nullptr, grad_factors,
-                                                        grad_projection, grad_mask_parts,
+                                                        grad_projection, grad_mask_parts, grad_bias_parts,
                                                         static_cast<hipStream_t>(stream)),
                             "triangle multiplication factor backward");
 }

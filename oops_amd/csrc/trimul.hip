@@ -33,6 +33,7 @@
 // with W_og) into separate accumulators, the product in the epilogue, and a
 // v_permlane32_swap so each lane stores 16 consecutive channels of its token.
 // The backward recomputes both projections and writes the two gradients.
+#include <algorithm>
 #include <type_traits>
 
 #include "attn_fast_common.h"
@@ -302,12 +303,14 @@ struct FactorArgs {
   const void* grad_factors;
   void* grad_proj;
   float* mask_parts;
+  float* bias_parts;  // backward: [token groups][4H] sums of the value / gate-logit gradients
   int64_t rows, positions, groups, c_row, tiles;
-  int H, cblocks;
+  int H, cblocks, tpw;
 };
 
-constexpr int kFM = 128;  // tokens per workgroup (32 per wave)
-constexpr int kFK = 64;   // k per step
+constexpr int kFM = 128;  // tokens per tile (32 per wave)
+constexpr int kFK = 64;   // k per panel / step
+constexpr int kFullWMaxK = 256;  // the whole W block stays in LDS up to this c_row
 
 template <typename T>
 __device__ __forceinline__ void load4(const T* p, bool vec, int64_t left, float (&x)[4]) {
@@ -320,12 +323,18 @@ __device__ __forceinline__ void load4(const T* p, bool vec, int64_t left, float 
   }
 }
 
-template <typename T, bool BWD>
+// One workgroup = one (factor, 64-channel block) and TPW consecutive tiles of
+// 128 tokens.  FULLW (c_row <= 256): the block's 128 W rows (64 value, 64
+// gate) x c_row are loaded into LDS once, as 64-wide swizzled panels, and
+// every token tile reuses them with no further barrier; otherwise W streams
+// through a two-buffer LDS tile per tile (TPW = 1).
+template <typename T, bool BWD, bool FULLW>
 __global__ __launch_bounds__(256) void trimul_factor_kernel(FactorArgs a) {
   using E = Elem<T>;
   using Frag = typename E::Frag;
-  constexpr int WT = 128 * kFK;
-  __shared__ __attribute__((aligned(16))) T w_lds[2 * WT];
+  constexpr int WT = 128 * kFK;  // one panel: 128 rows x 64 k
+  extern __shared__ __attribute__((aligned(16))) char lds_raw[];
+  T* w_lds = reinterpret_cast<T*>(lds_raw);
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63, lq = lane & 31, g2 = lane >> 5;
@@ -334,36 +343,25 @@ __global__ __launch_bounds__(256) void trimul_factor_kernel(FactorArgs a) {
   const int nb = 2 * a.cblocks;
   const int fc = (int)(tile % nb);
   const int f = fc / a.cblocks, cb = fc - f * a.cblocks;
-  const int64_t r0 = (tile / nb) * kFM;
+  const int64_t bmg = tile / nb;
   const int H = a.H;
   const int K = (int)a.c_row;
+  const int64_t P = a.positions, R = a.rows;
 
-  // this lane's token rows as the MFMA A operand (8 k per lane and chunk)
-  const int64_t rows_left = a.rows - r0;
-  const int nrows = (int)(rows_left < kFM ? rows_left : kFM);
-  const __amdgpu_buffer_rsrc_t xr =
-      make_rsrc(static_cast<const T*>(a.xn) + r0 * a.c_row, (uint32_t)((int64_t)nrows * a.c_row * 2));
-  const bool rv = wave * 32 + lq < nrows;
-  const uint32_t x_lane = (uint32_t)((wave * 32 + lq) * a.c_row * 2);
-  auto load_x = [&](int k0, uint4 (&xf)[4]) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int k = k0 + 16 * c + 8 * g2;
-      xf[c] = buffer_load16(xr, rv && k < K ? x_lane + (uint32_t)(k * 2) : kOut);
-    }
-  };
   // W rows: 0..63 value channels, 64..127 gate channels of block cb, factor f
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, (uint32_t)((int64_t)4 * H * a.c_row * 2));
+  auto w_row_off = [&](int row) -> int64_t {
+    const int hv = cb * 64 + (row & 63);
+    return hv < H ? (int64_t)(f * 2 * H + (row >= 64 ? H : 0) + hv) * a.c_row * 2 : -1;
+  };
   uint32_t w_off[4];
   bool w_ok[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int id = tid + 256 * j;
-    const int row = id >> 3, ch = id & 7;
-    const int hv = cb * 64 + (row & 63);
-    const int wrow = f * 2 * H + (row >= 64 ? H : 0) + hv;
-    w_ok[j] = hv < H;
-    w_off[j] = (uint32_t)((int64_t)wrow * a.c_row * 2 + ch * 16);
+    const int64_t o = w_row_off(id >> 3);
+    w_ok[j] = o >= 0;
+    w_off[j] = (uint32_t)((o >= 0 ? o : 0) + (id & 7) * 16);
   }
   auto load_w = [&](int k0, uint4 (&wu)[4]) {
 #pragma unroll
@@ -372,148 +370,251 @@ __global__ __launch_bounds__(256) void trimul_factor_kernel(FactorArgs a) {
       wu[j] = buffer_load16(wr, w_ok[j] && k0 + ch * 8 < K ? w_off[j] + (uint32_t)(k0 * 2) : kOut);
     }
   };
-  auto store_w = [&](int buf, const uint4 (&wu)[4]) {
+  auto store_w = [&](int panel, const uint4 (&wu)[4]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int id = tid + 256 * j;
-      *reinterpret_cast<uint4*>(&w_lds[buf * WT + swz_off<kFK>(id >> 3, (id & 7) * 8)]) = wu[j];
+      *reinterpret_cast<uint4*>(&w_lds[panel * WT + swz_off<kFK>(id >> 3, (id & 7) * 8)]) = wu[j];
     }
   };
-
-  f32x16 acc[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) acc[t] = f32x16{};
-  const int nsteps = (K + kFK - 1) / kFK;
-  uint4 xf[4], xn[4], wu[4];
-  load_w(0, wu);
-  load_x(0, xf);
-  store_w(0, wu);
-  __syncthreads();
-  for (int i = 0; i < nsteps; ++i) {
-    const int buf = i & 1;
-    const bool more = i + 1 < nsteps;
-    if (more) {
-      load_w((i + 1) * kFK, wu);
-      load_x((i + 1) * kFK, xn);
+  const int npanels = (K + kFK - 1) / kFK;
+  if constexpr (FULLW) {
+    for (int p = 0; p < npanels; ++p) {
+      uint4 wu[4];
+      load_w(p * kFK, wu);
+      store_w(p, wu);
     }
-    const T* wt = &w_lds[buf * WT];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const Frag afr = __builtin_bit_cast(Frag, xf[c]);
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        acc[t] = E::mma(afr, lds_frag<T>(wt + swz_off<kFK>(32 * t + lq, 16 * c + 8 * g2)), acc[t]);
-    }
-    if (more) store_w(buf ^ 1, wu);
-    lds_barrier();
-#pragma unroll
-    for (int c = 0; c < 4; ++c) xf[c] = xn[c];
+    __syncthreads();
   }
 
-  // ---- epilogue: tile t in {0, 1} holds value channel cb*64 + 32t + lq (tile t+2 its gate)
-  // for tokens r0 + 32 wave + 8q + 4 g2 + i
-  const int64_t P = a.positions, R = a.rows;
-  const bool vec4 = (P & 3) == 0;  // 4 tokens from a multiple of 4 share a group, 8-byte aligned
-  const float* mask = a.mask;
-  float mp[16];
+  float bsum[2][2] = {{0.f, 0.f}, {0.f, 0.f}};  // [t][value, gate] over this lane's tokens
+  const int tpw = FULLW ? a.tpw : 1;
+  for (int it = 0; it < tpw; ++it) {
+    const int64_t r0 = (bmg * tpw + it) * kFM;
+    if (r0 >= R) break;
+    const int64_t rows_left = R - r0;
+    const int nrows = (int)(rows_left < kFM ? rows_left : kFM);
+    const __amdgpu_buffer_rsrc_t xr =
+        make_rsrc(static_cast<const T*>(a.xn) + r0 * a.c_row, (uint32_t)((int64_t)nrows * a.c_row * 2));
+    const bool rv = wave * 32 + lq < nrows;
+    const uint32_t x_lane = (uint32_t)((wave * 32 + lq) * a.c_row * 2);
+    auto load_x = [&](int k0, uint4 (&xf)[4]) {
 #pragma unroll
-  for (int v = 0; v < 16; ++v) mp[v] = 0.f;
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int hv = cb * 64 + 32 * t + lq;
-    if (hv >= H) continue;
-    const float bv = a.bias ? a.bias[f * 2 * H + hv] : 0.f;
-    const float bg = a.bias ? a.bias[f * 2 * H + H + hv] : 0.f;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int64_t r4 = r0 + wave * 32 + 8 * q + 4 * g2;
-      if (r4 >= R) continue;
-      const int64_t left = R - r4;
-      float keep[4] = {1.f, 1.f, 1.f, 1.f};
-      if (mask) {
-        if (vec4) {
-          const float4 m4 = *reinterpret_cast<const float4*>(mask + r4);
-          keep[0] = m4.x, keep[1] = m4.y, keep[2] = m4.z, keep[3] = m4.w;
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) keep[i] = i < left ? mask[r4 + i] : 0.f;
-        }
+      for (int c = 0; c < 4; ++c) {
+        const int k = k0 + 16 * c + 8 * g2;
+        xf[c] = buffer_load16(xr, rv && k < K ? x_lane + (uint32_t)(k * 2) : kOut);
       }
-      float v[4], s[4];
+    };
+
+    f32x16 acc[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[i] = acc[t][4 * q + i] + bv;
-        s[i] = sigmoid_f(acc[t + 2][4 * q + i] + bg);
+    for (int t = 0; t < 4; ++t) acc[t] = f32x16{};
+    uint4 xf[4], xn[4], wu[4];
+    if constexpr (!FULLW) {
+      load_w(0, wu);
+      store_w(0, wu);
+    }
+    load_x(0, xf);
+    if constexpr (!FULLW) __syncthreads();
+    for (int i = 0; i < npanels; ++i) {
+      const bool more = i + 1 < npanels;
+      if (more) {
+        if constexpr (!FULLW) load_w((i + 1) * kFK, wu);
+        load_x((i + 1) * kFK, xn);
       }
-      if constexpr (!BWD) {
-        T* out = static_cast<T*>(a.factors);
-        if (vec4) {
-          const int64_t g = r4 / P, p = r4 - g * P;
-          const int64_t off = ((f * a.groups + g) * H + hv) * P + p;
-          *reinterpret_cast<uint2*>(out + off) =
-              make_uint2(pack2<T>(v[0] * s[0] * keep[0], v[1] * s[1] * keep[1]),
-                         pack2<T>(v[2] * s[2] * keep[2], v[3] * s[3] * keep[3]));
-        } else {
+      const T* wt = &w_lds[(FULLW ? i : (i & 1)) * WT];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            if (i >= left) break;
-            const int64_t g = (r4 + i) / P, p = r4 + i - g * P;
-            out[((f * a.groups + g) * H + hv) * P + p] = (T)(v[i] * s[i] * keep[i]);
-          }
-        }
-      } else {
+      for (int c = 0; c < 4; ++c) {
+        const Frag afr = __builtin_bit_cast(Frag, xf[c]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          acc[t] = E::mma(afr, lds_frag<T>(wt + swz_off<kFK>(32 * t + lq, 16 * c + 8 * g2)), acc[t]);
+      }
+      if constexpr (!FULLW) {
+        if (more) store_w((i & 1) ^ 1, wu);
+        lds_barrier();
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) xf[c] = xn[c];
+    }
+
+    // ---- epilogue: tile t in {0, 1} holds value channel cb*64 + 32t + lq (tile t+2 its gate)
+    // for tokens r0 + 32 wave + 8q + 4 g2 + i
+    const bool vec4 = (P & 3) == 0;  // 4 tokens from a multiple of 4 share a group, 8-byte aligned
+    const float* mask = a.mask;
+    // (group, position) of this lane's first token r0 + 32 wave + 4 g2 (one 64-bit division per
+    // tile); the tokens 8q further on step forward from it
+    int64_t g_q[4], p_q[4];
+    {
+      const int64_t rb = r0 + wave * 32 + 4 * g2;
+      int64_t g = rb / P, p = rb - g * P;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        g_q[q] = g;
+        p_q[q] = p;
+        p += 8;
+        while (p >= P) p -= P, ++g;
+      }
+    }
+    // every load of the epilogue is issued before its first store (a store could alias a later
+    // load, so loads interleaved with stores would each wait a full memory round trip)
+    float4 keep4[4];
+    uint2 dpre[2][4];
+    if (vec4) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t r4 = r0 + wave * 32 + 8 * q + 4 * g2;
+        keep4[q] = mask && r4 < R ? *reinterpret_cast<const float4*>(mask + r4) : make_float4(1.f, 1.f, 1.f, 1.f);
+      }
+      if constexpr (BWD) {
         const T* gf = static_cast<const T*>(a.grad_factors);
-        float d[4];
-        if (vec4) {
-          const int64_t g = r4 / P, p = r4 - g * P;
-          load4<T>(gf + ((f * a.groups + g) * H + hv) * P + p, true, left, d);
-        } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            d[i] = 0.f;
-            if (i < left) {
-              const int64_t g = (r4 + i) / P, p = r4 + i - g * P;
-              d[i] = to_f(gf[((f * a.groups + g) * H + hv) * P + p]);
-            }
+        for (int t = 0; t < 2; ++t) {
+          const int hv = cb * 64 + 32 * t + lq;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int64_t r4 = r0 + wave * 32 + 8 * q + 4 * g2;
+            dpre[t][q] = hv < H && r4 < R
+                             ? *reinterpret_cast<const uint2*>(gf + ((f * a.groups + g_q[q]) * H + hv) * P + p_q[q])
+                             : make_uint2(0, 0);
           }
         }
-        float dv[4], dg[4];
+      }
+    }
+    float bvs[2], bgs[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int hv = min(cb * 64 + 32 * t + lq, H - 1);
+      bvs[t] = a.bias ? a.bias[f * 2 * H + hv] : 0.f;
+      bgs[t] = a.bias ? a.bias[f * 2 * H + H + hv] : 0.f;
+    }
+    float mp[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) mp[v] = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int hv = cb * 64 + 32 * t + lq;
+      if (hv >= H) continue;
+      const float bv = bvs[t], bg = bgs[t];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t r4 = r0 + wave * 32 + 8 * q + 4 * g2;
+        if (r4 >= R) continue;
+        const int64_t left = R - r4;
+        float keep[4] = {1.f, 1.f, 1.f, 1.f};
+        if (vec4) {
+          keep[0] = keep4[q].x, keep[1] = keep4[q].y, keep[2] = keep4[q].z, keep[3] = keep4[q].w;
+        } else if (mask) {
+          {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) keep[i] = i < left ? mask[r4 + i] : 0.f;
+          }
+        }
+        float v[4], sg[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          dv[i] = d[i] * keep[i] * s[i];
-          dg[i] = d[i] * keep[i] * v[i] * s[i] * (1.f - s[i]);
-          mp[4 * q + i] += d[i] * v[i] * s[i];
+          v[i] = acc[t][4 * q + i] + bv;
+          sg[i] = sigmoid_f(acc[t + 2][4 * q + i] + bg);
         }
-        T* gp = static_cast<T*>(a.grad_proj);
-        T* gv = gp + (int64_t)(f * 2 * H + hv) * R + r4;
-        T* gg = gp + (int64_t)(f * 2 * H + H + hv) * R + r4;
-        if (vec4) {
-          *reinterpret_cast<uint2*>(gv) = make_uint2(pack2<T>(dv[0], dv[1]), pack2<T>(dv[2], dv[3]));
-          *reinterpret_cast<uint2*>(gg) = make_uint2(pack2<T>(dg[0], dg[1]), pack2<T>(dg[2], dg[3]));
-        } else {
+        if constexpr (!BWD) {
+          T* out = static_cast<T*>(a.factors);
+          if (vec4) {
+            const int64_t off = ((f * a.groups + g_q[q]) * H + hv) * P + p_q[q];
+            *reinterpret_cast<uint2*>(out + off) =
+                make_uint2(pack2<T>(v[0] * sg[0] * keep[0], v[1] * sg[1] * keep[1]),
+                           pack2<T>(v[2] * sg[2] * keep[2], v[3] * sg[3] * keep[3]));
+          } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (i < left) {
-              gv[i] = (T)dv[i];
-              gg[i] = (T)dg[i];
+            for (int i = 0; i < 4; ++i) {
+              if (i >= left) break;
+              const int64_t g = (r4 + i) / P, p = r4 + i - g * P;
+              out[((f * a.groups + g) * H + hv) * P + p] = (T)(v[i] * sg[i] * keep[i]);
             }
+          }
+        } else {
+          const T* gf = static_cast<const T*>(a.grad_factors);
+          float d[4];
+          if (vec4) {
+            const uint2 u = dpre[t][q];
+            d[0] = lo_f<T>(u.x), d[1] = hi_f<T>(u.x), d[2] = lo_f<T>(u.y), d[3] = hi_f<T>(u.y);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              d[i] = 0.f;
+              if (i < left) {
+                const int64_t g = (r4 + i) / P, p = r4 + i - g * P;
+                d[i] = to_f(gf[((f * a.groups + g) * H + hv) * P + p]);
+              }
+            }
+          }
+          float dv[4], dg[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            dv[i] = d[i] * keep[i] * sg[i];
+            dg[i] = d[i] * keep[i] * v[i] * sg[i] * (1.f - sg[i]);
+            mp[4 * q + i] += d[i] * v[i] * sg[i];
+          }
+          T* gp = static_cast<T*>(a.grad_proj);
+          T* gv = gp + (int64_t)(f * 2 * H + hv) * R + r4;
+          T* gg = gp + (int64_t)(f * 2 * H + H + hv) * R + r4;
+          if (vec4) {
+            const uint2 uv = make_uint2(pack2<T>(dv[0], dv[1]), pack2<T>(dv[2], dv[3]));
+            const uint2 ug = make_uint2(pack2<T>(dg[0], dg[1]), pack2<T>(dg[2], dg[3]));
+            *reinterpret_cast<uint2*>(gv) = uv;
+            *reinterpret_cast<uint2*>(gg) = ug;
+            // the bias gradient sums the stored (rounded) values, as a reduction of grad_proj would
+            bsum[t][0] += lo_f<T>(uv.x) + hi_f<T>(uv.x) + lo_f<T>(uv.y) + hi_f<T>(uv.y);
+            bsum[t][1] += lo_f<T>(ug.x) + hi_f<T>(ug.x) + lo_f<T>(ug.y) + hi_f<T>(ug.y);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (i < left) {
+                const T tv = (T)dv[i], tg = (T)dg[i];
+                gv[i] = tv;
+                gg[i] = tg;
+                bsum[t][0] += to_f(tv);
+                bsum[t][1] += to_f(tg);
+              }
+          }
         }
       }
     }
+    if constexpr (BWD) {
+      if (a.mask_parts != nullptr) {
+        // sum over the 32 channels of the half-wave (lanes of one g2 share tokens)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          for (int o = 1; o < 32; o <<= 1) mp[v] += __shfl_xor(mp[v], o);
+        float val = 0.f;
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          if (v == lq) val = mp[v];
+        const int64_t r = r0 + wave * 32 + 8 * (lq >> 2) + 4 * g2 + (lq & 3);
+        if (lq < 16 && r < R) a.mask_parts[(int64_t)(f * a.cblocks + cb) * R + r] = val;
+      }
+    }
   }
+
   if constexpr (BWD) {
-    if (a.mask_parts == nullptr) return;
-    // sum over the 32 channels of the half-wave (lanes of one g2 share tokens)
+    if (a.bias_parts == nullptr) return;
+    // channel sums: the two half-waves, then the four waves through LDS
+    __shared__ float bred[4][2][2][32];
 #pragma unroll
-    for (int v = 0; v < 16; ++v)
-      for (int o = 1; o < 32; o <<= 1) mp[v] += __shfl_xor(mp[v], o);
-    if (lq >= 16) return;
-    float val = 0.f;
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int v = 0; v < 16; ++v)
-      if (v == lq) val = mp[v];
-    const int64_t r = r0 + wave * 32 + 8 * (lq >> 2) + 4 * g2 + (lq & 3);
-    if (r < R) a.mask_parts[(int64_t)(f * a.cblocks + cb) * R + r] = val;
+      for (int k = 0; k < 2; ++k) {
+        bsum[t][k] += __shfl_xor(bsum[t][k], 32);
+        if (g2 == 0) bred[wave][t][k][lq] = bsum[t][k];
+      }
+    __syncthreads();
+    if (tid < 128) {
+      const int t = tid >> 6, k = (tid >> 5) & 1, c = tid & 31;
+      const int hv = cb * 64 + 32 * t + c;
+      if (hv < H) {
+        const float sum = bred[0][t][k][c] + bred[1][t][k][c] + bred[2][t][k][c] + bred[3][t][k][c];
+        a.bias_parts[bmg * 4 * H + f * 2 * H + k * H + hv] = sum;
+      }
+    }
   }
 }
 
@@ -1018,27 +1119,59 @@ int64_t factor_cblocks(const oops_trimul_geometry& g) { return (g.hidden + 63) /
 
 int64_t trimul_mask_parts(const oops_trimul_geometry& g) { return 2 * factor_cblocks(g); }
 
+namespace {
+struct FactorPlan {
+  bool fullw;
+  int tpw;
+  int64_t groups, tiles;
+  size_t lds;
+};
+FactorPlan factor_plan(const oops_trimul_geometry& g, bool backward) {
+  const int64_t cblocks = factor_cblocks(g);
+  const int64_t token_tiles = (g.groups * g.positions + kFM - 1) / kFM;
+  FactorPlan pl{};
+  // the backward's epilogue holds more live values: the streaming form keeps it under 256 VGPRs
+  pl.fullw = g.c_row <= kFullWMaxK && !backward;
+  // about 2048 workgroups: each keeps its W block across several token tiles
+  pl.tpw = pl.fullw ? (int)std::max<int64_t>(1, (token_tiles * 2 * cblocks + 2047) / 2048) : 1;
+  pl.groups = (token_tiles + pl.tpw - 1) / pl.tpw;
+  pl.tiles = pl.groups * 2 * cblocks;
+  const int64_t panels = (g.c_row + kFK - 1) / kFK;
+  pl.lds = (size_t)(pl.fullw ? panels : 2) * 128 * kFK * 2;
+  return pl;
+}
+}  // namespace
+
+int64_t trimul_bias_parts(const oops_trimul_geometry& g) { return factor_plan(g, true).groups; }
+
 hipError_t launch_trimul_factors(const oops_trimul_geometry& g, const void* normalized, const void* weight,
                                  const float* bias, const void* mask, void* factors, const void* grad_factors,
-                                 void* grad_projection, float* grad_mask_parts, hipStream_t stream) {
+                                 void* grad_projection, float* grad_mask_parts, float* grad_bias_parts,
+                                 hipStream_t stream) {
   FactorArgs a{};
   a.xn = normalized, a.w = weight, a.bias = bias, a.mask = g.has_mask ? static_cast<const float*>(mask) : nullptr;
   a.factors = factors, a.grad_factors = grad_factors, a.grad_proj = grad_projection;
   a.mask_parts = g.has_mask ? grad_mask_parts : nullptr;
+  a.bias_parts = grad_bias_parts;
   a.rows = g.groups * g.positions, a.positions = g.positions, a.groups = g.groups, a.c_row = g.c_row;
   a.H = g.hidden;
   a.cblocks = (int)factor_cblocks(g);
-  const int64_t tiles = (a.rows + kFM - 1) / kFM * 2 * a.cblocks;
-  if (tiles == 0) return hipSuccess;
-  a.tiles = tiles;
-  const dim3 grid((unsigned)xcd_grid(tiles, 0));
   const bool bwd = grad_factors != nullptr;
+  const FactorPlan pl = factor_plan(g, bwd);
+  if (pl.tiles == 0) return hipSuccess;
+  a.tiles = pl.tiles;
+  a.tpw = pl.tpw;
+  const dim3 grid((unsigned)xcd_grid(pl.tiles, 0));
   return by_half(g.dtype, [&](auto tag) -> hipError_t {
     using T = decltype(tag);
-    if (bwd)
-      hipLaunchKernelGGL((trimul_factor_kernel<T, true>), grid, dim3(256), 0, stream, a);
+    if (bwd && pl.fullw)
+      hipLaunchKernelGGL((trimul_factor_kernel<T, true, true>), grid, dim3(256), pl.lds, stream, a);
+    else if (bwd)
+      hipLaunchKernelGGL((trimul_factor_kernel<T, true, false>), grid, dim3(256), pl.lds, stream, a);
+    else if (pl.fullw)
+      hipLaunchKernelGGL((trimul_factor_kernel<T, false, true>), grid, dim3(256), pl.lds, stream, a);
     else
-      hipLaunchKernelGGL((trimul_factor_kernel<T, false>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((trimul_factor_kernel<T, false, false>), grid, dim3(256), pl.lds, stream, a);
     return hipGetLastError();
   });
 }

@@ -16,8 +16,10 @@ int64_t layer_norm_rows_parts(const oops_row_norm_geometry& g);
 
 hipError_t launch_trimul_factors(const oops_trimul_geometry& g, const void* normalized, const void* weight,
                                  const float* bias, const void* mask, void* factors, const void* grad_factors,
-                                 void* grad_projection, float* grad_mask_parts, hipStream_t stream);
+                                 void* grad_projection, float* grad_mask_parts, float* grad_bias_parts,
+                                 hipStream_t stream);
 int64_t trimul_mask_parts(const oops_trimul_geometry& g);
+int64_t trimul_bias_parts(const oops_trimul_geometry& g);
 
 hipError_t launch_trimul_output_norm_forward(const oops_trimul_geometry& g, const void* combined, const float* weight,
                                              const float* bias, void* normalized, float* mean, float* rstd,

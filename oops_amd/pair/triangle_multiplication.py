@@ -433,14 +433,16 @@ class _TriangleMultiplication(torch.autograd.Function):
             want_mask = mask32 is not None and needs[1]
             mparts = torch.empty(lib.oops_trimul_mask_parts(ctypes.byref(geo)), R, dtype=torch.float32,
                                  device=dev) if want_mask else None  # fmt: skip
+            bparts = torch.empty(lib.oops_trimul_bias_parts(ctypes.byref(geo)), 4 * H, dtype=torch.float32,
+                                 device=dev)  # fmt: skip
             _lib.check(lib.oops_trimul_factors_backward(ctypes.byref(geo), _ptr(xn), _ptr(w_cat), _ptr(b_cat),
                                                         _ptr(mask32), _ptr(d_factors), _ptr(d_proj), _ptr(mparts),
-                                                        stream),
+                                                        _ptr(bparts), stream),
                        "triangle_multiplication factor backward")  # fmt: skip
             w4 = w_cat[:, :C]
             d_xn = torch.addmm(d_xn, d_proj.t(), w4)
             d_w4 = _long_k_matmul(d_proj, xn[:, :C])  # (4H, C)
-            d_b4 = d_proj.sum(1, dtype=torch.float32)
+            d_b4 = bparts.sum(0)
 
             d_x = torch.empty(G, P, C, dtype=dtype, device=dev)
             rg = _row_geometry(dtype, R, C, C, C, ctx.eps_in)
