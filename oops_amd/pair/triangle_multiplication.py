@@ -36,6 +36,7 @@ from ..attention._runtime import is_nested, require_no_forward_mode, require_sam
 
 _OPERATOR = "triangle_multiplication"
 _KERNEL_DTYPES = (torch.bfloat16, torch.float16)
+_SERVED_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 _DTYPE_CODE = {torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
 MAX_FUSED_WIDTH = 1024
 
@@ -188,7 +189,7 @@ def _admit(pair: Tensor, weights, biases) -> None:
     affine = (weights[6], weights[7])
     ok = (
         pair.is_cuda
-        and pair.dtype in _KERNEL_DTYPES
+        and pair.dtype in _SERVED_DTYPES
         and 0 < pair.shape[-1] <= MAX_FUSED_WIDTH
         and 0 < hidden <= MAX_FUSED_WIDTH
         and all(w.device == pair.device for w in weights)
@@ -201,7 +202,7 @@ def _admit(pair: Tensor, weights, biases) -> None:
     if not ok:
         raise unsupported(
             _OPERATOR,
-            "requires a CUDA float16/bfloat16 pair, channel widths within the fused launch domain, and weights on "
+            "requires a CUDA float16/bfloat16/float32 pair, channel widths within the fused launch domain, and weights on "
             "the pair's device in the pair's dtype (float32 allowed for the two LayerNorms)",
             pair=_describe(pair),
             hidden_size=hidden,
@@ -476,8 +477,38 @@ class _TriangleMultiplication(torch.autograd.Function):
 
 def _run(grouped: Tensor, mask: Optional[Tensor], blocks, direction, weights, biases, eps_in, eps_out) -> Tensor:
     _admit(grouped, weights, biases)
+    if grouped.dtype == torch.float32:
+        return _run_float32(grouped, mask, blocks, direction, weights, biases, eps_in, eps_out)
     return _TriangleMultiplication.apply(grouped, mask, blocks, direction, float(eps_in), float(eps_out), *weights,
                                          *biases)  # fmt: skip
+
+
+def _run_float32(grouped, mask, blocks, direction, weights, biases, eps_in, eps_out) -> Tensor:
+    """float32 pairs: both LayerNorms on the HIP row kernels (``layer_norm``), the projections and the
+    contraction as exact float32 library GEMMs (the fused MFMA kernels are 16-bit), the gating as
+    elementwise ops; autograd differentiates the composition."""
+
+    from ..normalization.layer_norm import layer_norm
+
+    in_w, in_b, wlv, wlg, wrv, wrg, on_w, on_b, wo, wog = weights
+    blv, blg, brv, brg, bo, bog = biases
+    G, P, C = grouped.shape
+    H = wlv.shape[0]
+    linear = torch.nn.functional.linear
+    xn = layer_norm(grouped, C, in_w, in_b, eps_in)
+    keep = 1.0 if mask is None else mask.to(torch.float32).unsqueeze(-1)
+    left = keep * linear(xn, wlv, blv) * torch.sigmoid(linear(xn, wlg, blg))
+    right = keep * linear(xn, wrv, brv) * torch.sigmoid(linear(xn, wrg, brg))
+    left, right = left.transpose(1, 2), right.transpose(1, 2)  # (G, H, P)
+    pieces = []
+    for off, n in blocks:
+        lb = left[:, :, off : off + n * n].reshape(G, H, n, n)
+        rb = right[:, :, off : off + n * n].reshape(G, H, n, n)
+        x = lb @ rb.transpose(-1, -2) if direction == "outgoing" else lb.transpose(-1, -2) @ rb
+        pieces.append(x.reshape(G, H, n * n))
+    combined = (pieces[0] if len(pieces) == 1 else torch.cat(pieces, -1)).transpose(1, 2)  # (G, P, H)
+    normalized = layer_norm(combined, H, on_w, on_b, eps_out)
+    return linear(normalized, wo, bo) * torch.sigmoid(linear(xn, wog, bog))
 
 
 # ----------------------------------------------------------------- nested

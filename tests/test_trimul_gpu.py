@@ -23,7 +23,7 @@ from oracle import trimul as otm
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
-_ROUNDING = {torch.bfloat16: "bf16", torch.float16: "f16"}
+_ROUNDING = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: None}
 _NAMES = ("input_norm_weight", "input_norm_bias", "left_value_weight", "left_gate_weight", "right_value_weight",
           "right_gate_weight", "output_norm_weight", "output_norm_bias", "output_weight", "output_gate_weight")
 _BIAS = ("left_value_bias", "left_gate_bias", "right_value_bias", "right_gate_bias", "output_bias",
@@ -33,7 +33,7 @@ _BIAS = ("left_value_bias", "left_gate_bias", "right_value_bias", "right_gate_bi
 # the reference's gradient criterion for this operator
 # (tests/pair/triangle_multiplication/test_triangle_multiplication.py:36-40, :458-464):
 # |got - want| <= tol * max(1, max |want|) over each gradient tensor
-_GRAD_TOL = {torch.bfloat16: 5e-2, torch.float16: 3e-2}
+_GRAD_TOL = {torch.bfloat16: 5e-2, torch.float16: 3e-2, torch.float32: 1e-5}
 
 
 def _assert_grad_close(got, want, dtype, what):
@@ -97,6 +97,8 @@ def _check(pair, mask, weights, bs, direction, dtype, grads=True, mask_grad=Fals
         (torch.float16, 65, 96, 17, (), "incoming", True),
         (torch.bfloat16, 128, 128, 19, (2, 3), "outgoing", False),
         (torch.bfloat16, 128, 128, 64, (1,), "incoming", True),
+        (torch.float32, 17, 24, 7, (2,), "outgoing", True),
+        (torch.float32, 8, 12, 9, (), "incoming", False),
     ],
 )
 def test_trimul_dense(dtype, c, h, n, prefix, direction, biases):
@@ -196,6 +198,6 @@ def test_trimul_errors():
         _call(pair, torch.ones(5, 4, device=DEV), weights, bs, "outgoing")
     with pytest.raises(ValueError):
         _call(pair, None, (weights[0][:-1], *weights[1:]), bs, "outgoing")
-    fw, fb = _params(torch.float64, 16, 8, seed=1)
+    fw, fb = _params(torch.float64, 16, 8, seed=1)  # float64 is not served
     with pytest.raises(OOpsUnsupportedError):
         _call(pair.double(), None, fw, fb, "outgoing")
