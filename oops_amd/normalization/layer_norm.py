@@ -14,7 +14,7 @@ from __future__ import annotations
 
 import ctypes
 import math
-from typing import Iterable, Optional, Union
+from typing import Iterable, Optional, Tuple, Union
 
 import torch
 from torch import Tensor
@@ -86,7 +86,7 @@ def layer_norm(
             weight_dtype=None if weight is None else weight.dtype,
             bias_dtype=None if bias is None else bias.dtype,
         )
-    return _LayerNorm.apply(input, weight, bias, float(eps))
+    return _apply(input, weight, bias, float(eps))
 
 
 def _nested(input, normalized_shape, weight, bias, eps):
@@ -117,53 +117,93 @@ def _ptr(t: Optional[Tensor]) -> Optional[int]:
     return None if t is None or t.numel() == 0 else t.data_ptr()
 
 
-class _LayerNorm(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, x, weight, bias, eps):
-        lib = _lib.load()
-        width = x.shape[-1]
-        rows = x.numel() // width
-        x2 = x.resolve_neg().reshape(rows, width)
-        if x2.stride(1) != 1 or (rows > 1 and x2.stride(0) < width):
-            x2 = x2.contiguous()
-        f32 = lambda t: None if t is None else t.detach().resolve_neg().float().contiguous()  # noqa: E731
-        w32, b32 = f32(weight), f32(bias)
-        y = torch.empty(rows, width, dtype=x.dtype, device=x.device)
-        mean = torch.empty(rows, dtype=torch.float32, device=x.device)
-        rstd = torch.empty_like(mean)
-        geo = _geometry(x.dtype, rows, width, x2.stride(0) if rows > 1 else width, eps)
-        with torch.cuda.device(x.device):
-            rc = lib.oops_layer_norm_rows_forward(ctypes.byref(geo), _ptr(x2), _ptr(w32), _ptr(b32), _ptr(y),
-                                                  _ptr(mean), _ptr(rstd), torch.cuda.current_stream().cuda_stream)
-        _lib.check(rc, "layer_norm forward")
-        ctx.save_for_backward(x2, w32, mean, rstd)
-        ctx.eps = eps
-        ctx.shape = x.shape
-        ctx.dtypes = (None if weight is None else weight.dtype, None if bias is None else bias.dtype)
-        return y.view(x.shape)
+@torch.library.custom_op("oops_amd::layer_norm_forward", mutates_args=(), device_types="cuda")
+def layer_norm_forward(
+    x: Tensor, weight: Optional[Tensor], bias: Optional[Tensor], eps: float
+) -> Tuple[Tensor, Tensor, Tensor]:
+    """Rows ``x`` (rows, width) with unit column stride; float32 affine.  Returns (y, mean, rstd)."""
 
-    @staticmethod
-    def backward(ctx, dy):
-        lib = _lib.load()
-        x2, w32, mean, rstd = ctx.saved_tensors
-        rows, width = x2.shape
-        dy2 = dy.resolve_neg().to(x2.dtype).reshape(rows, width).contiguous()
-        dx = torch.empty(rows, width, dtype=x2.dtype, device=x2.device)
-        geo = _geometry(x2.dtype, rows, width, x2.stride(0) if rows > 1 else width, ctx.eps)
-        geo.y_row = width
-        parts = lib.oops_layer_norm_rows_parts(ctypes.byref(geo))
-        need_w, need_b = ctx.needs_input_grad[1], ctx.needs_input_grad[2]
-        acc = torch.empty(2, parts, width, dtype=torch.float32, device=x2.device) if need_w or need_b else None
-        # grad_x is written with x's row stride: give it x's layout when x is a row view
-        if x2.stride(0) != width and rows > 1:
-            dx = torch.empty_strided(x2.shape, x2.stride(), dtype=x2.dtype, device=x2.device)
-        with torch.cuda.device(x2.device):
-            rc = lib.oops_layer_norm_rows_backward(ctypes.byref(geo), _ptr(x2), _ptr(w32), _ptr(mean), _ptr(rstd),
-                                                   _ptr(dy2), _ptr(dx), None if acc is None else acc[0].data_ptr(),
-                                                   None if acc is None else acc[1].data_ptr(),
-                                                   torch.cuda.current_stream().cuda_stream)  # fmt: skip
-        _lib.check(rc, "layer_norm backward")
-        sums = acc.sum(1) if acc is not None else None
-        dw = sums[0].to(ctx.dtypes[0]) if need_w else None
-        db = sums[1].to(ctx.dtypes[1]) if need_b else None
-        return dx.reshape(ctx.shape), dw, db, None
+    lib = _lib.load()
+    rows, width = x.shape
+    y = torch.empty(rows, width, dtype=x.dtype, device=x.device)
+    mean = torch.empty(rows, dtype=torch.float32, device=x.device)
+    rstd = torch.empty_like(mean)
+    geo = _geometry(x.dtype, rows, width, x.stride(0) if rows > 1 else width, eps)
+    with torch.cuda.device(x.device):
+        rc = lib.oops_layer_norm_rows_forward(ctypes.byref(geo), _ptr(x), _ptr(weight), _ptr(bias), _ptr(y),
+                                              _ptr(mean), _ptr(rstd), torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "layer_norm forward")
+    return y, mean, rstd
+
+
+@layer_norm_forward.register_fake
+def _(x, weight, bias, eps):
+    rows, width = x.shape
+    return x.new_empty(rows, width), x.new_empty(rows, dtype=torch.float32), x.new_empty(rows, dtype=torch.float32)
+
+
+@torch.library.custom_op("oops_amd::layer_norm_backward", mutates_args=(), device_types="cuda")
+def layer_norm_backward(
+    dy: Tensor, x: Tensor, weight: Optional[Tensor], mean: Tensor, rstd: Tensor, eps: float, need_affine: bool
+) -> Tuple[Tensor, Tensor, Tensor]:
+    """(dx, dweight, dbias); the affine gradients are float32 (empty when not needed)."""
+
+    lib = _lib.load()
+    rows, width = x.shape
+    dy = dy.resolve_neg().to(x.dtype).reshape(rows, width).contiguous()
+    geo = _geometry(x.dtype, rows, width, x.stride(0) if rows > 1 else width, eps)
+    # grad_x is written with x's row stride
+    dx = torch.empty_strided(x.shape, x.stride(), dtype=x.dtype, device=x.device)
+    acc = None
+    if need_affine:
+        acc = torch.empty(2, lib.oops_layer_norm_rows_parts(ctypes.byref(geo)), width, dtype=torch.float32,
+                          device=x.device)  # fmt: skip
+    with torch.cuda.device(x.device):
+        rc = lib.oops_layer_norm_rows_backward(ctypes.byref(geo), _ptr(x), _ptr(weight), _ptr(mean), _ptr(rstd),
+                                               _ptr(dy), _ptr(dx), None if acc is None else acc[0].data_ptr(),
+                                               None if acc is None else acc[1].data_ptr(),
+                                               torch.cuda.current_stream().cuda_stream)  # fmt: skip
+    _lib.check(rc, "layer_norm backward")
+    if acc is None:
+        return dx, x.new_empty(0, dtype=torch.float32), x.new_empty(0, dtype=torch.float32)
+    return dx, acc[0].sum(0), acc[1].sum(0)
+
+
+@layer_norm_backward.register_fake
+def _(dy, x, weight, mean, rstd, eps, need_affine):
+    rows, width = x.shape
+    n = width if need_affine else 0
+    return (torch.empty_strided(x.shape, x.stride(), dtype=x.dtype, device=x.device),
+            x.new_empty(n, dtype=torch.float32), x.new_empty(n, dtype=torch.float32))  # fmt: skip
+
+
+def _setup_context(ctx, inputs, output):
+    x, weight, bias, eps = inputs
+    _y, mean, rstd = output
+    ctx.save_for_backward(x, weight, mean, rstd)
+    ctx.eps = eps
+    ctx.has = (weight is not None, bias is not None)
+    ctx.mark_non_differentiable(mean, rstd)
+
+
+def _backward(ctx, dy, _dmean, _drstd):
+    x, weight, mean, rstd = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    need_affine = bool(need[1] or need[2])
+    dx, dw, db = layer_norm_backward(dy, x, weight, mean, rstd, ctx.eps, need_affine)
+    return (dx if need[0] else None, dw if ctx.has[0] and need[1] else None,
+            db if ctx.has[1] and need[2] else None, None)  # fmt: skip
+
+
+layer_norm_forward.register_autograd(_backward, setup_context=_setup_context)
+
+
+def _apply(x: Tensor, weight: Optional[Tensor], bias: Optional[Tensor], eps: float) -> Tensor:
+    width = x.shape[-1]
+    rows = x.numel() // width
+    x2 = x.resolve_neg().reshape(rows, width)
+    if x2.stride(1) != 1 or (rows > 1 and x2.stride(0) < width):
+        x2 = x2.contiguous()
+    f32 = lambda t: None if t is None else t.resolve_neg().float().contiguous()  # noqa: E731
+    y, _, _ = layer_norm_forward(x2, f32(weight), f32(bias), eps)
+    return y.view(x.shape)

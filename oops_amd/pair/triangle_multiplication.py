@@ -24,7 +24,7 @@ contraction.
 from __future__ import annotations
 
 import ctypes
-from typing import Literal, Optional, Sequence
+from typing import List, Literal, Optional, Sequence, Tuple
 
 import torch
 from torch import Tensor
@@ -315,172 +315,254 @@ def _contract(factors: Tensor, out: Tensor, blocks, direction: str, grad: bool =
             out[1, :, :, cells].copy_(d_right.view(G, H, n * n))
 
 
-class _TriangleMultiplication(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, pair, mask, blocks, direction, eps_in, eps_out, *params):
-        lib = _lib.load()
-        in_w, in_b, wlv, wlg, wrv, wrg, on_w, on_b, wo, wog = params[:10]
-        blv, blg, brv, brg, bo, bog = params[10:]
-        G, P, C = pair.shape
-        H = wlv.shape[0]
-        R = G * P
-        dtype, dev = pair.dtype, pair.device
-        x = pair.resolve_neg().contiguous()
-        geo = _geometry(x, H, mask is not None, eps_out)
-        cp, hp = geo.c_row, geo.h_row
-        stream = _stream(dev)
-        # the small float32 parameters (projection and output biases, both LayerNorm affines) in one
-        # buffer: one concatenation and one conversion instead of a launch per parameter
-        small = (("b4", (blv, blg, brv, brg), H), ("bo", (bo,), C), ("bog", (bog,), C), ("in_w", (in_w,), C),
-                 ("in_b", (in_b,), C), ("on_w", (on_w,), H), ("on_b", (on_b,), H))  # fmt: skip
-        pieces, spans, off = [], {}, 0
-        for name, tensors, n in small:
-            if all(t is None for t in tensors):
-                spans[name] = None
-                continue
-            for t in tensors:
-                pieces.append(torch.zeros(n, device=dev) if t is None else t.detach().resolve_neg().reshape(-1))
-            spans[name] = (off, off + n * len(tensors))
-            off += n * len(tensors)
-        buf = torch.cat(pieces).float()
-        view = lambda name: None if spans[name] is None else buf[spans[name][0] : spans[name][1]]  # noqa: E731
-        b_cat, bo32, bog32 = view("b4"), view("bo"), view("bog")
-        in_w32, in_b32, on_w32, on_b32 = view("in_w"), view("in_b"), view("on_w"), view("on_b")
+def _pairs(blocks: List[int]):
+    return [(blocks[i], blocks[i + 1]) for i in range(0, len(blocks), 2)]
 
-        def padded(w: Tensor, width: int) -> Tensor:
-            w = w.detach().resolve_neg()
-            return (F.pad(w, (0, width - w.shape[1])) if width != w.shape[1] else w).contiguous()
 
-        # projection weights concatenated and zero-padded to the 16-byte rows the kernels load
-        w_cat = padded(torch.cat([w.detach() for w in (wlv, wlg, wrv, wrg)]), cp)
-        wo_p, wog_p = padded(wo, hp), padded(wog, cp)
-        mask32 = None if mask is None else mask.detach().resolve_neg().float().contiguous()
+@torch.library.custom_op("oops_amd::trimul_forward", mutates_args=(), device_types="cuda")
+def trimul_forward(
+    pair: Tensor,
+    mask: Optional[Tensor],
+    w_cat: Tensor,
+    b_cat: Optional[Tensor],
+    wo: Tensor,
+    wog: Tensor,
+    bo: Optional[Tensor],
+    bog: Optional[Tensor],
+    in_w: Tensor,
+    in_b: Tensor,
+    on_w: Tensor,
+    on_b: Tensor,
+    blocks: List[int],
+    direction: str,
+    eps_in: float,
+    eps_out: float,
+) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Forward on prepared operands: pair (G, P, C); float32 mask (G, P); w_cat [4H][c_row]; wo [C][h_row];
+    wog [C][c_row]; float32 biases and LayerNorm affines.  Returns (out, xn, mean_in, rstd_in, factors,
+    combined, nrm, mean_out, rstd_out); all but ``out`` are kept for the backward."""
 
-        with torch.cuda.device(dev):
-            xn = torch.empty(R, cp, dtype=dtype, device=dev)
-            mean_in = torch.empty(R, dtype=torch.float32, device=dev)
-            rstd_in = torch.empty_like(mean_in)
-            rg = _row_geometry(dtype, R, C, C, cp, eps_in)
-            _lib.check(lib.oops_layer_norm_rows_forward(ctypes.byref(rg), _ptr(x), _ptr(in_w32), _ptr(in_b32),
-                                                        _ptr(xn), _ptr(mean_in), _ptr(rstd_in), stream),
-                       "triangle_multiplication input LayerNorm")  # fmt: skip
-            factors = torch.empty(2, G, H, P, dtype=dtype, device=dev)
-            _lib.check(lib.oops_trimul_factors_forward(ctypes.byref(geo), _ptr(xn), _ptr(w_cat), _ptr(b_cat),
-                                                       _ptr(mask32), _ptr(factors), stream),
-                       "triangle_multiplication factors")  # fmt: skip
-            combined = torch.empty(G, H, P, dtype=dtype, device=dev)
-            _contract(factors, combined, blocks, direction)
-            nrm = torch.empty(R, hp, dtype=dtype, device=dev)
-            mean_out = torch.empty(R, dtype=torch.float32, device=dev)
-            rstd_out = torch.empty_like(mean_out)
-            _lib.check(lib.oops_trimul_output_norm_forward(ctypes.byref(geo), _ptr(combined), _ptr(on_w32),
-                                                           _ptr(on_b32), _ptr(nrm), _ptr(mean_out), _ptr(rstd_out),
-                                                           stream),
-                       "triangle_multiplication output LayerNorm")  # fmt: skip
-            out = torch.empty(G, P, C, dtype=dtype, device=dev)
-            _lib.check(lib.oops_trimul_output_forward(ctypes.byref(geo), _ptr(nrm), _ptr(xn), _ptr(wo_p),
-                                                      _ptr(wog_p), _ptr(bo32), _ptr(bog32), _ptr(out), stream),
-                       "triangle_multiplication output")  # fmt: skip
+    lib = _lib.load()
+    G, P, C = pair.shape
+    H = w_cat.shape[0] // 4
+    R = G * P
+    dtype, dev = pair.dtype, pair.device
+    geo = _geometry(pair, H, mask is not None, eps_out)
+    cp, hp = geo.c_row, geo.h_row
+    stream = _stream(dev)
+    with torch.cuda.device(dev):
+        xn = torch.empty(R, cp, dtype=dtype, device=dev)
+        mean_in = torch.empty(R, dtype=torch.float32, device=dev)
+        rstd_in = torch.empty_like(mean_in)
+        rg = _row_geometry(dtype, R, C, C, cp, eps_in)
+        _lib.check(lib.oops_layer_norm_rows_forward(ctypes.byref(rg), _ptr(pair), _ptr(in_w), _ptr(in_b), _ptr(xn),
+                                                    _ptr(mean_in), _ptr(rstd_in), stream),
+                   "triangle_multiplication input LayerNorm")  # fmt: skip
+        factors = torch.empty(2, G, H, P, dtype=dtype, device=dev)
+        _lib.check(lib.oops_trimul_factors_forward(ctypes.byref(geo), _ptr(xn), _ptr(w_cat), _ptr(b_cat),
+                                                   _ptr(mask), _ptr(factors), stream),
+                   "triangle_multiplication factors")  # fmt: skip
+        combined = torch.empty(G, H, P, dtype=dtype, device=dev)
+        _contract(factors, combined, _pairs(blocks), direction)
+        nrm = torch.empty(R, hp, dtype=dtype, device=dev)
+        mean_out = torch.empty(R, dtype=torch.float32, device=dev)
+        rstd_out = torch.empty_like(mean_out)
+        _lib.check(lib.oops_trimul_output_norm_forward(ctypes.byref(geo), _ptr(combined), _ptr(on_w), _ptr(on_b),
+                                                       _ptr(nrm), _ptr(mean_out), _ptr(rstd_out), stream),
+                   "triangle_multiplication output LayerNorm")  # fmt: skip
+        out = torch.empty(G, P, C, dtype=dtype, device=dev)
+        _lib.check(lib.oops_trimul_output_forward(ctypes.byref(geo), _ptr(nrm), _ptr(xn), _ptr(wo), _ptr(wog),
+                                                  _ptr(bo), _ptr(bog), _ptr(out), stream),
+                   "triangle_multiplication output")  # fmt: skip
+    return out, xn, mean_in, rstd_in, factors, combined, nrm, mean_out, rstd_out
 
-        ctx.save_for_backward(x, xn, mean_in, rstd_in, in_w32, w_cat, b_cat, mask32, factors, combined, nrm,
-                              mean_out, rstd_out, on_w32, wo_p, wog_p, bo32, bog32)  # fmt: skip
-        ctx.blocks, ctx.direction, ctx.eps_in, ctx.eps_out = blocks, direction, eps_in, eps_out
-        ctx.param_meta = [(None if p is None else (p.dtype, p.shape)) for p in params]
-        ctx.mask_dtype = None if mask is None else mask.dtype
-        return out
 
-    @staticmethod
-    def backward(ctx, dout):
-        lib = _lib.load()
-        (x, xn, mean_in, rstd_in, in_w32, w_cat, b_cat, mask32, factors, combined, nrm, mean_out, rstd_out, on_w32,
-         wo_p, wog_p, bo32, bog32) = ctx.saved_tensors  # fmt: skip
-        G, P, C = x.shape
-        H = factors.shape[2]
-        R = G * P
-        dtype, dev = x.dtype, x.device
-        geo = _geometry(x, H, mask32 is not None, ctx.eps_out)
-        cp, hp = geo.c_row, geo.h_row
-        stream = _stream(dev)
-        dout = dout.resolve_neg().to(dtype).contiguous()
-        needs = ctx.needs_input_grad
-        with torch.cuda.device(dev):
-            g_val = torch.empty(R, cp, dtype=dtype, device=dev)
-            g_gate = torch.empty(R, cp, dtype=dtype, device=dev)
-            _lib.check(lib.oops_trimul_output_backward(ctypes.byref(geo), _ptr(nrm), _ptr(xn), _ptr(wo_p),
-                                                       _ptr(wog_p), _ptr(bo32), _ptr(bog32), _ptr(dout),
-                                                       _ptr(g_val), _ptr(g_gate), stream),
-                       "triangle_multiplication output backward")  # fmt: skip
-            gv, gg = g_val[:, :C], g_gate[:, :C]
-            wo, wog = wo_p[:, :H], wog_p[:, :C]
-            d_nrm = gv.mm(wo).contiguous()  # (R, H)
-            d_xn = gg.mm(wog)  # (R, C)
-            d_wo = _long_k_matmul(gv.t(), nrm[:, :H])
-            d_wog = _long_k_matmul(gg.t(), xn[:, :C])
-            d_bo = gv.sum(0, dtype=torch.float32)
-            d_bog = gg.sum(0, dtype=torch.float32)
+@trimul_forward.register_fake
+def _(pair, mask, w_cat, b_cat, wo, wog, bo, bog, in_w, in_b, on_w, on_b, blocks, direction, eps_in, eps_out):
+    G, P, C = pair.shape
+    H = w_cat.shape[0] // 4
+    R = G * P
+    f32 = dict(dtype=torch.float32, device=pair.device)
+    return (pair.new_empty(G, P, C), pair.new_empty(R, w_cat.shape[1]), pair.new_empty(R, **f32),
+            pair.new_empty(R, **f32), pair.new_empty(2, G, H, P), pair.new_empty(G, H, P),
+            pair.new_empty(R, wo.shape[1]), pair.new_empty(R, **f32), pair.new_empty(R, **f32))  # fmt: skip
 
-            d_comb = torch.empty(G, H, P, dtype=dtype, device=dev)
-            parts = lib.oops_trimul_output_norm_parts(ctypes.byref(geo))
-            on_parts = torch.empty(2, parts, H, dtype=torch.float32, device=dev)
-            on_w_parts, on_b_parts = on_parts[0], on_parts[1]
-            _lib.check(lib.oops_trimul_output_norm_backward(ctypes.byref(geo), _ptr(combined), _ptr(on_w32),
-                                                            _ptr(mean_out), _ptr(rstd_out), _ptr(d_nrm),
-                                                            _ptr(d_comb), _ptr(on_w_parts), _ptr(on_b_parts),
-                                                            stream),
-                       "triangle_multiplication output LayerNorm backward")  # fmt: skip
-            d_factors = torch.empty_like(factors)
-            _contract(factors, d_factors, ctx.blocks, ctx.direction, grad=True, grad_out=d_comb)
-            d_proj = torch.empty(4 * H, R, dtype=dtype, device=dev)
-            want_mask = mask32 is not None and needs[1]
-            mparts = torch.empty(lib.oops_trimul_mask_parts(ctypes.byref(geo)), R, dtype=torch.float32,
-                                 device=dev) if want_mask else None  # fmt: skip
-            bparts = torch.empty(lib.oops_trimul_bias_parts(ctypes.byref(geo)), 4 * H, dtype=torch.float32,
-                                 device=dev)  # fmt: skip
-            _lib.check(lib.oops_trimul_factors_backward(ctypes.byref(geo), _ptr(xn), _ptr(w_cat), _ptr(b_cat),
-                                                        _ptr(mask32), _ptr(d_factors), _ptr(d_proj), _ptr(mparts),
-                                                        _ptr(bparts), stream),
-                       "triangle_multiplication factor backward")  # fmt: skip
-            w4 = w_cat[:, :C]
-            d_xn = torch.addmm(d_xn, d_proj.t(), w4)
-            d_w4 = _long_k_matmul(d_proj, xn[:, :C])  # (4H, C)
-            d_b4 = bparts.sum(0)
 
-            d_x = torch.empty(G, P, C, dtype=dtype, device=dev)
-            rg = _row_geometry(dtype, R, C, C, C, ctx.eps_in)
-            rparts = lib.oops_layer_norm_rows_parts(ctypes.byref(rg))
-            in_parts = torch.empty(2, rparts, C, dtype=torch.float32, device=dev)
-            in_w_parts, in_b_parts = in_parts[0], in_parts[1]
-            d_xn = d_xn.contiguous()
-            _lib.check(lib.oops_layer_norm_rows_backward(ctypes.byref(rg), _ptr(x), _ptr(in_w32), _ptr(mean_in),
-                                                         _ptr(rstd_in), _ptr(d_xn), _ptr(d_x), _ptr(in_w_parts),
-                                                         _ptr(in_b_parts), stream),
-                       "triangle_multiplication input LayerNorm backward")  # fmt: skip
+@torch.library.custom_op("oops_amd::trimul_backward", mutates_args=(), device_types="cuda")
+def trimul_backward(
+    dout: Tensor,
+    pair: Tensor,
+    mask: Optional[Tensor],
+    w_cat: Tensor,
+    b_cat: Optional[Tensor],
+    wo: Tensor,
+    wog: Tensor,
+    bo: Optional[Tensor],
+    bog: Optional[Tensor],
+    in_w: Tensor,
+    on_w: Tensor,
+    xn: Tensor,
+    mean_in: Tensor,
+    rstd_in: Tensor,
+    factors: Tensor,
+    combined: Tensor,
+    nrm: Tensor,
+    mean_out: Tensor,
+    rstd_out: Tensor,
+    blocks: List[int],
+    direction: str,
+    eps_in: float,
+    eps_out: float,
+    need_mask: bool,
+) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Gradients of every prepared operand: (pair, mask, w_cat, b_cat, wo, wog, bo, bog, in_w, in_b, on_w,
+    on_b); an absent optional operand gets an empty tensor."""
 
-        meta = ctx.param_meta
+    lib = _lib.load()
+    G, P, C = pair.shape
+    H = factors.shape[2]
+    R = G * P
+    dtype, dev = pair.dtype, pair.device
+    geo = _geometry(pair, H, mask is not None, eps_out)
+    cp, hp = geo.c_row, geo.h_row
+    stream = _stream(dev)
+    dout = dout.resolve_neg().to(dtype).contiguous()
 
-        def cast(i, g):
-            return None if meta[i] is None or not needs[6 + i] else g.to(meta[i][0])
+    def empty():  # a fresh tensor per absent gradient: custom-op outputs may not alias
+        return pair.new_empty(0, dtype=torch.float32)
 
-        in_ab, on_ab = in_parts.sum(1), on_parts.sum(1)
-        d_w4s = d_w4.split(H)
-        d_b4s = d_b4.split(H)
-        grads = [
-            cast(0, in_ab[0]), cast(1, in_ab[1]),
-            cast(2, d_w4s[0]), cast(3, d_w4s[1]), cast(4, d_w4s[2]), cast(5, d_w4s[3]),
-            cast(6, on_ab[0]), cast(7, on_ab[1]), cast(8, d_wo), cast(9, d_wog),
-            cast(10, d_b4s[0]), cast(11, d_b4s[1]), cast(12, d_b4s[2]), cast(13, d_b4s[3]),
-            cast(14, d_bo), cast(15, d_bog),
-        ]  # fmt: skip
-        d_mask = mparts.sum(0).view(G, P).to(ctx.mask_dtype) if want_mask else None
-        return (d_x if needs[0] else None, d_mask, None, None, None, None, *grads)
+    with torch.cuda.device(dev):
+        g_val = torch.empty(R, cp, dtype=dtype, device=dev)
+        g_gate = torch.empty(R, cp, dtype=dtype, device=dev)
+        _lib.check(lib.oops_trimul_output_backward(ctypes.byref(geo), _ptr(nrm), _ptr(xn), _ptr(wo), _ptr(wog),
+                                                   _ptr(bo), _ptr(bog), _ptr(dout), _ptr(g_val), _ptr(g_gate),
+                                                   stream),
+                   "triangle_multiplication output backward")  # fmt: skip
+        gv, gg = g_val[:, :C], g_gate[:, :C]
+        d_nrm = gv.mm(wo[:, :H]).contiguous()  # (R, H)
+        d_xn = gg.mm(wog[:, :C])  # (R, C)
+        d_wo = F.pad(_long_k_matmul(gv.t(), nrm[:, :H]), (0, hp - H)) if hp != H else _long_k_matmul(gv.t(), nrm[:, :H])
+        d_wog = F.pad(_long_k_matmul(gg.t(), xn[:, :C]), (0, cp - C)) if cp != C else _long_k_matmul(gg.t(), xn[:, :C])
+        d_bo = gv.sum(0, dtype=torch.float32) if bo is not None else empty()
+        d_bog = gg.sum(0, dtype=torch.float32) if bog is not None else empty()
+
+        d_comb = torch.empty(G, H, P, dtype=dtype, device=dev)
+        on_parts = torch.empty(2, lib.oops_trimul_output_norm_parts(ctypes.byref(geo)), H, dtype=torch.float32,
+                               device=dev)  # fmt: skip
+        _lib.check(lib.oops_trimul_output_norm_backward(ctypes.byref(geo), _ptr(combined), _ptr(on_w),
+                                                        _ptr(mean_out), _ptr(rstd_out), _ptr(d_nrm), _ptr(d_comb),
+                                                        _ptr(on_parts[0]), _ptr(on_parts[1]), stream),
+                   "triangle_multiplication output LayerNorm backward")  # fmt: skip
+        d_factors = torch.empty_like(factors)
+        _contract(factors, d_factors, _pairs(blocks), direction, grad=True, grad_out=d_comb)
+        d_proj = torch.empty(4 * H, R, dtype=dtype, device=dev)
+        want_mask = mask is not None and need_mask
+        mparts = torch.empty(lib.oops_trimul_mask_parts(ctypes.byref(geo)), R, dtype=torch.float32,
+                             device=dev) if want_mask else None  # fmt: skip
+        bparts = torch.empty(lib.oops_trimul_bias_parts(ctypes.byref(geo)), 4 * H, dtype=torch.float32, device=dev)
+        _lib.check(lib.oops_trimul_factors_backward(ctypes.byref(geo), _ptr(xn), _ptr(w_cat), _ptr(b_cat),
+                                                    _ptr(mask), _ptr(d_factors), _ptr(d_proj), _ptr(mparts),
+                                                    _ptr(bparts), stream),
+                   "triangle_multiplication factor backward")  # fmt: skip
+        d_xn = torch.addmm(d_xn, d_proj.t(), w_cat[:, :C]).contiguous()
+        d_wcat = _long_k_matmul(d_proj, xn[:, :C])
+        if cp != C:
+            d_wcat = F.pad(d_wcat, (0, cp - C))
+        d_bcat = bparts.sum(0) if b_cat is not None else empty()
+
+        d_pair = torch.empty(G, P, C, dtype=dtype, device=dev)
+        rg = _row_geometry(dtype, R, C, C, C, eps_in)
+        in_parts = torch.empty(2, lib.oops_layer_norm_rows_parts(ctypes.byref(rg)), C, dtype=torch.float32,
+                               device=dev)  # fmt: skip
+        _lib.check(lib.oops_layer_norm_rows_backward(ctypes.byref(rg), _ptr(pair), _ptr(in_w), _ptr(mean_in),
+                                                     _ptr(rstd_in), _ptr(d_xn), _ptr(d_pair), _ptr(in_parts[0]),
+                                                     _ptr(in_parts[1]), stream),
+                   "triangle_multiplication input LayerNorm backward")  # fmt: skip
+    d_mask = mparts.sum(0).view(G, P) if want_mask else empty()
+    return (d_pair, d_mask, d_wcat, d_bcat, d_wo, d_wog, d_bo, d_bog, in_parts[0].sum(0), in_parts[1].sum(0),
+            on_parts[0].sum(0), on_parts[1].sum(0))  # fmt: skip
+
+
+@trimul_backward.register_fake
+def _(dout, pair, mask, w_cat, b_cat, wo, wog, bo, bog, in_w, on_w, xn, mean_in, rstd_in, factors, combined, nrm,
+      mean_out, rstd_out, blocks, direction, eps_in, eps_out, need_mask):  # fmt: skip
+    G, P, C = pair.shape
+    H = factors.shape[2]
+    f32 = dict(dtype=torch.float32, device=pair.device)
+    opt = lambda t, *shape: pair.new_empty(0, **f32) if t is None else pair.new_empty(*shape, **f32)  # noqa: E731
+    return (pair.new_empty(G, P, C), opt(mask if need_mask else None, G, P),
+            torch.empty_like(w_cat), opt(b_cat, 4 * H), torch.empty_like(wo), torch.empty_like(wog), opt(bo, C),
+            opt(bog, C), pair.new_empty(C, **f32), pair.new_empty(C, **f32), pair.new_empty(H, **f32),
+            pair.new_empty(H, **f32))  # fmt: skip
+
+
+def _setup_context(ctx, inputs, output):
+    (pair, mask, w_cat, b_cat, wo, wog, bo, bog, in_w, in_b, on_w, on_b, blocks, direction, eps_in, eps_out) = inputs
+    _out, xn, mean_in, rstd_in, factors, combined, nrm, mean_out, rstd_out = output
+    ctx.save_for_backward(pair, mask, w_cat, b_cat, wo, wog, bo, bog, in_w, on_w, xn, mean_in, rstd_in, factors,
+                          combined, nrm, mean_out, rstd_out)  # fmt: skip
+    ctx.args = (blocks, direction, eps_in, eps_out)
+    ctx.optional = (mask is not None, b_cat is not None, bo is not None, bog is not None)
+    for t in output[1:]:
+        ctx.mark_non_differentiable(t)
+
+
+def _backward(ctx, dout, *_unused):
+    saved = ctx.saved_tensors
+    blocks, direction, eps_in, eps_out = ctx.args
+    need = ctx.needs_input_grad
+    grads = trimul_backward(dout, *saved, blocks, direction, eps_in, eps_out, bool(need[1]))
+    has_mask, has_bcat, has_bo, has_bog = ctx.optional
+    d_pair, d_mask, d_wcat, d_bcat, d_wo, d_wog, d_bo, d_bog, d_in_w, d_in_b, d_on_w, d_on_b = grads
+    return (
+        d_pair, d_mask if has_mask and need[1] else None, d_wcat, d_bcat if has_bcat else None, d_wo, d_wog,
+        d_bo if has_bo else None, d_bog if has_bog else None, d_in_w, d_in_b, d_on_w, d_on_b, None, None, None, None,
+    )  # fmt: skip
+
+
+trimul_forward.register_autograd(_backward, setup_context=_setup_context)
+
+
+def _prepare(grouped: Tensor, mask: Optional[Tensor], weights, biases):
+    """Kernel operands from the caller's tensors, with differentiable torch ops (their autograd maps the
+    operands' gradients back): projections concatenated and zero-padded to 16-byte rows; the small float32
+    parameters (biases, LayerNorm affines) cut from one concatenated buffer, one conversion for all."""
+
+    in_w, in_b, wlv, wlg, wrv, wrg, on_w, on_b, wo, wog = weights
+    blv, blg, brv, brg, bo, bog = biases
+    C, H = grouped.shape[-1], wlv.shape[0]
+    cp, hp = _round8(C), _round8(H)
+    small = (("b4", (blv, blg, brv, brg), H), ("bo", (bo,), C), ("bog", (bog,), C), ("in_w", (in_w,), C),
+             ("in_b", (in_b,), C), ("on_w", (on_w,), H), ("on_b", (on_b,), H))  # fmt: skip
+    pieces, spans, off = [], {}, 0
+    for name, tensors, n in small:
+        if all(t is None for t in tensors):
+            spans[name] = None
+            continue
+        for t in tensors:
+            pieces.append(torch.zeros(n, device=grouped.device) if t is None else t.resolve_neg().reshape(-1))
+        spans[name] = (off, off + n * len(tensors))
+        off += n * len(tensors)
+    buf = torch.cat(pieces).float()
+    view = lambda name: None if spans[name] is None else buf[spans[name][0] : spans[name][1]]  # noqa: E731
+
+    def padded(w: Tensor, width: int) -> Tensor:
+        w = w.resolve_neg()
+        return (F.pad(w, (0, width - w.shape[1])) if width != w.shape[1] else w).contiguous()
+
+    pair = grouped.resolve_neg().contiguous()
+    mask32 = None if mask is None else mask.resolve_neg().float().contiguous()
+    return (pair, mask32, padded(torch.cat([wlv, wlg, wrv, wrg]), cp), view("b4"), padded(wo, hp), padded(wog, cp),
+            view("bo"), view("bog"), view("in_w"), view("in_b"), view("on_w"), view("on_b"))  # fmt: skip
 
 
 def _run(grouped: Tensor, mask: Optional[Tensor], blocks, direction, weights, biases, eps_in, eps_out) -> Tensor:
     _admit(grouped, weights, biases)
     if grouped.dtype == torch.float32:
         return _run_float32(grouped, mask, blocks, direction, weights, biases, eps_in, eps_out)
-    return _TriangleMultiplication.apply(grouped, mask, blocks, direction, float(eps_in), float(eps_out), *weights,
-                                         *biases)  # fmt: skip
+    flat = [v for block in blocks for v in block]
+    operands = _prepare(grouped, mask, weights, biases)
+    return trimul_forward(*operands, flat, direction, float(eps_in), float(eps_out))[0]
 
 
 def _run_float32(grouped, mask, blocks, direction, weights, biases, eps_in, eps_out) -> Tensor:

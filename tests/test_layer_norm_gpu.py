@@ -89,3 +89,21 @@ def test_layer_norm_errors():
         layer_norm(x, 8, torch.ones(8, device=DEV, dtype=torch.bfloat16))  # half affine over float32
     with pytest.raises(OOpsUnsupportedError):
         layer_norm(torch.randn(4, 5000, device=DEV), 5000)
+
+
+def test_layer_norm_compile_matches_eager():
+    g = torch.Generator().manual_seed(8)
+    x0 = torch.randn(64, 96, generator=g).to(torch.bfloat16).to(DEV)
+    w = torch.randn(96, generator=g).to(DEV).requires_grad_(True)
+    dy = torch.randn(64, 96, generator=g).to(torch.bfloat16).to(DEV)
+
+    def run(x):
+        return layer_norm(x, 96, w, None)
+
+    results = []
+    for fn in (run, torch.compile(run, fullgraph=True)):
+        x = x0.clone().requires_grad_(True)
+        y = fn(x)
+        results.append((y.detach(), *torch.autograd.grad(y, [x, w], dy)))
+    for got, ref in zip(*results):
+        torch.testing.assert_close(got, ref, atol=0, rtol=0)

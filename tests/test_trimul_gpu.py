@@ -201,3 +201,25 @@ def test_trimul_errors():
     fw, fb = _params(torch.float64, 16, 8, seed=1)  # float64 is not served
     with pytest.raises(OOpsUnsupportedError):
         _call(pair.double(), None, fw, fb, "outgoing")
+
+
+def test_trimul_compile_matches_eager():
+    """torch.compile(fullgraph=True) traces the custom ops (the reference tests its compile mode)."""
+
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(21)
+    pair0 = torch.randn(2, 12, 12, 32, generator=g).to(dtype).to(DEV)
+    mask = (torch.rand(2, 12, 12, generator=g) > 0.2).float().to(DEV)
+    weights, bs = _params(dtype, 32, 48, seed=21)
+    dy = torch.randn(2, 12, 12, 32, generator=g).to(dtype).to(DEV)
+
+    def run(p):
+        return _call(p, mask, weights, bs, "incoming")
+
+    results = []
+    for fn in (run, torch.compile(run, fullgraph=True)):
+        p = pair0.clone().requires_grad_(True)
+        out = fn(p)
+        results.append((out.detach(), *torch.autograd.grad(out, [p, weights[2], bs[0]], dy)))
+    for got, ref in zip(*results):
+        torch.testing.assert_close(got, ref, atol=0, rtol=0)
