@@ -187,6 +187,18 @@ __global__ __launch_bounds__(256) void gate_projection_kernel(GateArgs a) {
   const T* att = static_cast<const T*>(a.attention) + att_row(a, r);
   T* lrow = STORE_LOGITS ? static_cast<T*>(a.logits) + r * N : nullptr;
   T* grow = static_cast<T*>(a.gated) + r * N;
+  // the attention runs are loaded before the first store: a store may alias a later load, so loads
+  // placed after stores would each wait for them
+  uint4 att_lo[4], att_hi[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int n = n0 + 32 * t + 16 * g2;
+    if (n >= N) continue;
+    const int h = n / a.width, d = n - h * a.width;
+    const T* arow = att + h * a.a_sh + d;
+    att_lo[t] = *reinterpret_cast<const uint4*>(arow);
+    att_hi[t] = *reinterpret_cast<const uint4*>(arow + 8);
+  }
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     uint32_t p[8];
@@ -207,10 +219,8 @@ __global__ __launch_bounds__(256) void gate_projection_kernel(GateArgs a) {
       *reinterpret_cast<uint4*>(lrow + n) = lo;
       *reinterpret_cast<uint4*>(lrow + n + 8) = hi;
     }
-    const int h = n / a.width, d = n - h * a.width;
-    const T* arow = att + h * a.a_sh + d;
-    const uint4 alo = *reinterpret_cast<const uint4*>(arow);
-    const uint4 ahi = *reinterpret_cast<const uint4*>(arow + 8);
+    const uint4 alo = att_lo[t];
+    const uint4 ahi = att_hi[t];
     const T* le = reinterpret_cast<const T*>(&lo);
     const T* he = reinterpret_cast<const T*>(&hi);
     const T* ae = reinterpret_cast<const T*>(&alo);
