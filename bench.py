@@ -157,6 +157,23 @@ def measured_traffic(kernel):
 KERNEL_GEMMS = {"fwd": 2, "dq": 3, "dkv": 4, "dbias": 2}
 
 
+def bias_traffic(kt):
+    """Bias bytes per kernel at config 3 (no mask there): each kernel reads the shared [H, N, N] bf16 bias
+    (its fragment-major copy) from HBM once; the forward, dQ and dK/dV kernels re-read it from L2 for every
+    one of the N rows, the dBias kernel once per part of rows (8 at config 3) since it keeps a tile's bias
+    while it walks the part's rows.  Rates are those bytes over the kernel's measured time."""
+
+    once = H * N * N * 2
+    reuse = {"fwd": N, "dq": N, "dkv": N, "dbias": 8}
+    out = {"bias_bytes": once, "mask_bytes": 0}
+    for k, ms in kt.items():
+        out[k] = {
+            "hbm_gbps": round(once / (ms * 1e-3) / 1e9, 1),
+            "l2_gbps": round(reuse.get(k, 1) * once / (ms * 1e-3) / 1e9, 1),
+        }
+    return out
+
+
 def _median_ms(fn, iters=10, warmup=3, reps=3):
     """ms per call of `iters` back-to-back calls (median of `reps` runs): the
     host enqueues while the GPU works, as in a training loop."""
@@ -562,6 +579,7 @@ def main():
             "parallelism": "single GPU",
         },
         "mfma_util_pct": round(100 * value / PEAK_BF16_TFLOPS, 2),
+        "bias_traffic": bias_traffic(kt),
         "peak_mem_bytes": int(peak_mem),
         "kernel_ms": {k_: round(v_, 4) for k_, v_ in kt.items()},
         "roofline": {
