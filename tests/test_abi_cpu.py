@@ -169,3 +169,32 @@ def test_pointer_and_workspace_validation(lib):
     need = lib.oops_attn_backward_workspace_bytes(ctypes.byref(geo))
     rc = lib.oops_attn_backward(ctypes.byref(geo), 1, 1, 1, None, 1, 1, None, 1, 1, 1, 1, 1, 1, 8, need, None)
     assert rc == 3 and "aligned" in lib.oops_last_error().decode()
+
+
+def test_row_norm_and_trimul_validation(lib):
+    """The LayerNorm and triangle-multiplication entry points reject bad geometry on the host."""
+
+    rg = _lib.RowNormGeometry()
+    rg.dtype, rg.width, rg.rows, rg.x_row, rg.y_row, rg.eps = _lib.BF16, 0, 4, 8, 8, 1e-5
+    fake = ctypes.c_void_p(16)
+    assert lib.oops_layer_norm_rows_forward(ctypes.byref(rg), fake, None, None, fake, fake, fake, None) != 0
+    assert b"width" in lib.oops_last_error()
+    rg.width, rg.y_row = 8, 4  # y row stride below the width
+    assert lib.oops_layer_norm_rows_forward(ctypes.byref(rg), fake, None, None, fake, fake, fake, None) != 0
+    rg.width, rg.y_row, rg.x_row = 5000, 5000, 5000
+    assert lib.oops_layer_norm_rows_parts(ctypes.byref(rg)) == 0
+
+    tg = _lib.TrimulGeometry()
+    tg.dtype, tg.channels, tg.hidden, tg.has_mask = _lib.F32, 16, 16, 0
+    tg.groups, tg.positions, tg.c_row, tg.h_row, tg.eps = 1, 16, 16, 16, 1e-5
+    assert lib.oops_trimul_factors_forward(ctypes.byref(tg), fake, fake, None, None, fake, None) != 0
+    assert b"bfloat16" in lib.oops_last_error()
+    tg.dtype, tg.c_row = _lib.BF16, 12  # padded row stride must be a multiple of 8
+    assert lib.oops_trimul_output_forward(ctypes.byref(tg), fake, fake, fake, fake, None, None, fake, None) != 0
+    tg.c_row, tg.has_mask = 16, 1  # a mask flag without a mask pointer
+    assert lib.oops_trimul_factors_forward(ctypes.byref(tg), fake, fake, None, None, fake, None) != 0
+    assert b"mask" in lib.oops_last_error()
+    tg.has_mask = 0
+    assert lib.oops_trimul_mask_parts(ctypes.byref(tg)) == 2
+    assert lib.oops_trimul_bias_parts(ctypes.byref(tg)) >= 1
+    assert lib.oops_trimul_output_norm_parts(ctypes.byref(tg)) >= 1
