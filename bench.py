@@ -375,6 +375,34 @@ def trimul_stage(device, n=512, c=128, h=128):
     }
 
 
+def layer_norm_stage(device, rows=512 * 512, width=128):
+    """layer_norm fwd+bwd over 262144 x 128 bf16 rows (the pair LayerNorm at N=512) with float32 affine;
+    HBM rate of the forward (x read, y written) and backward (x, dy read, dx written) against 8 TB/s."""
+
+    import torch
+
+    from oops_amd import layer_norm
+
+    g = torch.Generator().manual_seed(14)
+    x = torch.randn(rows, width, generator=g).to(torch.bfloat16).to(device).requires_grad_(True)
+    w = torch.randn(width, generator=g).to(device).requires_grad_(True)
+    b = torch.randn(width, generator=g).to(device).requires_grad_(True)
+    dy = torch.randn(rows, width, generator=g).to(torch.bfloat16).to(device)
+    with torch.no_grad():
+        ms_fwd = _median_ms(lambda: layer_norm(x, width, w, b), iters=20, warmup=3)
+    y = layer_norm(x, width, w, b)
+    ms_bwd = _median_ms(lambda: torch.autograd.grad(y, [x, w, b], dy, retain_graph=True), iters=20, warmup=3)
+    nbytes = rows * width * 2
+    return {
+        "workload": f"layer_norm {rows} x {width} bf16, float32 affine",
+        "ms_fwd": round(ms_fwd, 4),
+        "fwd_gbps": round(2 * nbytes / (ms_fwd * 1e-3) / 1e9, 1),
+        "ms_bwd": round(ms_bwd, 4),
+        "bwd_gbps": round(3 * nbytes / (ms_bwd * 1e-3) / 1e9, 1),
+        "peak_gbps": 8000.0,
+    }
+
+
 def gate_stage(device):
     """The gated output stage (the row after attention) at config 4's MSA shape.
 
@@ -486,6 +514,11 @@ def main():
         help="only copy a 256 MiB device buffer 3 times (scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)",
     )
     ap.add_argument(
+        "--only",
+        choices=("nested_msa", "layer_norm"),
+        help="only measure one of the rows beside attention (3 repetitions) and print its JSON",
+    )
+    ap.add_argument(
         "--trimul-only",
         action="store_true",
         help="only measure triangle_multiplication (N=512, C=H=128, 3 repetitions) and print its JSON",
@@ -519,6 +552,12 @@ def main():
     _lib.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.only:
+        fn = {"nested_msa": nested_msa, "layer_norm": layer_norm_stage}[args.only]
+        for _ in range(3):
+            res = fn(dev)
+        print(json.dumps(res))
+        return
     if args.trimul_only:
         for _ in range(3):
             res = trimul_stage(dev)
@@ -598,7 +637,7 @@ def main():
         _log("bench: " + json.dumps(line["other_configs"]))
         _log("bench: gated output stage")
         line["next_rows"] = {"gate_c4_shape": gate_stage(dev), "nested_msa": nested_msa(dev),
-                             "trimul_n512": trimul_stage(dev)}
+                             "trimul_n512": trimul_stage(dev), "layer_norm": layer_norm_stage(dev)}
         _log("bench: " + json.dumps(line["next_rows"]))
     if not args.no_cpu:
         _log("bench: cpu baseline")
