@@ -389,32 +389,49 @@ __global__ __launch_bounds__(256) void trimul_factor_kernel(FactorArgs a) {
 
   float bsum[2][2] = {{0.f, 0.f}, {0.f, 0.f}};  // [t][value, gate] over this lane's tokens
   const int tpw = FULLW ? a.tpw : 1;
+  const uint32_t x_lane = (uint32_t)((wave * 32 + lq) * a.c_row * 2);
+  // the token rows of the tile at r0 as one buffer resource; rv: this lane's row exists
+  auto tile_x = [&](int64_t r0, __amdgpu_buffer_rsrc_t& xr, bool& rv) {
+    const int64_t rows_left = R - r0;
+    const int nrows = (int)(rows_left < kFM ? rows_left : kFM);
+    xr = make_rsrc(static_cast<const T*>(a.xn) + r0 * a.c_row, (uint32_t)((int64_t)nrows * a.c_row * 2));
+    rv = wave * 32 + lq < nrows;
+  };
+  auto load_x_of = [&](const __amdgpu_buffer_rsrc_t& xr, bool rv, int k0, uint4 (&xf)[4]) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int k = k0 + 16 * c + 8 * g2;
+      xf[c] = buffer_load16(xr, rv && k < K ? x_lane + (uint32_t)(k * 2) : kOut);
+    }
+  };
+  uint4 xf[4];
+  bool prefetched = false;  // xf holds this tile's first panel, loaded during the previous epilogue
+  // (group, position) of this lane's first token r0 + 32 wave + 4 g2: one 64-bit division per
+  // workgroup, then stepped forward by 128 tokens per tile
+  int64_t g_cur, p_cur;
+  {
+    const int64_t rb = bmg * tpw * kFM + wave * 32 + 4 * g2;
+    g_cur = rb / P;
+    p_cur = rb - g_cur * P;
+  }
+  const int64_t fG = (int64_t)f * a.groups;
   for (int it = 0; it < tpw; ++it) {
     const int64_t r0 = (bmg * tpw + it) * kFM;
     if (r0 >= R) break;
-    const int64_t rows_left = R - r0;
-    const int nrows = (int)(rows_left < kFM ? rows_left : kFM);
-    const __amdgpu_buffer_rsrc_t xr =
-        make_rsrc(static_cast<const T*>(a.xn) + r0 * a.c_row, (uint32_t)((int64_t)nrows * a.c_row * 2));
-    const bool rv = wave * 32 + lq < nrows;
-    const uint32_t x_lane = (uint32_t)((wave * 32 + lq) * a.c_row * 2);
-    auto load_x = [&](int k0, uint4 (&xf)[4]) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int k = k0 + 16 * c + 8 * g2;
-        xf[c] = buffer_load16(xr, rv && k < K ? x_lane + (uint32_t)(k * 2) : kOut);
-      }
-    };
+    __amdgpu_buffer_rsrc_t xr;
+    bool rv;
+    tile_x(r0, xr, rv);
+    auto load_x = [&](int k0, uint4 (&dst)[4]) { load_x_of(xr, rv, k0, dst); };
 
     f32x16 acc[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[t] = f32x16{};
-    uint4 xf[4], xn[4], wu[4];
+    uint4 xn[4], wu[4];
     if constexpr (!FULLW) {
       load_w(0, wu);
       store_w(0, wu);
     }
-    load_x(0, xf);
+    if (!prefetched) load_x(0, xf);
     if constexpr (!FULLW) __syncthreads();
     for (int i = 0; i < npanels; ++i) {
       const bool more = i + 1 < npanels;
@@ -437,24 +454,35 @@ __global__ __launch_bounds__(256) void trimul_factor_kernel(FactorArgs a) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) xf[c] = xn[c];
     }
+    if constexpr (FULLW) {
+      // the next tile's first panel loads while this tile's epilogue runs
+      const int64_t rn = r0 + kFM;
+      prefetched = it + 1 < tpw && rn < R;
+      if (prefetched) {
+        __amdgpu_buffer_rsrc_t xr_n;
+        bool rv_n;
+        tile_x(rn, xr_n, rv_n);
+        load_x_of(xr_n, rv_n, 0, xf);
+      }
+    }
 
     // ---- epilogue: tile t in {0, 1} holds value channel cb*64 + 32t + lq (tile t+2 its gate)
     // for tokens r0 + 32 wave + 8q + 4 g2 + i
     const bool vec4 = (P & 3) == 0;  // 4 tokens from a multiple of 4 share a group, 8-byte aligned
     const float* mask = a.mask;
-    // (group, position) of this lane's first token r0 + 32 wave + 4 g2 (one 64-bit division per
-    // tile); the tokens 8q further on step forward from it
-    int64_t g_q[4], p_q[4];
+    // element offset of channel 0 for the tokens 8q further on: ((f G + g) H) P + p, to which a
+    // channel adds hv P
+    int64_t base_q[4];
     {
-      const int64_t rb = r0 + wave * 32 + 4 * g2;
-      int64_t g = rb / P, p = rb - g * P;
+      int64_t g = g_cur, p = p_cur;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        g_q[q] = g;
-        p_q[q] = p;
+        base_q[q] = (fG + g) * H * P + p;
         p += 8;
         while (p >= P) p -= P, ++g;
       }
+      p_cur += kFM;
+      while (p_cur >= P) p_cur -= P, ++g_cur;
     }
     // every load of the epilogue is issued before its first store (a store could alias a later
     // load, so loads interleaved with stores would each wait a full memory round trip)
@@ -475,7 +503,7 @@ __global__ __launch_bounds__(256) void trimul_factor_kernel(FactorArgs a) {
           for (int q = 0; q < 4; ++q) {
             const int64_t r4 = r0 + wave * 32 + 8 * q + 4 * g2;
             dpre[t][q] = hv < H && r4 < R
-                             ? *reinterpret_cast<const uint2*>(gf + ((f * a.groups + g_q[q]) * H + hv) * P + p_q[q])
+                             ? *reinterpret_cast<const uint2*>(gf + base_q[q] + (int64_t)hv * P)
                              : make_uint2(0, 0);
           }
         }
@@ -519,7 +547,7 @@ __global__ __launch_bounds__(256) void trimul_factor_kernel(FactorArgs a) {
         if constexpr (!BWD) {
           T* out = static_cast<T*>(a.factors);
           if (vec4) {
-            const int64_t off = ((f * a.groups + g_q[q]) * H + hv) * P + p_q[q];
+            const int64_t off = base_q[q] + (int64_t)hv * P;
             *reinterpret_cast<uint2*>(out + off) =
                 make_uint2(pack2<T>(v[0] * sg[0] * keep[0], v[1] * sg[1] * keep[1]),
                            pack2<T>(v[2] * sg[2] * keep[2], v[3] * sg[3] * keep[3]));
