@@ -590,18 +590,17 @@ __global__ __launch_bounds__(256) void trimul_factor_kernel(FactorArgs a) {
             const uint2 ug = make_uint2(pack2<T>(dg[0], dg[1]), pack2<T>(dg[2], dg[3]));
             *reinterpret_cast<uint2*>(gv) = uv;
             *reinterpret_cast<uint2*>(gg) = ug;
-            // the bias gradient sums the stored (rounded) values, as a reduction of grad_proj would
-            bsum[t][0] += lo_f<T>(uv.x) + hi_f<T>(uv.x) + lo_f<T>(uv.y) + hi_f<T>(uv.y);
-            bsum[t][1] += lo_f<T>(ug.x) + hi_f<T>(ug.x) + lo_f<T>(ug.y) + hi_f<T>(ug.y);
+            // the bias gradient sums the float32 values (before their rounding to the dtype)
+            bsum[t][0] += (dv[0] + dv[1]) + (dv[2] + dv[3]);
+            bsum[t][1] += (dg[0] + dg[1]) + (dg[2] + dg[3]);
           } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
               if (i < left) {
-                const T tv = (T)dv[i], tg = (T)dg[i];
-                gv[i] = tv;
-                gg[i] = tg;
-                bsum[t][0] += to_f(tv);
-                bsum[t][1] += to_f(tg);
+                gv[i] = (T)dv[i];
+                gg[i] = (T)dg[i];
+                bsum[t][0] += dv[i];
+                bsum[t][1] += dg[i];
               }
           }
         }
@@ -1205,10 +1204,13 @@ hipError_t launch_trimul_factors(const oops_trimul_geometry& g, const void* norm
 }
 
 namespace {
+#ifndef OOPS_OUTNORM_NPB
+#define OOPS_OUTNORM_NPB 32
+#endif
 // positions per output-norm workgroup: a divisor of 256 whose LDS tiles fit
 int out_norm_npb(int H, bool backward) {
   const int tiles = backward ? 2 : 1;
-  int npb = 64;
+  int npb = OOPS_OUTNORM_NPB;
   while (npb > 1 && (int64_t)tiles * H * (npb + 1) * 4 > 64 * 1024) npb /= 2;
   return npb;
 }
