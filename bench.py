@@ -367,11 +367,53 @@ def trimul_stage(device, n=512, c=128, h=128):
     rows = n * n
     fwd_flops = 2 * rows * c * 4 * h + 2 * h * n**3 + 2 * rows * (h + c) * c
     flops = 3 * fwd_flops  # backward: two products per forward product
+
+    # the factor projection kernels alone (the largest HIP kernels of the update), through the C ABI on
+    # the operator's own prepared operands, against HBM: forward reads xn and writes both factors,
+    # backward also reads the factor gradients and writes the [4H][R] projection gradients
+    import ctypes
+    import importlib
+
+    from oops_amd import _lib
+
+    tm = importlib.import_module("oops_amd.pair.triangle_multiplication")
+    lib = _lib.load()
+    with torch.no_grad():
+        grouped = pair.detach().reshape(1, rows, c)
+        ops = tm._prepare(grouped, mask.reshape(1, rows), tuple(list(w.values())[:10]), tuple(list(w.values())[10:]))
+        _pair, mask32, w_cat, b_cat = ops[:4]
+        saved = tm.trimul_forward(*ops, [0, n], "outgoing", 1e-5, 1e-5)
+        xn, factors = saved[1], saved[4]
+        geo = tm._geometry(grouped, h, True, 1e-5)
+        stream = torch.cuda.current_stream().cuda_stream
+        d_fac = torch.randn_like(factors)
+        d_proj = torch.empty(4 * h, rows, dtype=dt, device=device)
+        bparts = torch.empty(lib.oops_trimul_bias_parts(ctypes.byref(geo)), 4 * h, device=device)
+        ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+
+        def f_fwd():
+            lib.oops_trimul_factors_forward(ctypes.byref(geo), ptr(xn), ptr(w_cat), ptr(b_cat), ptr(mask32),
+                                            ptr(factors), stream)  # fmt: skip
+
+        def f_bwd():
+            lib.oops_trimul_factors_backward(ctypes.byref(geo), ptr(xn), ptr(w_cat), ptr(b_cat), ptr(mask32),
+                                             ptr(d_fac), ptr(d_proj), None, ptr(bparts), stream)  # fmt: skip
+
+        k_fwd = _median_ms(f_fwd, iters=20, warmup=3)
+        k_bwd = _median_ms(f_bwd, iters=20, warmup=3)
+    el = 2
+    fwd_bytes = rows * c * el + 2 * h * rows * el
+    bwd_bytes = rows * c * el + 2 * h * rows * el + 4 * h * rows * el
+    kern = lambda ms_, b_: {"ms": round(ms_, 4), "achieved_gbps": round(b_ / (ms_ * 1e-3) / 1e9, 1),  # noqa: E731
+                            "frac": round(b_ / (ms_ * 1e-3) / 1e9 / 8000.0, 4)}  # fmt: skip
     return {
         "workload": f"triangle_multiplication outgoing fwd+bwd, N={n}, C=H={c}, bf16, mask, biases",
         "ms_fwd_bwd": round(ms, 4),
         "ms_fwd": round(ms_fwd, 4),
         "tflops_fwd_bwd": round(flops / ms / 1e9, 2),
+        "factor_kernel_fwd": kern(k_fwd, fwd_bytes),
+        "factor_kernel_bwd": kern(k_bwd, bwd_bytes),
+        "roofline_bound": "hbm",
     }
 
 
