@@ -97,6 +97,9 @@ def _check(pair, mask, weights, bs, direction, dtype, grads=True, mask_grad=Fals
         (torch.float16, 65, 96, 17, (), "incoming", True),
         (torch.bfloat16, 128, 128, 19, (2, 3), "outgoing", False),
         (torch.bfloat16, 128, 128, 64, (1,), "incoming", True),
+        (torch.bfloat16, 384, 384, 33, (), "outgoing", False),  # c_row > 256: W streamed through LDS
+        (torch.float16, 1024, 8, 5, (), "incoming", True),  # widest pair, narrow hidden
+        (torch.bfloat16, 8, 1024, 5, (), "outgoing", True),  # widest hidden (few positions per LDS tile)
         (torch.float32, 17, 24, 7, (2,), "outgoing", True),
         (torch.float32, 8, 12, 9, (), "incoming", False),
     ],
