@@ -201,7 +201,7 @@ int oops_gate_multiply_backward(const oops_gate_geometry* geo, const void* atten
  * padded y feeds 16-byte MFMA operand loads. */
 typedef struct oops_row_norm_geometry {
   int32_t dtype; /* x and y: OOPS_F32 / OOPS_BF16 / OOPS_F16 */
-  int32_t width; /* 1..4096 */
+  int32_t width; /* 1..8192 */
   int64_t rows;
   int64_t x_row; /* x row stride in elements */
   int64_t y_row; /* y row stride in elements (>= width) */

@@ -237,11 +237,11 @@ int check_row_norm(const oops_row_norm_geometry* g) {
   if (g == nullptr) return fail(OOPS_EINVAL, "row-norm geometry is NULL");
   if (g->dtype != OOPS_BF16 && g->dtype != OOPS_F16 && g->dtype != OOPS_F32)
     return fail(OOPS_EINVAL, "unknown dtype %lld", g->dtype);
-  if (g->width <= 0 || g->width > 4096) return fail(OOPS_EINVAL, "width must be in 1..4096, got %lld", g->width);
+  if (g->width <= 0 || g->width > 8192) return fail(OOPS_EINVAL, "width must be in 1..8192, got %lld", g->width);
   if (g->rows < 0) return fail(OOPS_EINVAL, "rows must be >= 0");
   if (g->x_row < g->width || g->y_row < g->width)
     return fail(OOPS_EINVAL, "row strides (%lld, %lld) must cover the width", g->x_row, g->y_row);
-  if (g->y_row > 4096) return fail(OOPS_EINVAL, "y row stride too large (%lld)", g->y_row);
+  if (g->y_row > 8192) return fail(OOPS_EINVAL, "y row stride too large (%lld)", g->y_row);
   return OOPS_OK;
 }
 

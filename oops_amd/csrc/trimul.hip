@@ -1111,6 +1111,7 @@ hipError_t run_rows(const oops_row_norm_geometry& g, bool backward, RowNormArgs&
       case 2: return launch_rows<T, 2>(backward, pl.vec, pl.blocks, a, stream);
       case 4: return launch_rows<T, 4>(backward, pl.vec, pl.blocks, a, stream);
       case 8: return launch_rows<T, 8>(backward, pl.vec, pl.blocks, a, stream);
+      case 16: return launch_rows<T, 16>(backward, pl.vec, pl.blocks, a, stream);  // widths above 4096
       default: return hipErrorInvalidValue;
     }
   });

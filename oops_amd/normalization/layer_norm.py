@@ -3,7 +3,7 @@
 Drop-in for the reference's operator
 (oops/normalization/layer_norm/layer_norm.py:30-148): dense or DanLing
 nested input whose normalized (final) axis is static and physically last,
-float16 / bfloat16 / float32 activations, optional affine parameters in the
+float16 / bfloat16 / float32 activations, widths 1-8192, optional affine parameters in the
 activation dtype (or float32 over half activations).  Forward and backward run
 in ``row_norm_*_kernel`` behind ``oops_layer_norm_rows_forward/backward``
 (float32 statistics, biased variance); the affine gradients are float32
@@ -26,7 +26,7 @@ from ..attention._runtime import is_nested, require_no_forward_mode, require_sam
 _OPERATOR = "layer_norm"
 _HALF = (torch.float16, torch.bfloat16)
 _DTYPE_CODE = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
-MAX_WIDTH = 4096
+MAX_WIDTH = 8192
 
 
 def layer_norm(
@@ -41,7 +41,7 @@ def layer_norm(
     Args:
         input: CUDA float16 / bfloat16 / float32 ``(..., C)`` tensor, or a
             nested tensor whose final feature axis is static and physically last.
-        normalized_shape: ``C`` or ``(C,)`` with ``1 <= C <= 4096``.
+        normalized_shape: ``C`` or ``(C,)`` with ``1 <= C <= 8192``.
         weight, bias: optional ``(C,)`` affine parameters in the activation
             dtype, or float32 for half activations.
         eps: added to the variance before the reciprocal square root.

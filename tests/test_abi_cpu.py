@@ -181,7 +181,7 @@ def test_row_norm_and_trimul_validation(lib):
     assert b"width" in lib.oops_last_error()
     rg.width, rg.y_row = 8, 4  # y row stride below the width
     assert lib.oops_layer_norm_rows_forward(ctypes.byref(rg), fake, None, None, fake, fake, fake, None) != 0
-    rg.width, rg.y_row, rg.x_row = 5000, 5000, 5000
+    rg.width, rg.y_row, rg.x_row = 9000, 9000, 9000
     assert lib.oops_layer_norm_rows_parts(ctypes.byref(rg)) == 0
 
     tg = _lib.TrimulGeometry()

@@ -2,7 +2,7 @@
 
 Follows the reference's layer_norm contract (oops/normalization/layer_norm/
 layer_norm.py:30-148): float16 / bfloat16 / float32 activations, widths from 1
-to 4096 (odd and non-multiple-of-8 widths take the element path), affine in
+to 8192 (odd and non-multiple-of-8 widths take the element path), affine in
 the activation dtype, float32 over half, or absent; strided rows; nested
 values.  Values and the input gradient are compared elementwise; the affine
 gradients (sums over every row) with the tolerance scaled by their largest
@@ -34,7 +34,7 @@ def _grad_close(got, want, dtype, what):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("width", [1, 17, 128, 384, 4096])
+@pytest.mark.parametrize("width", [1, 17, 128, 384, 4096, 8192])
 @pytest.mark.parametrize("affine", ["same", "f32", "none"])
 def test_layer_norm(dtype, width, affine):
     if affine == "f32" and dtype == torch.float32:
@@ -88,7 +88,7 @@ def test_layer_norm_errors():
     with pytest.raises(OOpsUnsupportedError):
         layer_norm(x, 8, torch.ones(8, device=DEV, dtype=torch.bfloat16))  # half affine over float32
     with pytest.raises(OOpsUnsupportedError):
-        layer_norm(torch.randn(4, 5000, device=DEV), 5000)
+        layer_norm(torch.randn(4, 9000, device=DEV), 9000)
 
 
 def test_layer_norm_compile_matches_eager():
