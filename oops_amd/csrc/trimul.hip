@@ -293,6 +293,19 @@ __global__ __launch_bounds__(256) void row_norm_backward_kernel(RowNormArgs a) {
   }
 }
 
+// Packed pairs p[2q], p[2q+1] of a lane's tokens 8q + 4g .. 8q + 4g + 3 (q = 0..3, g = lane / 32) are
+// traded between the two 32-lane halves with v_permlane32_swap: afterwards the lower half holds
+// tokens 0..15 and the upper half tokens 16..31, lo = the first 8 and hi = the next 8 (one 32-byte
+// run per lane).  Every lane of the wave must execute it.
+__device__ __forceinline__ void trade16(const uint32_t (&p)[8], uint4& lo, uint4& hi) {
+  const auto x0 = __builtin_amdgcn_permlane32_swap(p[0], p[4], false, false);
+  const auto x1 = __builtin_amdgcn_permlane32_swap(p[1], p[5], false, false);
+  const auto x2 = __builtin_amdgcn_permlane32_swap(p[2], p[6], false, false);
+  const auto x3 = __builtin_amdgcn_permlane32_swap(p[3], p[7], false, false);
+  lo = make_uint4(x0[0], x1[0], x0[1], x1[1]);
+  hi = make_uint4(x2[0], x3[0], x2[1], x3[1]);
+}
+
 // ------------------------------------------------------------------ factors
 struct FactorArgs {
   const void* xn;
@@ -310,7 +323,10 @@ struct FactorArgs {
 
 constexpr int kFM = 128;  // tokens per tile (32 per wave)
 constexpr int kFK = 64;   // k per panel / step
-constexpr int kFullWMaxK = 256;  // the whole W block stays in LDS up to this c_row
+#ifndef OOPS_FACTOR_FULLW_MAX_K
+#define OOPS_FACTOR_FULLW_MAX_K 256
+#endif
+constexpr int kFullWMaxK = OOPS_FACTOR_FULLW_MAX_K;  // the whole W block stays in LDS up to this c_row
 
 template <typename T>
 __device__ __forceinline__ void load4(const T* p, bool vec, int64_t left, float (&x)[4]) {
@@ -328,8 +344,12 @@ __device__ __forceinline__ void load4(const T* p, bool vec, int64_t left, float 
 // gate) x c_row are loaded into LDS once, as 64-wide swizzled panels, and
 // every token tile reuses them with no further barrier; otherwise W streams
 // through a two-buffer LDS tile per tile (TPW = 1).
+// streamed W: three workgroups per CU; W kept whole in LDS: two
+#ifndef OOPS_FACTOR_BWD_OCC
+#define OOPS_FACTOR_BWD_OCC 3
+#endif
 template <typename T, bool BWD, bool FULLW>
-__global__ __launch_bounds__(256) void trimul_factor_kernel(FactorArgs a) {
+__global__ __launch_bounds__(256, FULLW ? 2 : OOPS_FACTOR_BWD_OCC) void trimul_factor_kernel(FactorArgs a) {
   using E = Elem<T>;
   using Frag = typename E::Frag;
   constexpr int WT = 128 * kFK;  // one panel: 128 rows x 64 k
@@ -469,6 +489,8 @@ __global__ __launch_bounds__(256) void trimul_factor_kernel(FactorArgs a) {
     // ---- epilogue: tile t in {0, 1} holds value channel cb*64 + 32t + lq (tile t+2 its gate)
     // for tokens r0 + 32 wave + 8q + 4 g2 + i
     const bool vec4 = (P & 3) == 0;  // 4 tokens from a multiple of 4 share a group, 8-byte aligned
+    // 16 tokens from a multiple of 16 share a group: the halves trade values so each lane stores 32 bytes
+    const bool vec16 = (P & 15) == 0;
     const float* mask = a.mask;
     // element offset of channel 0 for the tokens 8q further on: ((f G + g) H) P + p, to which a
     // channel adds hv P
@@ -524,6 +546,8 @@ __global__ __launch_bounds__(256) void trimul_factor_kernel(FactorArgs a) {
       const int hv = cb * 64 + 32 * t + lq;
       if (hv >= H) continue;
       const float bv = bvs[t], bg = bgs[t];
+      // vec16: packed pairs of this lane's tokens 8q + 4 g2 .. +3 (pair 2q: first two), stored after the loop
+      uint32_t po[8] = {0, 0, 0, 0, 0, 0, 0, 0}, pg[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int64_t r4 = r0 + wave * 32 + 8 * q + 4 * g2;
@@ -547,10 +571,12 @@ __global__ __launch_bounds__(256) void trimul_factor_kernel(FactorArgs a) {
         if constexpr (!BWD) {
           T* out = static_cast<T*>(a.factors);
           if (vec4) {
-            const int64_t off = base_q[q] + (int64_t)hv * P;
-            *reinterpret_cast<uint2*>(out + off) =
-                make_uint2(pack2<T>(v[0] * sg[0] * keep[0], v[1] * sg[1] * keep[1]),
-                           pack2<T>(v[2] * sg[2] * keep[2], v[3] * sg[3] * keep[3]));
+            po[2 * q] = pack2<T>(v[0] * sg[0] * keep[0], v[1] * sg[1] * keep[1]);
+            po[2 * q + 1] = pack2<T>(v[2] * sg[2] * keep[2], v[3] * sg[3] * keep[3]);
+            if (!vec16) {
+              const int64_t off = base_q[q] + (int64_t)hv * P;
+              *reinterpret_cast<uint2*>(out + off) = make_uint2(po[2 * q], po[2 * q + 1]);
+            }
           } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -586,10 +612,12 @@ __global__ __launch_bounds__(256) void trimul_factor_kernel(FactorArgs a) {
           T* gv = gp + (int64_t)(f * 2 * H + hv) * R + r4;
           T* gg = gp + (int64_t)(f * 2 * H + H + hv) * R + r4;
           if (vec4) {
-            const uint2 uv = make_uint2(pack2<T>(dv[0], dv[1]), pack2<T>(dv[2], dv[3]));
-            const uint2 ug = make_uint2(pack2<T>(dg[0], dg[1]), pack2<T>(dg[2], dg[3]));
-            *reinterpret_cast<uint2*>(gv) = uv;
-            *reinterpret_cast<uint2*>(gg) = ug;
+            po[2 * q] = pack2<T>(dv[0], dv[1]), po[2 * q + 1] = pack2<T>(dv[2], dv[3]);
+            pg[2 * q] = pack2<T>(dg[0], dg[1]), pg[2 * q + 1] = pack2<T>(dg[2], dg[3]);
+            if (!vec16) {
+              *reinterpret_cast<uint2*>(gv) = make_uint2(po[2 * q], po[2 * q + 1]);
+              *reinterpret_cast<uint2*>(gg) = make_uint2(pg[2 * q], pg[2 * q + 1]);
+            }
             // the bias gradient sums the float32 values (before their rounding to the dtype)
             bsum[t][0] += (dv[0] + dv[1]) + (dv[2] + dv[3]);
             bsum[t][1] += (dg[0] + dg[1]) + (dg[2] + dg[3]);
@@ -602,6 +630,30 @@ __global__ __launch_bounds__(256) void trimul_factor_kernel(FactorArgs a) {
                 bsum[t][0] += dv[i];
                 bsum[t][1] += dg[i];
               }
+          }
+        }
+      }
+      if (vec16) {
+        // lane (lq, g2) stores tokens 16 g2 .. 16 g2 + 15 of the wave's 32 (wholly in or past R);
+        // the trade runs in every lane, the stores only where the tokens exist
+        uint4 lo, hi, glo, ghi;
+        trade16(po, lo, hi);
+        if constexpr (BWD) trade16(pg, glo, ghi);
+        const int64_t r16 = r0 + wave * 32 + 16 * g2;
+        if (r16 < R) {
+          if constexpr (!BWD) {
+            // base_q[2] of an upper lane is token 20: token 16 is 4 positions before it in the same group
+            T* dst = static_cast<T*>(a.factors) + (g2 ? base_q[2] - 4 : base_q[0]) + (int64_t)hv * P;
+            *reinterpret_cast<uint4*>(dst) = lo;
+            *reinterpret_cast<uint4*>(dst + 8) = hi;
+          } else {
+            T* gp = static_cast<T*>(a.grad_proj);
+            T* dv16 = gp + (int64_t)(f * 2 * H + hv) * R + r16;
+            T* dg16 = gp + (int64_t)(f * 2 * H + H + hv) * R + r16;
+            *reinterpret_cast<uint4*>(dv16) = lo;
+            *reinterpret_cast<uint4*>(dv16 + 8) = hi;
+            *reinterpret_cast<uint4*>(dg16) = glo;
+            *reinterpret_cast<uint4*>(dg16 + 8) = ghi;
           }
         }
       }
