@@ -338,13 +338,14 @@ def _setup_context(ctx, inputs, output):
     ctx.bias_shape = None if bias is None else bias.shape
     ctx.bias_dtype = None if bias is None else bias.dtype
     ctx.mark_non_differentiable(out_lo, lse)
+    ctx.set_materialize_grads(False)  # no zero-filled gradients for the residual and LSE outputs
 
 
 def _backward(ctx, dout, dout_lo, dlse):
     q, k, v, mask, bias, out, out_lo, lse = ctx.saved_tensors
     need_q, need_k, need_v, _, need_b = ctx.needs_input_grad[:5]
     need_b = bool(need_b and bias is not None)
-    if not (need_q or need_k or need_v or need_b):
+    if dout is None or not (need_q or need_k or need_v or need_b):
         return (None,) * 10
     dbias_numel = 0 if bias is None else bias.numel()
     dq, dk, dv, dbias = attention_backward(

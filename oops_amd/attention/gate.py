@@ -199,9 +199,12 @@ def _setup_context(ctx, inputs, output):
     _gated, logits = output
     ctx.save_for_backward(attention, single, weight, logits)
     ctx.mark_non_differentiable(logits)
+    ctx.set_materialize_grads(False)  # no zero-filled gradient for the logits output
 
 
 def _backward(ctx, grad_gated, _grad_logits):
+    if grad_gated is None:
+        return None, None, None, None
     attention, single, weight, logits = ctx.saved_tensors
     need_att, need_single, need_weight = ctx.needs_input_grad[:3]
     need_logits = need_single or need_weight

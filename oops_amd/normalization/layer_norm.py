@@ -184,9 +184,12 @@ def _setup_context(ctx, inputs, output):
     ctx.eps = eps
     ctx.has = (weight is not None, bias is not None)
     ctx.mark_non_differentiable(mean, rstd)
+    ctx.set_materialize_grads(False)  # no zero-filled gradients for mean and rstd
 
 
 def _backward(ctx, dy, _dmean, _drstd):
+    if dy is None:
+        return None, None, None, None
     x, weight, mean, rstd = ctx.saved_tensors
     need = ctx.needs_input_grad
     need_affine = bool(need[1] or need[2])

@@ -518,9 +518,12 @@ def _setup_context(ctx, inputs, output):
     ctx.optional = (mask is not None, b_cat is not None, bo is not None, bog is not None)
     for t in output[1:]:
         ctx.mark_non_differentiable(t)
+    ctx.set_materialize_grads(False)  # no zero-filled gradients for the saved intermediates
 
 
 def _backward(ctx, dout, *_unused):
+    if dout is None:
+        return (None,) * 16
     saved = ctx.saved_tensors
     blocks, direction, eps_in, eps_out = ctx.args
     need = ctx.needs_input_grad
