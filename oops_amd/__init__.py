@@ -6,10 +6,11 @@ is the drop-in for ``from oops import ...`` on the attention path.
 
 from ._errors import OOpsUnsupportedError
 from .attention import gate_attention_output, gated_pair_bias_attention, pair_bias_attention, triangle_attention
-from .normalization import layer_norm
+from .normalization import LayerNorm, layer_norm
 from .pair import triangle_multiplication
 
 __all__ = [
+    "LayerNorm",
     "OOpsUnsupportedError",
     "gate_attention_output",
     "gated_pair_bias_attention",

@@ -74,29 +74,64 @@ class force_generic:
 
 # ----------------------------------------------------------------- tables
 
-_TABLE_CACHE: "OrderedDict[tuple, tuple[Tensor, Tensor]]" = OrderedDict()
-_TABLE_CACHE_SIZE = 512
+class _TableCache:
+    """Least-recently-used cache of geometry tables, except that an entry used
+    while the current stream is being captured into a graph is pinned for the
+    life of the process: the graph holds the device copy's address and replays
+    read it long after the call that built it."""
+
+    def __init__(self, size: int, make):
+        self.size = size
+        self.make = make  # key -> (host copy, device copy)
+        self.lru: "OrderedDict[tuple, tuple]" = OrderedDict()
+        self.pinned: dict = {}
+
+    def get(self, key: tuple, capturing: bool) -> tuple:
+        hit = self.pinned.get(key)
+        if hit is not None:
+            return hit
+        hit = self.lru.get(key)
+        if hit is None:
+            hit = self.make(key)
+        else:
+            del self.lru[key]
+        if capturing:
+            self.pinned[key] = hit
+            return hit
+        self.lru[key] = hit
+        while len(self.lru) > self.size:
+            self.lru.popitem(last=False)
+        return hit
+
+
+def _make_table(key: tuple) -> tuple:
+    device = torch.device("cuda", key[0])
+    host = torch.tensor(key[1], dtype=torch.int64).pin_memory()
+    dev = torch.empty(host.shape, dtype=torch.int64, device=device)
+    dev.copy_(host, non_blocking=True)
+    # (host, device copy, streams the device copy is recorded on)
+    return host, dev, {torch.cuda.current_stream(device).cuda_stream}
+
+
+_TABLES = _TableCache(512, _make_table)
 
 
 def device_table(table: Sequence[int], device: torch.device) -> tuple[Tensor, Tensor]:
     """(pinned host copy, device copy) of a geometry table, cached by value.
 
     The device copy is filled from pinned memory with an async copy, which is
-    legal under CUDA-graph capture; cached entries are reused unchanged, so a
-    captured graph keeps reading valid memory.
+    legal under CUDA-graph capture.  Entries are reused unchanged; one used
+    under capture is never evicted, and the device copy is recorded on every
+    stream that reads it, so its memory is not handed out again while a
+    launch on another stream may still read it.
     """
 
     key = (device.index, tuple(int(x) for x in table))
-    hit = _TABLE_CACHE.get(key)
-    if hit is not None:
-        _TABLE_CACHE.move_to_end(key)
-        return hit
-    host = torch.tensor(key[1], dtype=torch.int64).pin_memory()
-    dev = torch.empty(host.shape, dtype=torch.int64, device=device)
-    dev.copy_(host, non_blocking=True)
-    _TABLE_CACHE[key] = (host, dev)
-    while len(_TABLE_CACHE) > _TABLE_CACHE_SIZE:
-        _TABLE_CACHE.popitem(last=False)
+    host, dev, streams = _TABLES.get(key, torch.cuda.is_current_stream_capturing())
+    stream = torch.cuda.current_stream(device)
+    if stream.cuda_stream not in streams:
+        dev.record_stream(stream)
+        streams.add(stream.cuda_stream)
     return host, dev
 
 

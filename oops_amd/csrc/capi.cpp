@@ -175,7 +175,7 @@ int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
       track(c, c_red, u_red);
     }
     plan.sred_uniform = u_red && c_red > 0 ? c_red : 0;
-    if (plan.sbias_tiles > kMaxGrid || plan.sred_tiles > kMaxGrid)
+    if (plan.sbias_tiles > kMaxGrid || plan.fast_sbias_tiles > kMaxGrid || plan.sred_tiles > kMaxGrid)
       return fail(OOPS_EINVAL, "dBias launch grid exceeds 2^31-1 workgroups");
   }
   // fragment-major copy of the shared biases for the fast kernels: one slab

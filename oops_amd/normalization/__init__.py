@@ -1,5 +1,6 @@
 """Normalization operators (the reference's ``oops.normalization``)."""
 
 from .layer_norm import layer_norm
+from .modules import LayerNorm
 
-__all__ = ["layer_norm"]
+__all__ = ["LayerNorm", "layer_norm"]

@@ -183,3 +183,25 @@ def test_dout_table_remap(make_dout, remapped):
     got = flat[dout.storage_offset() + off + g * sg + hh * sh + i * si + d]
     torch.testing.assert_close(got, dout, rtol=0, atol=0)
     assert new[: _lib.T_DO_OFF] == table[: _lib.T_DO_OFF]
+
+
+def test_table_cache_pins_entries_used_under_capture():
+    """A geometry table first used while a graph is being captured stays cached (a replay reads its
+    device copy) however many other tables follow; ordinary entries are evicted least-recently-used."""
+
+    from oops_amd.attention._core import _TableCache
+
+    made = []
+    cache = _TableCache(4, lambda key: made.append(key) or ("host", key, set()))
+    captured = cache.get((0, (1, 2)), capturing=True)
+    for i in range(600):
+        cache.get((0, (i, 9)), capturing=False)
+    assert cache.get((0, (1, 2)), capturing=False) is captured
+    assert made.count((0, (1, 2))) == 1
+    assert len(cache.lru) == 4
+    # an entry cached before capture is pinned when a capture uses it
+    early = cache.get((0, (7, 7)), capturing=False)
+    cache.get((0, (7, 7)), capturing=True)
+    for i in range(600, 700):
+        cache.get((0, (i, 9)), capturing=False)
+    assert cache.get((0, (7, 7)), capturing=False) is early

@@ -15,7 +15,7 @@ import torch
 
 from accuracy import assert_close
 from nested_standin import NestedTensor
-from oops_amd import OOpsUnsupportedError, layer_norm
+from oops_amd import LayerNorm, OOpsUnsupportedError, layer_norm
 from oracle import layer_norm as oln
 
 pytestmark = pytest.mark.gpu
@@ -33,12 +33,14 @@ def _grad_close(got, want, dtype, what):
     assert err <= tol * max(1.0, float(np.abs(want).max())), f"{what}: {err:.3g}"
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+# float32 affine over a float32 activation is the "same" case, so it is not listed twice
+_CASES = [(d, a) for d in (torch.float32, torch.bfloat16, torch.float16) for a in ("same", "f32", "none")
+          if not (a == "f32" and d == torch.float32)]  # fmt: skip
+
+
+@pytest.mark.parametrize("dtype,affine", _CASES)
 @pytest.mark.parametrize("width", [1, 17, 128, 384, 4096, 8192])
-@pytest.mark.parametrize("affine", ["same", "f32", "none"])
 def test_layer_norm(dtype, width, affine):
-    if affine == "f32" and dtype == torch.float32:
-        pytest.skip("same as 'same'")
     g = torch.Generator().manual_seed(width)
     rows = 3000 if width <= 384 else 200
     x = (torch.randn(rows, width, generator=g) * 2 + 0.5).to(dtype).to(DEV).requires_grad_(True)
@@ -107,3 +109,43 @@ def test_layer_norm_compile_matches_eager():
         results.append((y.detach(), *torch.autograd.grad(y, [x, w], dy)))
     for got, ref in zip(*results):
         torch.testing.assert_close(got, ref, atol=0, rtol=0)
+
+
+def test_layer_norm_module():
+    """oops_amd.LayerNorm (reference oops/normalization/layer_norm/modules.py:31-70): torch.nn.LayerNorm's
+    constructor and parameters; CUDA half/float32 calls run the HIP kernels, declined inputs (float64,
+    several normalized dimensions) fall back to PyTorch's LayerNorm."""
+
+    import importlib
+
+    ln_mod = importlib.import_module("oops_amd.normalization.layer_norm")
+
+    torch.manual_seed(3)
+    m = LayerNorm(96, eps=1e-6).to(DEV)
+    assert isinstance(m, torch.nn.LayerNorm)
+    with torch.no_grad():
+        m.weight.normal_()
+        m.bias.normal_()
+    x = torch.randn(4, 50, 96, device=DEV).to(torch.bfloat16).requires_grad_(True)
+    calls = []
+    real = ln_mod._apply
+    ln_mod._apply = lambda *a: calls.append(1) or real(*a)
+    try:
+        y = m(x)
+    finally:
+        ln_mod._apply = real
+    assert calls, "the module did not run the HIP path"
+    assert_close(y, oln.layer_norm_forward(_np(x), _np(m.weight), _np(m.bias), eps=1e-6), torch.bfloat16, "y")
+    dy = torch.randn_like(y)
+    gx, gw, gb = torch.autograd.grad(y, (x, m.weight, m.bias), dy)
+    dx, dw, db = oln.layer_norm_backward(_np(x), _np(dy), _np(m.weight), eps=1e-6)
+    assert_close(gx, dx, torch.bfloat16, "dx")
+    _grad_close(gw, dw, torch.bfloat16, "dweight")
+    _grad_close(gb, db, torch.bfloat16, "dbias")
+    # declined by layer_norm -> native LayerNorm
+    m64 = LayerNorm(96).to(DEV).double()
+    x64 = torch.randn(3, 96, device=DEV, dtype=torch.float64)
+    torch.testing.assert_close(m64(x64), torch.nn.functional.layer_norm(x64, (96,), m64.weight, m64.bias))
+    m2 = LayerNorm((5, 96)).to(DEV)
+    x2 = torch.randn(2, 5, 96, device=DEV)
+    torch.testing.assert_close(m2(x2), torch.nn.functional.layer_norm(x2, (5, 96), m2.weight, m2.bias))

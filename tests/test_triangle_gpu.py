@@ -209,3 +209,66 @@ def test_errors():
         triangle_attention(q.double(), q.double(), q.double())
     with pytest.raises(OOpsUnsupportedError):
         triangle_attention(q, q, q, torch.ones(1, 3, 5, device=DEV))  # non-bool mask
+
+
+def test_unmasked_swapped_fast_path():
+    """Ending-node layout without a mask: the unmasked-tile (MASKED_TILES=false) fast kernels."""
+
+    for bias_kind in ("shared", "full", "none"):
+        case = make_case(torch.bfloat16, rows=5, cols=192, heads=4, head=32, bias_kind=bias_kind, masked=False,
+                         layout="swapped", seed=31)  # fmt: skip
+        run_and_check(*case, torch.bfloat16)
+
+
+def test_config_c1_fp32():
+    """starting node, fp32, N=64, H=4, c=32, no mask, forward and gradients
+    against the full float64 oracle at 1e-5 (tests/attention/triangle/test_triangle_attention.py:42-63)."""
+
+    g = torch.Generator().manual_seed(1)
+    n, h, c = 64, 4, 32
+    q, k, v, dout = (torch.randn(1, n, n, h, c, generator=g) for _ in range(4))
+    bias = torch.randn(1, 1, h, n, n, generator=g)
+    run_and_check(q, k, v, None, bias, dout, torch.float32)
+
+
+def _report(name, got, want):
+    got = got.detach().double().cpu().numpy()
+    err = np.abs(got - want)
+    print(f"c3 {name}: max-abs {err.max():.3g} mean-rel {err.mean() / max(np.abs(want).mean(), 1e-30):.3g}", flush=True)
+
+
+def test_config_c3_ending_node():
+    """BASELINE config 3 (the headline) at full size, on exactly the benchmark's inputs
+    (bench.make_inputs: seed 2, randn(1,768,768,4,32) bf16 passed as .transpose(1,2) views, shared
+    bias (1,1,4,768,768), no mask, upstream gradient in the output's layout).
+
+    Rows are independent, so O, dQ, dK and dV are checked against the float64 oracle on 4 rows.
+    The shared dBias sums dS over all 768 rows; it is checked against the float64 oracle over every
+    row on 6 query positions (all heads, all keys), through the oracle's pair-bias form, whose
+    queries may be a subset of the keys.
+    """
+
+    from bench import make_inputs, step
+
+    q, k, v, bias, dout = make_inputs(DEV)
+    out = triangle_attention(q, k, v, None, bias)
+    dq, dk, dv, db = torch.autograd.grad(out, (q, k, v, bias), dout)
+    # the benchmark's own step returns the same gradients (no state between calls)
+    for a_, b_ in zip(step(q, k, v, bias, dout), (dq, dk, dv, db)):
+        assert torch.equal(a_, b_)
+    qn, kn, vn, don, bn = (_np(t) for t in (q, k, v, dout, bias))
+    rows = [0, 257, 511, 767]
+    exp_out, _ = ora.triangle_attention_forward(qn[:, rows], kn[:, rows], vn[:, rows], None, bn)
+    want = ora.triangle_attention_backward(qn[:, rows], kn[:, rows], vn[:, rows], don[:, rows], None, bn)
+    for name, got, w in zip(("out", "dq", "dk", "dv"), (out, dq, dk, dv), (exp_out, *want[:3])):
+        _report(name, got[:, rows], w)
+        assert_close(got[:, rows], w, torch.bfloat16, name)
+    # dBias over every row on a few query positions: head-major (S=rows, H, Q, D) pair-bias form
+    qpos = [0, 1, 100, 383, 640, 767]
+    hm = lambda x: np.ascontiguousarray(np.swapaxes(x[0], 1, 2))  # (rows, cols, H, D) -> (rows, H, cols, D)
+    qh, kh, vh, dh = hm(qn), hm(kn), hm(vn), hm(don)
+    _, _, _, db_want = ora.pair_bias_attention_backward(
+        qh[:, :, qpos], kh, vh, dh[:, :, qpos], None, bn[0, 0][:, qpos], dtype=np.float64
+    )
+    _report("dbias", db[0, 0][:, qpos], db_want)
+    assert_close(db[0, 0][:, qpos], db_want, torch.bfloat16, "dbias")
