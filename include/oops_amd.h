@@ -117,6 +117,22 @@ int oops_attn_forward(const oops_attn_geometry* geo, const void* q, const void* 
                       const uint8_t* mask, const void* bias, void* out, void* out_lo, float* lse,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* oops_attn_forward without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  It
+ * runs the same kernels; what oops_attn_forward keeps in the caller's
+ * workspace (the fragment-major copy of a row-shared bias) goes to a static
+ * device scratch array of OOPS_NOALLOC_SCRATCH_BYTES that the library holds
+ * on every GPU it runs on until the process ends; the entry point calls no
+ * allocator.  Geometries whose oops_attn_forward_workspace_bytes exceeds that
+ * size return OOPS_EWORKSPACE.  All calls on one GPU share the array: calls
+ * that overlap in time on one GPU (different streams, no ordering between
+ * them) race on it and must be serialised by the caller. */
+#define OOPS_NOALLOC_SCRATCH_BYTES 33554432
+int oops_attn_forward_noalloc(const oops_attn_geometry* geo, const void* q, const void* k, const void* v,
+                              const uint8_t* mask, const void* bias, void* out, void* out_lo, float* lse,
+                              void* stream);
+
 /* Bytes of device workspace oops_attn_forward needs for this geometry (0 when
  * none: workspace may then be NULL).  The forward uses it for a fragment-major
  * copy of a row-shared bias (H x Lq x Lk elements, padded to 32), which the

@@ -16,6 +16,7 @@ LIB_PATH = Path(os.environ.get("OOPS_AMD_LIB") or Path(__file__).resolve().paren
 
 F32, BF16, F16 = 0, 1, 2
 BIAS_NONE, BIAS_FULL, BIAS_SHARED = 0, 1, 2
+NOALLOC_SCRATCH_BYTES = 32 << 20
 PHASE_DELTA, PHASE_DQ, PHASE_DKV, PHASE_DBIAS = 1, 2, 4, 8
 TABLE_WIDTH = 40
 ABI_VERSION = 5
@@ -37,6 +38,7 @@ ABI_VERSION = 5
 
 EXPORTED_SYMBOLS = (
     "oops_attn_forward",
+    "oops_attn_forward_noalloc",
     "oops_attn_forward_workspace_bytes",
     "oops_attn_backward_workspace_bytes",
     "oops_attn_backward",
@@ -148,6 +150,8 @@ def load() -> ctypes.CDLL:
         geo = ctypes.POINTER(Geometry)
         lib.oops_attn_forward.argtypes = [geo, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
         lib.oops_attn_forward.restype = i32
+        lib.oops_attn_forward_noalloc.argtypes = [geo, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        lib.oops_attn_forward_noalloc.restype = i32
         lib.oops_attn_forward_workspace_bytes.argtypes = [geo]
         lib.oops_attn_forward_workspace_bytes.restype = sz
         lib.oops_attn_backward_workspace_bytes.argtypes = [geo]

@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "attn_kernels.h"
@@ -267,6 +268,60 @@ int gate_launch_result(hipError_t err, const char* what) {
   return OOPS_ELAUNCH;
 }
 
+// Device scratch of oops_attn_forward_noalloc: the fragment-major bias copy
+// that oops_attn_forward puts in its caller's workspace.  Every GPU the
+// library runs on holds its own copy of this array until the process ends.
+// In host code `scratch` only names the symbol; its device address on the
+// current GPU comes from hipGetSymbolAddress, taken once per device.
+constexpr size_t kNoAllocScratchBytes = OOPS_NOALLOC_SCRATCH_BYTES;
+static_assert(kNoAllocScratchBytes % 256 == 0, "scratch size");
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on the
+// first call on that device).
+int scratch_on_current_device(void** ptr) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return fail(OOPS_ELAUNCH, "hipGetDevice failed");
+  if (dev < 0 || dev >= kMaxDevices) return fail(OOPS_EINVAL, "device index %lld out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr) {
+      g_last_error = std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(err);
+      return OOPS_ELAUNCH;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return OOPS_OK;
+}
+
+int check_forward_pointers(const oops_attn_geometry* geo, const void* q, const void* k, const void* v,
+                           const uint8_t* mask, const void* bias, const void* out) {
+  if (!q || !k || !v || !out) return fail(OOPS_EINVAL, "q, k, v and out must be non-NULL");
+  if (geo->has_bias && !bias) return fail(OOPS_EINVAL, "has_bias is set but bias is NULL");
+  if (geo->has_mask && !mask) return fail(OOPS_EINVAL, "has_mask is set but mask is NULL");
+  return OOPS_OK;
+}
+
+int run_forward(const oops_attn_geometry* geo, const oops::Plan& plan, const void* q, const void* k, const void* v,
+                const uint8_t* mask, const void* bias, void* out, void* out_lo, float* lse, void* workspace,
+                void* stream) {
+  const hipError_t err = oops::launch_forward(*geo, plan, q, k, v, mask, bias, workspace, out, out_lo, lse,
+                                              static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) {
+    g_last_error = std::string("forward launch failed: ") + hipGetErrorString(err);
+    return OOPS_ELAUNCH;
+  }
+  return OOPS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -287,17 +342,27 @@ int oops_attn_forward(const oops_attn_geometry* geo, const void* q, const void* 
   g_last_error.clear();
   oops::Plan plan;
   if (int rc = make_plan(geo, plan)) return rc;
-  if (!q || !k || !v || !out) return fail(OOPS_EINVAL, "q, k, v and out must be non-NULL");
-  if (geo->has_bias && !bias) return fail(OOPS_EINVAL, "has_bias is set but bias is NULL");
-  if (geo->has_mask && !mask) return fail(OOPS_EINVAL, "has_mask is set but mask is NULL");
+  if (int rc = check_forward_pointers(geo, q, k, v, mask, bias, out)) return rc;
   if (int rc = check_workspace(workspace, ws_bytes, forward_workspace_bytes(plan))) return rc;
-  const hipError_t err = oops::launch_forward(*geo, plan, q, k, v, mask, bias, workspace, out, out_lo, lse,
-                                              static_cast<hipStream_t>(stream));
-  if (err != hipSuccess) {
-    g_last_error = std::string("forward launch failed: ") + hipGetErrorString(err);
-    return OOPS_ELAUNCH;
+  return run_forward(geo, plan, q, k, v, mask, bias, out, out_lo, lse, workspace, stream);
+}
+
+int oops_attn_forward_noalloc(const oops_attn_geometry* geo, const void* q, const void* k, const void* v,
+                              const uint8_t* mask, const void* bias, void* out, void* out_lo, float* lse,
+                              void* stream) {
+  g_last_error.clear();
+  oops::Plan plan;
+  if (int rc = make_plan(geo, plan)) return rc;
+  const size_t need = forward_workspace_bytes(plan);
+  if (need > kNoAllocScratchBytes)
+    return fail(OOPS_EWORKSPACE, "this geometry needs %lld bytes of scratch; the no-allocation forward has %lld",
+                (long long)need, (long long)kNoAllocScratchBytes);
+  if (int rc = check_forward_pointers(geo, q, k, v, mask, bias, out)) return rc;
+  void* ws = nullptr;
+  if (need > 0) {
+    if (int rc = scratch_on_current_device(&ws)) return rc;
   }
-  return OOPS_OK;
+  return run_forward(geo, plan, q, k, v, mask, bias, out, out_lo, lse, ws, stream);
 }
 
 size_t oops_attn_backward_workspace_bytes(const oops_attn_geometry* geo) {
