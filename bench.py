@@ -109,8 +109,9 @@ def kernel_times(q, k, v, bias, dout, iters=20):
     fwd = lambda: _core.attention_forward(qd, kd, vd, None, bd, table, H, scale, lse_numel, True)
     o, o_lo, lse = fwd()
     res = {"fwd": time_events(fwd, iters, 3, stream)}
-    # dq includes delta = rowsum(O * dO), which the dQ kernel computes itself
-    for name, ph in (("dq", _lib.PHASE_DQ), ("dkv", _lib.PHASE_DKV), ("dbias", _lib.PHASE_DBIAS)):
+    # dq includes delta = rowsum(O * dO), which the dQ kernel computes itself; dkvb is the fused
+    # dK/dV + shared-dBias kernel with the reduction of its per-part dBias slabs
+    for name, ph in (("dq", _lib.PHASE_DQ), ("dkvb", _lib.PHASE_DKV | _lib.PHASE_DBIAS)):
 
         def bwd(ph=ph):
             with _core.profile_phases(ph):
@@ -125,7 +126,7 @@ def kernel_times(q, k, v, bias, dout, iters=20):
                                      [True, True, True, True])  # fmt: skip
 
     overhead = time_events(empty_bwd, iters, 3, stream)
-    for name in ("dq", "dkv", "dbias"):
+    for name in ("dq", "dkvb"):
         res[name] = max(res[name] - overhead, 1e-6)
     return res
 
@@ -154,17 +155,16 @@ def measured_traffic(kernel):
 
 
 # per-kernel MFMA work in units of 2*H*c*N^3 (one N x N x c GEMM per row and head)
-KERNEL_GEMMS = {"fwd": 2, "dq": 3, "dkv": 4, "dbias": 2}
+KERNEL_GEMMS = {"fwd": 2, "dq": 3, "dkvb": 4}
 
 
 def bias_traffic(kt):
     """Bias bytes per kernel at config 3 (no mask there): each kernel reads the shared [H, N, N] bf16 bias
-    (its fragment-major copy) from HBM once; the forward, dQ and dK/dV kernels re-read it from L2 for every
-    one of the N rows, the dBias kernel once per part of rows (8 at config 3) since it keeps a tile's bias
-    while it walks the part's rows.  Rates are those bytes over the kernel's measured time."""
+    (its fragment-major copy) from HBM once and re-reads it from L2 for every one of the N rows.  Rates are
+    those bytes over the kernel's measured time."""
 
     once = H * N * N * 2
-    reuse = {"fwd": N, "dq": N, "dkv": N, "dbias": 8}
+    reuse = {"fwd": N, "dq": N, "dkvb": N}
     out = {"bias_bytes": once, "mask_bytes": 0}
     for k, ms in kt.items():
         out[k] = {

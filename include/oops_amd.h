@@ -104,7 +104,8 @@ typedef struct oops_attn_geometry {
   int32_t vec_ok;      /* 1 when every row of Q/K/V/O/dO/bias starts 16-byte aligned */
   float scale;         /* multiplies Q.K before the bias is added */
   int32_t phases;      /* backward kernels to run: OR of OOPS_PHASE_*, 0 = all */
-  int32_t force_generic; /* 1: skip the specialised fast kernels (testing) */
+  int32_t force_generic; /* testing: 1 skips the specialised fast kernels, 2 keeps them but
+                            runs dK/dV and the shared dBias in separate kernels */
   const int64_t* table_host;   /* host copy, used for grid sizing */
   const int64_t* table_device; /* device copy, read by the kernels */
 } oops_attn_geometry;

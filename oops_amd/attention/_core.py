@@ -72,6 +72,21 @@ class force_generic:
         return False
 
 
+class separate_dkv_dbias:
+    """Context manager keeping the 16-bit fast kernels but running dK/dV and the shared dBias in
+    separate kernels instead of the fused one (testing)."""
+
+    def __enter__(self):
+        global _FORCE_GENERIC
+        self.saved, _FORCE_GENERIC = _FORCE_GENERIC, 2
+        return self
+
+    def __exit__(self, *exc):
+        global _FORCE_GENERIC
+        _FORCE_GENERIC = self.saved
+        return False
+
+
 # ----------------------------------------------------------------- tables
 
 class _TableCache:

@@ -769,6 +769,21 @@ hipError_t launch_backward(const oops_attn_geometry& geo, const Plan& plan, cons
         check();
       }
     }
+    // dK, dV and the shared dBias in one kernel when it serves the geometry
+    const bool fused = fast && (phases & OOPS_PHASE_DKV) && (phases & OOPS_PHASE_DBIAS) && a.dbias != nullptr &&
+                       dkvb_fused_ok(geo, plan);
+    if (fused) {
+      if (err == hipSuccess) err = launch_dkvb_fused(geo, plan, L, stream);
+      a.parts = plan.fused_parts;
+      a.part_groups = plan.fused_part_groups;
+      if (a.parts > 1) {
+        a.uniform_tiles = plan.sred_uniform;
+        hipLaunchKernelGGL((attn_dbias_reduce_kernel<T, BT, DP>), dim3((unsigned)plan.sred_tiles), block, 0,
+                           stream, a);
+        check();
+      }
+      return;
+    }
     if ((phases & OOPS_PHASE_DKV) && (dk != nullptr || dv != nullptr) && plan.dkv_tiles > 0) {
       if (fast) {
         if (err == hipSuccess) err = launch_dkv_fast(geo, plan, L, stream);

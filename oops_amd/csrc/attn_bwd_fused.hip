@@ -1,0 +1,540 @@
+// Fused dK, dV and row-shared dBias for 16-bit Q/K/V, head size <= 32.
+//
+// The backward of attention over G groups (rows of the pair representation)
+// with one bias shared by every group needs three reductions along three
+// different axes: dQ sums over keys, dK and dV over queries, and the shared
+// dBias over groups.  The dQ kernel (attn_dq_fast_kernel, which also writes
+// delta) owns the first; this kernel owns the other two, so each score's P
+// and dS are formed once for dK, dV and dBias together instead of once in a
+// dK/dV kernel and again in a dBias kernel.
+//
+// One workgroup = 8 wavefronts = 32 keys of one (sample, head) and one range
+// ("part") of the groups.  It walks the groups of its part; for each group g
+// every wave walks its eighth of the queries: wave w takes the 32-query tiles
+// w, w + 8, w + 16 (at most three, so Lq <= 768).  Every lane owns one key
+// (the MFMA column).  Per step a wave computes, for one query tile,
+//   S  = Q K^T (+ bias by an identity MFMA, - LSE as the accumulator input),
+//   dP = dO V^T - delta,   P = exp2(S * scale * log2 e),   dS = P * dP,
+//   dV^T += dO^T P,  dK^T += Q^T dS,  region[step] += dS.
+// The dBias region of a wave (32 keys x its query tiles) stays in registers
+// for the whole part.  At the end of each group the eight waves' dK/dV
+// partials are summed in a fixed order through LDS and stored; at the end of
+// the part the region goes to the part's dBias slab, and
+// attn_dbias_reduce_kernel sums the slabs.  No atomics: results are
+// bit-identical from run to run.
+//
+// Data movement: every load of the main loop goes straight from global
+// memory to LDS (buffer_load ... lds, issued through inline assembly and
+// ordered by explicit vmcnt waits).  Each wave has its own 3-stage LDS ring
+// (Q and dO tiles with XOR-swizzled rows, raw LSE and delta), filled two
+// steps ahead, so the steps need no workgroup barrier; each group's K/V
+// block and keep bytes go into 2-buffer slots shared by the waves, one group
+// ahead; the bias of the workgroup's 32 keys and all query tiles (identity-
+// MFMA fragments, from the fragment-major copy made by attn_bias_frag_kernel)
+// is loaded into LDS once per part.  Two barriers per tensor at each group's
+// end, around the dK/dV sum, which reuses the ring stage just read.
+//
+// Semantics: the reference's _backward_key_value and _backward_shared_bias
+// (oops/attention/triangle/triton/kernel.py:569-873, generic.py:484-534) with
+// softmax_backward_dscores (oops/attention/flash/triton/kernel.py:53-62).
+// Masked keys get dK = dV = 0 and contribute nothing to dBias.
+#include "attn_fast_common.h"
+
+namespace oops {
+
+using namespace fast;
+
+namespace {
+
+constexpr int kFusedWaves = 8;
+constexpr int kFusedMaxSteps = 3;  // query tiles per wave: Lq <= 8 * 3 * 32
+constexpr int kFusedMaxQT = kFusedWaves * kFusedMaxSteps;  // query tiles of the bias region (the step switch has 4 cases)
+constexpr int kQT = 32 * 32;       // elements of one 32 x 32 tile
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer resource as four scalar dwords (the same descriptor as make_rsrc):
+// the operand form of the inline-assembly load below.
+__device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  u32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  r[1] = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32)) & 0xffffu;
+  r[2] = __builtin_amdgcn_readfirstlane(bytes);
+  r[3] = 0x00020000u;
+  return r;
+}
+
+// 16 bytes per lane from a buffer into 64 consecutive 16-byte LDS slots at
+// lds (wave-uniform), like dma16, but issued through inline assembly.  The
+// compiler then does not know that this load writes LDS, so it does not wait
+// for it before every later LDS read it cannot prove disjoint (it cannot
+// tell the ring slots apart, and would wait for each step's own prefetch);
+// the kernel's explicit vmcnt waits order these loads instead.  Nothing else
+// in the kernel uses M0.
+__device__ __forceinline__ void dma16_asm(const u32x4& r, const void* lds, uint32_t voff, uint32_t soff) {
+  const uint32_t m0 =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(lds));
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(m0),
+      "v"(voff), "s"(r), "s"(soff)
+      : "memory", "m0");
+}
+
+// The LSE and delta values of 32 queries into 64 consecutive floats at lds:
+// lanes 0..31 read rl (LSE), lanes 32..63 read rd (delta), each at byte
+// offset voff (two loads, each with half of the lanes enabled).  Every load
+// of the main loop goes straight to LDS: none leaves a register waiting for
+// its data, which the compiler, not knowing the load, could copy too early.
+__device__ __forceinline__ void dma_ld_asm(const u32x4& rl, const u32x4& rd, const void* lds, uint32_t voff) {
+  const uint32_t m0 =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(lds));
+  uint64_t saved;
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_mov_b64 %0, exec\n\t"
+      "s_mov_b32 exec_hi, 0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dword %2, %3, 0 offen lds\n\t"
+      "s_mov_b64 exec, %0\n\t"
+      "s_mov_b32 exec_lo, 0\n\t"
+      "buffer_load_dword %2, %4, 0 offen lds\n\t"
+      "s_mov_b64 exec, %0"
+      : "=&s"(saved)
+      : "s"(m0), "v"(voff), "s"(rl), "s"(rd)
+      : "memory", "m0");
+}
+// one byte per lane into a zero-extended dword at lds + 4 lane
+__device__ __forceinline__ void dma_u8_asm(const u32x4& r, const void* lds, uint32_t voff) {
+  const uint32_t m0 =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(lds));
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_ubyte %1, %2, 0 offen lds" ::"s"(m0),
+      "v"(voff), "s"(r)
+      : "memory", "m0");
+}
+// s_waitcnt vmcnt(N): all but the last N loads have landed in LDS (the
+// memory clobber keeps later LDS reads after it)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// LDS of one wave's ring stage: Q tile, dO tile (swizzled rows), -LSE/c, -delta
+struct RingStage {
+  uint16_t q[kQT];
+  uint16_t d[kQT];
+  float ld[64];  // -LSE / c of the 32 queries, then -delta (raw until the step's start)
+};
+
+template <typename T, bool MASKED>
+__global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a) {
+  using E = Elem<T>;
+  using Frag = typename E::Frag;
+  static_assert(sizeof(T) == 2, "16-bit operands");
+
+  // per-wave ring of three stages (two in flight while one is read); at a
+  // group's end a wave's just-read stage holds its dK/dV partials
+  __shared__ __attribute__((aligned(16))) RingStage ring_lds[3][kFusedWaves];
+  // K / V block of a group: [g parity][K, V][32 keys][32]
+  __shared__ __attribute__((aligned(16))) T kv_lds[2 * 2 * 32 * 32];
+  // the workgroup's bias region, identity-MFMA fragments of its 32 keys for
+  // every query tile: [query tile][chunk c][64 lanes][8], loaded once per part
+  __shared__ __attribute__((aligned(16))) T bias_lds[kFusedMaxQT * 2 * 64 * 8];
+  // keep bytes of the 32 keys of a group, per lane (lanes 32..63 repeat
+  // 0..31): [g parity][64]
+  __shared__ uint32_t keep_lds[2][64];
+
+  const int tid = threadIdx.x;
+  // (readfirstlane: the wave index, and everything derived from it, is
+  // wave-uniform and lives in scalar registers, e.g. the LDS base of the
+  // direct-to-LDS loads, which must be a scalar)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int lq = lane & 31;
+  const int g2 = lane >> 5;
+
+  int64_t tile = xcd_tile(blockIdx.x, gridDim.x, xcd_chunk(a.uniform_tiles));
+  if (tile >= a.total_tiles) return;
+  const Sample* tab = reinterpret_cast<const Sample*>(a.table);
+  const int H = a.num_heads;
+  const int s_idx = find_sample(tile, tab, a.num_samples, a.uniform_tiles, [&](const Sample& s) {
+    return (int64_t)H * cdiv(s.Lk, 32) * parts_for(s.G, a.part_groups, a.parts);
+  });
+  if (s_idx < 0) return;
+  const Sample& S = tab[__builtin_amdgcn_readfirstlane(s_idx)];
+  // every table field the loop needs, read once into (scalar) registers: the
+  // barriers are compiler memory fences, after which fields read through S
+  // would be fetched from global memory again
+  auto u64 = [](int64_t x) { return (int64_t)uniform64((uint64_t)x); };
+  auto uptr = [](auto* p) { return reinterpret_cast<decltype(p)>(uniform64(reinterpret_cast<uint64_t>(p))); };
+  const int64_t G = u64(S.G);
+  const int P = parts_for(G, a.part_groups, a.parts);
+  const int Lq = __builtin_amdgcn_readfirstlane((int)S.Lq), Lk = __builtin_amdgcn_readfirstlane((int)S.Lk);
+  const int nkb = (int)cdiv(Lk, 32);
+  // logical order (head, part, key block): the key blocks of one (head, part)
+  // read the same Q / dO rows and run next to each other on one XCD
+  const int kb = (int)(tile % nkb);
+  int64_t rest = tile / nkb;
+  const int part = (int)(rest % P);
+  const int h = (int)(rest / P);
+  const int g_begin = __builtin_amdgcn_readfirstlane((int)(G * part / P));
+  const int g_end = __builtin_amdgcn_readfirstlane((int)(G * (part + 1) / P));
+  const int D = a.head_size;
+  const int nqt = (Lq + 31) >> 5;
+  const int NS = (nqt + 7) >> 3;  // steps per group (<= kFusedMaxSteps, checked on the host)
+  const int q_si = __builtin_amdgcn_readfirstlane((int)S.q_si);
+  const int do_si = __builtin_amdgcn_readfirstlane((int)S.do_si);
+  const float c1 = a.scale * kLog2e;
+  const float inv_c1 = 1.0f / c1;
+  const int key = kb * 32 + lq;  // this lane's key
+  const int ld_q = kappa(lq >> 4, lq & 15);  // query of ring position lq (the inverse of perm32)
+  const bool has_mask = MASKED && a.mask != nullptr && S.m_off >= 0;
+
+  const T* const q_h = uptr(a.q + S.q_off + h * S.q_sh);
+  const T* const do_h = uptr(a.dout + S.do_off + h * S.do_sh);
+  const int64_t q_sg = u64(S.q_sg), do_sg = u64(S.do_sg);
+  const uint32_t q_bytes = (uint32_t)(((int64_t)(Lq - 1) * q_si + D) * 2);
+  const uint32_t do_bytes = (uint32_t)(((int64_t)(Lq - 1) * do_si + D) * 2);
+  // LSE (lanes 0..31) and delta (lanes 32..63) rows of (g, h)
+  const float* const lse_h = uptr(a.lse + S.l_off + (int64_t)h * Lq);
+  const float* const dlt_h = uptr(a.delta + S.l_off + (int64_t)h * Lq);
+  const int64_t ld_sg = (int64_t)H * Lq;
+  const uint8_t* const m_h = has_mask ? uptr(a.mask + S.m_off) : nullptr;
+  const int64_t m_sg = has_mask ? u64(S.m_sg) : 0;
+
+  // ---- per-lane DMA offsets (bytes) of the Q / dO tile rows: load r (0, 1)
+  // of a tile covers rows 16 r .. 16 r + 15; lane l writes slot l = row
+  // 16 r + l / 4, physical chunk l % 4, which holds logical chunk (l % 4) ^ swz(row)
+  uint32_t q_lane_off[2], do_lane_off[2];
+  int st_row[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    st_row[r] = 16 * r + (lane >> 2);
+    const int col = ((lane & 3) ^ swz<32>(st_row[r])) * 8;
+    q_lane_off[r] = col < D ? (uint32_t)((st_row[r] * q_si + col) * 2) : kOut;
+    do_lane_off[r] = col < D ? (uint32_t)((st_row[r] * do_si + col) * 2) : kOut;
+  }
+  // K/V block DMA: waves 0..3 load tensor w / 2 (K, V), rows 16 (w % 2) .. +15
+  const int kv_t = (wave >> 1) & 1;
+  const int kv_row = 16 * (wave & 1) + (lane >> 2);
+  const int kv_col = (lane & 3) * 8;
+  const int64_t kv_si = u64(kv_t ? S.v_si : S.k_si);
+  const int64_t kv_sg = u64(kv_t ? S.v_sg : S.k_sg);
+  const T* const kv_h = uptr(kv_t ? a.v + S.v_off + h * S.v_sh : a.k + S.k_off + h * S.k_sh);
+  const uint32_t kv_bytes = (uint32_t)(((int64_t)(Lk - 1) * kv_si + D) * 2);
+  const int kv_key = kb * 32 + kv_row;
+  const uint32_t kv_lane_off = kv_key < Lk && kv_col < D ? (uint32_t)((kv_key * kv_si + kv_col) * 2) : kOut;
+  // bias fragments (A operand, lane = query): the fragment-major copy of the
+  // shared bias; the 1 KB block of (query tile, chunk c) sits at a uniform offset
+  const bool bf_in = kb < a.bf_nkt;
+  const u32x4 b_rsrc =
+      rsrc_words(a.bias_frag + s_idx * a.bf_sample_stride + (int64_t)h * a.bf_nqt * a.bf_nkt * 1024 +
+                    (bf_in ? kb : 0) * 1024,
+                bf_in ? (uint32_t)(((int64_t)a.bf_nqt * a.bf_nkt - kb) * 2048) : 0u);
+  const uint32_t b_lane = (uint32_t)lane * 16;
+  const int bf_step = a.bf_nkt * 2 * 1024;  // bytes per query tile
+  float* const db_col = (P == 1 ? a.dbias : a.dbias_part + (int64_t)part * a.dbias_extent) + S.db_off +
+                        h * S.db_sh + key;
+  const int64_t db_si = S.db_si;
+
+  Frag ident[2];
+  identity_frags<T>(ident, 1.0f / a.scale, lane);
+  const TrLane trl = tr_lane<32>(lane, 0);
+
+  // a stage is (group g, step i): query tile 8 i + wave of group g; stages
+  // past the part read nothing.  (The fields are wave-uniform; readfirstlane
+  // keeps them, and the address arithmetic on them, in scalar registers.)
+  struct Stage {
+    int g;
+    int i;
+  };
+  auto advance = [&](Stage st) {
+    if (++st.i == NS) {
+      st.i = 0;
+      ++st.g;
+    }
+    st.g = __builtin_amdgcn_readfirstlane(st.g);
+    st.i = __builtin_amdgcn_readfirstlane(st.i);
+    return st;
+  };
+  // Q and dO rows of a stage into ring stage rs of this wave (4 DMA loads)
+  // (A stage past the part gets empty buffer ranges, so every load still
+  // issues but reads nothing; per-lane validity goes into the offsets as
+  // arithmetic, never as a branch: the count of issued loads must not vary.)
+  auto dma_stage = [&](Stage st, const RingStage& rs) {
+    const bool live = st.g < g_end;
+    const int64_t gg = live ? st.g : g_begin;
+    const int qt = st.i * 8 + wave;
+    const u32x4 qr = rsrc_words(q_h + gg * q_sg, live ? q_bytes : 0u);
+    const u32x4 dr = rsrc_words(do_h + gg * do_sg, live ? do_bytes : 0u);
+    // the tile offset is the uniform soffset; a row past Lq gets 2^31 added
+    // to its lane offset (out of range; the sum stays below 2^32)
+    const uint32_t qs = (uint32_t)(qt * 32 * q_si * 2), ds = (uint32_t)(qt * 32 * do_si * 2);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t out = (uint32_t)(qt * 32 + st_row[r] >= Lq) << 31;
+      dma16_asm(qr, rs.q + 16 * r * 32, q_lane_off[r] | out, qs);
+      dma16_asm(dr, rs.d + 16 * r * 32, do_lane_off[r] | out, ds);
+    }
+  };
+  // LSE (ring ld[0..31]) and delta (ld[32..63]) of a stage's 32 queries,
+  // raw: lane l reads query ld_q of the tile, so that position l holds the
+  // query the accumulator layout puts there (a query past Lq reads 0)
+  auto dma_ld = [&](Stage st, const RingStage& rs) {
+    const bool live = st.g < g_end;
+    const int64_t gg = live ? st.g : g_begin;
+    const uint32_t bytes = live ? (uint32_t)(Lq * 4) : 0u;
+    const u32x4 rl = rsrc_words(lse_h + gg * ld_sg, bytes);
+    const u32x4 rd = rsrc_words(dlt_h + gg * ld_sg, bytes);
+    dma_ld_asm(rl, rd, rs.ld, (uint32_t)(((st.i * 8 + wave) * 32 + ld_q) * 4));
+  };
+  // K/V block of group g into slot g & 1: one DMA load per wave (waves 4..7
+  // repeat the loads of waves 0..3, writing the same bytes, so that every
+  // wave issues the same loads)
+  auto dma_kv = [&](int g) {
+    const bool live = g < g_end;
+    const int64_t gg = live ? g : g_begin;
+    const u32x4 r = rsrc_words(kv_h + gg * kv_sg, live ? kv_bytes : 0u);
+    dma16_asm(r, kv_lds + ((g & 1) * 2 + kv_t) * 32 * 32 + 16 * (wave & 1) * 32, kv_lane_off, 0);
+  };
+  // keep bytes of group g's keys into keep_lds[g & 1] (one load)
+  auto dma_keep = [&](int g) {
+    const bool live = g < g_end;
+    const int64_t gg = live ? g : g_begin;
+    const u32x4 r = rsrc_words(has_mask ? m_h + gg * m_sg : nullptr, has_mask && live ? (uint32_t)Lk : 0u);
+    dma_u8_asm(r, keep_lds[g & 1], (uint32_t)key);
+  };
+  // whether key k (< 32) of group g is attended (its keep byte has landed)
+  auto kv_keep = [&](int g, int k) {
+    return g < g_end && kb * 32 + k < Lk && (!has_mask || keep_lds[g & 1][k] != 0);
+  };
+
+  // reducer role of this thread at each group's end: accumulator lane
+  // red_lane (key red_lane % 32) and registers 2 red_jp, 2 red_jp + 1, which
+  // hold head dims red_d0, red_d0 + 1
+  const int red_lane = tid & 63, red_jp = tid >> 6;
+  const int red_key = red_lane & 31;
+  const int red_d0 = 8 * (red_jp >> 1) + 4 * (red_lane >> 5) + 2 * (red_jp & 1);
+  const int red_gkey = kb * 32 + red_key;
+  const bool red_live = red_gkey < Lk && red_d0 < D;
+  const int64_t red_k = S.k_off + h * S.k_sh + (int64_t)red_gkey * S.k_si + red_d0;
+  const int64_t red_v = S.v_off + h * S.v_sh + (int64_t)red_gkey * S.v_si + red_d0;
+  const int64_t k_sg = S.k_sg, v_sg = S.v_sg;
+  constexpr int kStageFloats = (int)(sizeof(RingStage) / 4);
+  static_assert(16 * 64 <= kStageFloats, "a wave's partials fit its ring stage");
+  // one tensor's partials (acc) -> each wave's ring stage `slot` (read
+  // already), barrier, the fixed-order sum of the eight waves' partials,
+  // scaled, stored; barrier (partials read before that LDS is written again)
+  auto reduce_store = [&](int slot, const f32x16& acc, T* dst, int64_t off, float sc, bool kv_ok) {
+    float* const red = reinterpret_cast<float*>(&ring_lds[slot][0]);
+    float* rw = red + wave * kStageFloats + lane;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) rw[j * 64] = acc[j];
+    __syncthreads();
+    const float* src = red + 2 * red_jp * 64 + red_lane;
+    float o0 = src[0], o1 = src[64];
+#pragma unroll
+    for (int w = 1; w < kFusedWaves; ++w) {
+      o0 += src[w * kStageFloats];
+      o1 += src[w * kStageFloats + 64];
+    }
+    if (dst != nullptr && red_live) {
+      const float f = kv_ok ? sc : 0.0f;
+      *reinterpret_cast<uint32_t*>(dst + off) = pack2<T>(o0 * f, o1 * f);
+    }
+    __syncthreads();
+  };
+
+  float region[kFusedMaxSteps][16];
+#pragma unroll
+  for (int i = 0; i < kFusedMaxSteps; ++i)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) region[i][j] = 0.0f;
+  f32x16 dk = f32x16{}, dv = f32x16{};
+
+  // ---- prologue: K/V and keep bytes of the first group, stages 0 and 1,
+  // the bias region
+  Stage st{g_begin, 0};  // the stage being computed
+  dma_kv(g_begin);
+  if constexpr (MASKED) dma_keep(g_begin);
+  dma_ld(st, ring_lds[0][wave]);
+  dma_stage(st, ring_lds[0][wave]);
+  Stage st2 = advance(st);
+  dma_ld(st2, ring_lds[1][wave]);
+  dma_stage(st2, ring_lds[1][wave]);
+  st2 = advance(st2);  // the stage two ahead, whose loads the next step issues
+  // the bias region: wave w loads query tiles w, w + 8, ... (both chunks)
+  // (query tiles past Lq, which the last step's ghost tiles read, are zeros)
+  for (int qt = wave; qt < NS * kFusedWaves; qt += kFusedWaves) {
+    const bool in = qt < nqt && qt < a.bf_nqt;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+      dma16_asm(b_rsrc, bias_lds + (qt * 2 + c) * 64 * 8, in ? b_lane : kOut,
+                in ? (uint32_t)(qt * bf_step + c * 1024) : 0u);
+  }
+  wait_vm<0>();
+  __syncthreads();
+
+  // Loads per step, in issue order: [at a group's first step: the next
+  // group's K/V block and keep bytes (1 + MASKED)], LSE/delta (2), Q/dO tiles
+  // (4), all for the stage two ahead.  A step first waits for its own stage,
+  // issued two steps earlier: everything issued after it (the previous
+  // step's loads) may still be in flight.
+  constexpr int kPerStep = 6;
+  constexpr int kGroupLoads = MASKED ? 2 : 1;
+  int slot = 0;  // ring slot of the stage being computed
+  for (int g = g_begin; g < g_end; ++g) {
+    // this group's K / V fragments (B operand: lane = key, 8 consecutive d)
+    Frag kf[2], vf[2];
+    const bool kvalid = MASKED ? kv_keep(g, lq) : true;
+    const bool wave_masked = MASKED && __any(!kvalid);
+    {
+      const T* kb_ = kv_lds + ((g & 1) * 2) * 32 * 32 + lq * 32;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        kf[s] = lds_frag<T>(kb_ + 16 * s + 8 * g2);
+        vf[s] = lds_frag<T>(kb_ + 32 * 32 + 16 * s + 8 * g2);
+        if (MASKED && !kvalid) {
+          kf[s] = Frag{};
+          vf[s] = Frag{};
+        }
+      }
+    }
+
+    // one step: the region tile is a compile-time index, the step count a
+    // runtime one (a loop over a switch rather than an unrolled loop, which
+    // the compiler would schedule across and keep far more registers live)
+    auto step = [&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      // keep each step's temporaries within the step (the register budget
+      // is 256 per lane at two waves per SIMD)
+      __builtin_amdgcn_sched_barrier(0);
+      // the previous step was a group's first (it issued the group loads too)
+      if (i == 1 || NS == 1) wait_vm<kPerStep + kGroupLoads>();
+      else wait_vm<kPerStep>();
+      RingStage& cur = ring_lds[slot][wave];
+      {
+        // -LSE / c (lanes 0..31) and -delta (lanes 32..63)
+        float* const raw = cur.ld + lane;
+        *raw = *raw * (g2 ? -1.0f : -inv_c1);
+      }
+      if (i == 0) {
+        dma_kv(g + 1);
+        if constexpr (MASKED) dma_keep(g + 1);
+      }
+      RingStage& nxt2 = ring_lds[slot == 0 ? 2 : slot - 1][wave];
+      dma_ld(st2, nxt2);
+      dma_stage(st2, nxt2);
+      st2 = advance(st2);
+
+      // ---- compute this stage
+      const T* qt_ = reinterpret_cast<const T*>(cur.q);
+      const T* dt_ = reinterpret_cast<const T*>(cur.d);
+      f32x16 sacc = *reinterpret_cast<const f32x16*>(&cur.ld[g2 * 16]);
+      {
+        const T* bq = bias_lds + (i * 8 + wave) * 2 * 64 * 8 + lane * 8;
+        sacc = E::mma(lds_frag<T>(bq), ident[0], sacc);
+        sacc = E::mma(lds_frag<T>(bq + 64 * 8), ident[1], sacc);
+      }
+      f32x16 pacc = *reinterpret_cast<const f32x16*>(&cur.ld[32 + g2 * 16]);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        sacc = E::mma(lds_frag<T>(qt_ + swz_off<32>(lq, s * 16 + g2 * 8)), kf[s], sacc);
+        pacc = E::mma(lds_frag<T>(dt_ + swz_off<32>(lq, s * 16 + g2 * 8)), vf[s], pacc);
+      }
+      // two halves of 8 scores: each half's P and dS feed their MFMAs at once
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        float p[8], ds[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int j = 8 * m + e;
+          p[e] = __builtin_amdgcn_exp2f(sacc[j] * c1);
+          if (MASKED && wave_masked) p[e] = kvalid ? p[e] : 0.0f;
+          ds[e] = p[e] * pacc[j];
+          region[i][j] += ds[e];
+        }
+        const Frag pf = pack8<T>(p);
+        const Frag sf = pack8<T>(ds);
+        const int at = (16 * m) * 32;
+        dv = E::mma(lds_read_tr_frag_sw<T>(dt_ + at, trl), pf, dv);
+        dk = E::mma(lds_read_tr_frag_sw<T>(qt_ + at, trl), sf, dk);
+      }
+      slot = slot == 2 ? 0 : slot + 1;
+    };
+    static_assert(kFusedMaxSteps == 3, "the step switch has three cases");
+    for (int i = 0; i < NS; ++i) {
+      switch (i) {
+        case 0: step(std::integral_constant<int, 0>{}); break;
+        case 1: step(std::integral_constant<int, 1>{}); break;
+        default: step(std::integral_constant<int, 2>{}); break;
+      }
+    }
+
+    // ---- group end: the next group's K/V block and keep bytes have landed
+    // (issued at this group's first step, followed by kPerStep loads per
+    // step); the waves' dK and dV partials are summed and stored through the
+    // ring stage the last step read
+    if (NS == 1) wait_vm<kPerStep>();
+    else if (NS == 2) wait_vm<2 * kPerStep>();
+    else wait_vm<3 * kPerStep>();
+    const int red_slot = slot == 0 ? 2 : slot - 1;
+    // (this wave's own load wrote the keep bytes it reads; the other waves'
+    // loads write the same bytes)
+    const bool kv_ok = MASKED ? kv_keep(g, red_key) : true;
+    reduce_store(red_slot, dk, a.dk, red_k + (int64_t)g * k_sg, a.scale, kv_ok);
+    reduce_store(red_slot, dv, a.dv, red_v + (int64_t)g * v_sg, 1.0f, kv_ok);
+    dk = f32x16{};
+    dv = f32x16{};
+  }
+
+  // ---- the part's dBias slab: region[i] holds queries (8 i + wave) * 32 +
+  // kappa(g2, j) of this lane's key
+  if (key < Lk) {
+#pragma unroll
+    for (int i = 0; i < kFusedMaxSteps; ++i) {
+      if (i >= NS) break;
+      const int q0 = (8 * i + wave) * 32;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int q = q0 + kappa(g2, j);
+        if (q < Lq) db_col[(int64_t)q * db_si] = region[i][j];
+      }
+    }
+  }
+}
+
+}  // namespace
+
+bool dkvb_fused_ok(const oops_attn_geometry& geo, const Plan& plan) {
+  return geo.force_generic == 0 && fast_path_ok(geo, plan) && plan.dp == 32 && plan.all_shared && plan.bias_frag &&
+         plan.max_len_q <= kFusedWaves * kFusedMaxSteps * 32 && plan.fused_tiles > 0;
+}
+
+hipError_t launch_dkvb_fused(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L,
+                             hipStream_t stream) {
+  auto go = [&](auto tag) {
+    using T = typename decltype(tag)::type;
+    BwdArgsT<T, T> a;
+    fill_bwd_args(a, geo, plan, L);
+    a.parts = plan.fused_parts;
+    a.part_groups = plan.fused_part_groups;
+    a.uniform_tiles = plan.fused_uniform;
+    a.total_tiles = plan.fused_tiles;
+    const dim3 grid((unsigned)xcd_grid(plan.fused_tiles, xcd_chunk(plan.fused_uniform)));
+    if (geo.has_mask)
+      hipLaunchKernelGGL((attn_dkvb_fast_kernel<T, true>), grid, dim3(512), 0, stream, a);
+    else
+      hipLaunchKernelGGL((attn_dkvb_fast_kernel<T, false>), grid, dim3(512), 0, stream, a);
+    return hipGetLastError();
+  };
+  return geo.dtype == OOPS_BF16 ? go(Tag<__bf16>{}) : go(Tag<_Float16>{});
+}
+
+}  // namespace oops

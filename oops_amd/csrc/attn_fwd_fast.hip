@@ -390,7 +390,7 @@ OOPS_FWD_FAST_INST(_Float16, 32)
 OOPS_FWD_FAST_INST(_Float16, 64)
 
 bool fast_path_ok(const oops_attn_geometry& geo, const Plan& plan) {
-  if (geo.force_generic) return false;
+  if (geo.force_generic == 1) return false;
   if (geo.dtype == OOPS_F32 || plan.dp > 64 || plan.max_len_k > 64 * kMaxKeyTiles || plan.any_pair_mask ||
       !geo.vec_ok || geo.head_size % 8 != 0 || !plan.offsets_32bit)
     return false;

@@ -132,6 +132,11 @@ struct Plan {
   int fast_parts = 1;                            // largest per-sample part count (fast path)
   int64_t fast_part_groups = 1;                  // groups per part the fast path aims at
   bool any_full = false, any_shared = false;
+  bool all_shared = false;                       // every sample has a row-shared bias
+  // fused dK/dV + shared dBias kernel (attn_bwd_fused.hip): 64-key blocks x group ranges
+  int64_t fused_tiles = 0, fused_uniform = 0;
+  int fused_parts = 1;
+  int64_t fused_part_groups = 1;
   bool any_pair_mask = false;                    // a mask that depends on the query
   bool masked_tiles = false;                     // some 64-key tile has masked or out-of-range keys
   bool offsets_32bit = true;                     // every per-(group, head) K/V/bias block < 2 GiB
@@ -216,6 +221,10 @@ hipError_t launch_dkv_fast(const oops_attn_geometry& geo, const Plan& plan, cons
 // later kernels (no separate delta pass)
 hipError_t launch_dq_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L, bool delta_in_dq,
                           hipStream_t stream);
+// Fused dK, dV and row-shared dBias (head size <= 32, Lq <= 768, every sample a shared bias).
+bool dkvb_fused_ok(const oops_attn_geometry& geo, const Plan& plan);
+hipError_t launch_dkvb_fused(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L,
+                             hipStream_t stream);
 hipError_t launch_dbias_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L,
                              hipStream_t stream);
 

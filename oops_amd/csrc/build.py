@@ -26,8 +26,17 @@ LIB_DIR = PKG / "lib"
 OBJ_DIR = REPO / "_build" / "oops_amd"
 LIB_NAME = "liboops_amd.so"
 
-SOURCES = ("attn_fwd.hip", "attn_fwd_fast.hip", "attn_bwd.hip", "attn_bwd_fast.hip", "gate.hip", "trimul.hip", "capi.cpp")
-FAST_MATH_SOURCES = ("attn_fwd_fast.hip", "attn_bwd_fast.hip")
+SOURCES = (
+    "attn_fwd.hip",
+    "attn_fwd_fast.hip",
+    "attn_bwd.hip",
+    "attn_bwd_fast.hip",
+    "attn_bwd_fused.hip",
+    "gate.hip",
+    "trimul.hip",
+    "capi.cpp",
+)
+FAST_MATH_SOURCES = ("attn_fwd_fast.hip", "attn_bwd_fast.hip", "attn_bwd_fused.hip")
 ARCH = "gfx950"
 
 

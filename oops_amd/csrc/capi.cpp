@@ -33,6 +33,8 @@ constexpr int kMaxParts = 64;
 // a dBias part shorter than this spends more on its set-up and partial-sum store than on groups
 constexpr int64_t kMinPartGroups = OOPS_MIN_PART_GROUPS;
 constexpr size_t kMaxBiasFragBytes = size_t(1) << 30;
+constexpr int64_t kTargetFusedBlocks = 768;  // three rounds of one workgroup per CU on 256 CUs
+constexpr int64_t kMinFusedPartGroups = 16;
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -176,6 +178,30 @@ int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
       track(c, c_red, u_red);
     }
     plan.sred_uniform = u_red && c_red > 0 ? c_red : 0;
+    // fused dK/dV + dBias kernel: one workgroup per (head, 32-key block, part),
+    // about kTargetFusedBlocks workgroups (whole rounds of one per CU)
+    plan.all_shared = geo->has_bias != 0;
+    int64_t fused_units = 0;
+    for (int s = 0; s < geo->num_samples; ++s) {
+      const Sample& S = tab[s];
+      if (S.bias_mode != OOPS_BIAS_SHARED || S.b_off < 0) plan.all_shared = false;
+      fused_units += H * cdiv(S.Lk, 32) * S.G;
+    }
+    if (plan.all_shared) {
+      plan.fused_part_groups = std::max<int64_t>(cdiv(fused_units, kTargetFusedBlocks), kMinFusedPartGroups);
+      int64_t c_fu = -1;
+      bool u_fu = true;
+      for (int s = 0; s < geo->num_samples; ++s) {
+        const Sample& S = tab[s];
+        const int p = oops::parts_for(S.G, plan.fused_part_groups, kMaxParts);
+        const int64_t c = H * cdiv(S.Lk, 32) * p;
+        plan.fused_parts = std::max(plan.fused_parts, p);
+        plan.fused_tiles += c;
+        track(c, c_fu, u_fu);
+      }
+      plan.fused_uniform = u_fu && c_fu > 0 ? c_fu : 0;
+      if (plan.fused_tiles > kMaxGrid) plan.fused_tiles = 0;  // not served by the fused kernel
+    }
     if (plan.sbias_tiles > kMaxGrid || plan.fast_sbias_tiles > kMaxGrid || plan.sred_tiles > kMaxGrid)
       return fail(OOPS_EINVAL, "dBias launch grid exceeds 2^31-1 workgroups");
   }
@@ -202,7 +228,7 @@ size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
 // Backward workspace: delta [lse_extent f32] | dBias partial slabs | bias fragment copy.
 size_t parts_bytes(const oops::Plan& plan) {
-  const int parts = std::max(plan.parts, plan.fast_parts);
+  const int parts = std::max({plan.parts, plan.fast_parts, plan.fused_parts});
   return plan.any_shared && parts > 1 ? align256(sizeof(float) * (size_t)parts * plan.dbias_extent) : 0;
 }
 

@@ -272,3 +272,35 @@ def test_config_c3_ending_node():
     )
     _report("dbias", db[0, 0][:, qpos], db_want)
     assert_close(db[0, 0][:, qpos], db_want, torch.bfloat16, "dbias")
+
+
+@pytest.mark.parametrize(
+    "cols,rows,masked,layout",
+    [(96, 5, True, "swapped"), (200, 3, True, "dense"), (40, 4, False, "swapped"), (768, 2, False, "swapped"),
+     (33, 6, True, "dense"), (384, 64, True, "dense")],
+)  # fmt: skip
+def test_fused_dkv_dbias(cols, rows, masked, layout):
+    """The fused dK/dV + shared-dBias kernel (16-bit, head size <= 32, Lq <= 768, row-shared bias):
+    oracle parity, agreement with the separate dK/dV and dBias kernels, and bit-identical repeats."""
+
+    case = make_case(torch.bfloat16, prefix=(1,), rows=rows, cols=cols, heads=4, head=32, masked=masked,
+                     layout=layout, seed=cols + rows)  # fmt: skip
+    run_and_check(*case, torch.bfloat16)
+    q, k, v, mask, bias, dout = (None if t is None else t.to(DEV) for t in case)
+    if layout == "swapped":
+        q, k, v = (torch.empty_strided(t.shape, t.stride(), dtype=t.dtype, device=DEV).copy_(t) for t in (q, k, v))
+
+    def grads():
+        leaves = [t.detach().clone().requires_grad_(True) for t in (q, k, v, bias)]
+        out = triangle_attention(leaves[0], leaves[1], leaves[2], mask, leaves[3])
+        return torch.autograd.grad(out, leaves, dout)
+
+    fused = grads()
+    again = grads()
+    for a_, b_ in zip(fused, again):
+        assert torch.equal(a_, b_)
+    with _core.separate_dkv_dbias():
+        separate = grads()
+    for name, a_, b_ in zip(("dq", "dk", "dv", "dbias"), fused, separate):
+        err = (a_.float() - b_.float()).abs().max().item()
+        assert err <= 2e-2 * max(1.0, b_.float().abs().max().item()), (name, err)
