@@ -729,7 +729,8 @@ int head_group_of(const oops_attn_geometry& geo) { return head_group(geo); }
 hipError_t launch_backward(const oops_attn_geometry& geo, const Plan& plan, const void* q, const void* k,
                            const void* v, const uint8_t* mask, const void* bias, const void* out,
                            const void* out_lo, const float* lse, const void* dout, void* dq, void* dk, void* dv,
-                           float* dbias, float* delta, float* dbias_part, void* bias_frag, hipStream_t stream) {
+                           float* dbias, float* delta, float* ld_pack, void* qdo_compact, float* dbias_part,
+                           void* bias_frag, hipStream_t stream) {
   const bool fast = backward_fast_ok(geo, plan);
   const int phases = geo.phases == 0 ? 0xF : geo.phases;
   hipError_t err = hipSuccess;
@@ -739,8 +740,14 @@ hipError_t launch_backward(const oops_attn_geometry& geo, const Plan& plan, cons
     err = launch_bias_frag(geo, plan, bias, bias_frag, stream);
     if (err != hipSuccess) return err;
   }
-  const BwdLaunch L{q, k, v, out, out_lo, dout, bias, mask, lse, delta, dq, dk, dv, dbias, dbias_part,
-                    use_bf ? bias_frag : nullptr};
+  // the fast dQ kernel writes the LSE/delta pack and the compact Q / dO of the
+  // fused dK/dV + dBias kernel
+  const bool fusable = fast && ld_pack != nullptr && qdo_compact != nullptr && dkvb_fused_ok(geo, plan);
+  const size_t compact_elems = (size_t)plan.lse_extent * kCompactRow;
+  void* qc = fusable ? qdo_compact : nullptr;
+  void* dc = fusable ? static_cast<char*>(qdo_compact) + compact_elems * 2 : nullptr;
+  const BwdLaunch L{q, k, v, out, out_lo, dout, bias, mask, lse, delta, fusable ? ld_pack : nullptr, qc, dc, dq, dk,
+                    dv, dbias, dbias_part, use_bf ? bias_frag : nullptr};
   const bool ok = dispatch_config(geo.dtype, geo.bias_dtype, plan.dp, [&](auto t, auto bt, auto dpc) {
     using T = typename decltype(t)::type;
     using BT = typename decltype(bt)::type;
@@ -769,9 +776,12 @@ hipError_t launch_backward(const oops_attn_geometry& geo, const Plan& plan, cons
         check();
       }
     }
-    // dK, dV and the shared dBias in one kernel when it serves the geometry
-    const bool fused = fast && (phases & OOPS_PHASE_DKV) && (phases & OOPS_PHASE_DBIAS) && a.dbias != nullptr &&
-                       dkvb_fused_ok(geo, plan);
+    // dK, dV and the shared dBias in one kernel when it serves the geometry and
+    // the pack is ready: the fast dQ kernel has just written it, or (a call
+    // without the dQ and delta phases) a previous call's did
+    const bool pack_ready = (fast && run_dq) || !(phases & (OOPS_PHASE_DQ | OOPS_PHASE_DELTA));
+    const bool fused = fusable && pack_ready && (phases & OOPS_PHASE_DKV) && (phases & OOPS_PHASE_DBIAS) &&
+                       a.dbias != nullptr;
     if (fused) {
       if (err == hipSuccess) err = launch_dkvb_fused(geo, plan, L, stream);
       a.parts = plan.fused_parts;

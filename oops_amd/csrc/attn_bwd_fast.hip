@@ -393,6 +393,19 @@ __global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT
       qu[i] = buffer_load16(qr, ok[i] ? (uint32_t)(((q0w + q_row[i]) * (int)S.q_si + q_col[i]) * 2) : kOut);
       du[i] = buffer_load16(dr, ok[i] ? (uint32_t)(((q0w + q_row[i]) * (int)S.do_si + q_col[i]) * 2) : kOut);
     }
+    if constexpr (DP == kCompactRow) {
+      // compact copies of these Q and dO rows for the fused dK/dV + dBias kernel
+      if (a.qc != nullptr) {
+        const int64_t row0 = S.l_off + ((int64_t)g * H + h) * Lq + q0w;
+#pragma unroll
+        for (int i = 0; i < NQR; ++i)
+          if (ok[i]) {
+            const int64_t e = (row0 + q_row[i]) * kCompactRow + q_col[i];
+            *reinterpret_cast<uint4*>(a.qc + e) = qu[i];
+            *reinterpret_cast<uint4*>(a.dc + e) = du[i];
+          }
+      }
+    }
     float dl;
     if (a.delta_in_dq) {
       // delta = rowsum((O + O_lo) * dO): partial sums over this lane's
@@ -449,6 +462,12 @@ __global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT
       dl = qv ? a.delta[lidx] : 0.0f;
     }
     ndelta = -dl;
+  }
+  // the pack of the fused dK/dV + dBias kernel: per (g, h) row, -LSE / c of
+  // the Lq queries (lanes 0..31), then -delta (lanes 32..63)
+  if (a.ld_pack != nullptr && qv) {
+    float* const pk_row = a.ld_pack + 2 * (lidx - q_lane);
+    pk_row[g2 * Lq + q_lane] = g2 ? ndelta : neg_lse * (1.0f / (a.scale * kLog2e));
   }
   Frag ident[2];
   identity_frags<T>(ident, 1.0f / a.scale, lane);

@@ -83,27 +83,17 @@ __device__ __forceinline__ void dma16_asm(const u32x4& r, const void* lds, uint3
       : "memory", "m0");
 }
 
-// The LSE and delta values of 32 queries into 64 consecutive floats at lds:
-// lanes 0..31 read rl (LSE), lanes 32..63 read rd (delta), each at byte
-// offset voff (two loads, each with half of the lanes enabled).  Every load
-// of the main loop goes straight to LDS: none leaves a register waiting for
-// its data, which the compiler, not knowing the load, could copy too early.
-__device__ __forceinline__ void dma_ld_asm(const u32x4& rl, const u32x4& rd, const void* lds, uint32_t voff) {
+// 4 bytes per lane into 64 consecutive dwords at lds.  Every load of the
+// main loop goes straight to LDS: none leaves a register waiting for its
+// data, which the compiler, not knowing the load, could copy too early.
+__device__ __forceinline__ void dma4_asm(const u32x4& r, const void* lds, uint32_t voff) {
   const uint32_t m0 =
       __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(lds));
-  uint64_t saved;
   asm volatile(
-      "s_mov_b32 m0, %1\n\t"
-      "s_mov_b64 %0, exec\n\t"
-      "s_mov_b32 exec_hi, 0\n\t"
+      "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
-      "buffer_load_dword %2, %3, 0 offen lds\n\t"
-      "s_mov_b64 exec, %0\n\t"
-      "s_mov_b32 exec_lo, 0\n\t"
-      "buffer_load_dword %2, %4, 0 offen lds\n\t"
-      "s_mov_b64 exec, %0"
-      : "=&s"(saved)
-      : "s"(m0), "v"(voff), "s"(rl), "s"(rd)
+      "buffer_load_dword %1, %2, 0 offen lds" ::"s"(m0),
+      "v"(voff), "s"(r)
       : "memory", "m0");
 }
 // one byte per lane into a zero-extended dword at lds + 4 lane
@@ -129,14 +119,15 @@ __device__ __forceinline__ void wait_vm() {
 struct RingStage {
   uint16_t q[kQT];
   uint16_t d[kQT];
-  float ld[64];  // -LSE / c of the 32 queries, then -delta (raw until the step's start)
+  float ld[64];  // -LSE / c of the 32 queries, then -delta
 };
 
-template <typename T, bool MASKED>
+template <typename T, bool MASKED, int NS>
 __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a) {
   using E = Elem<T>;
   using Frag = typename E::Frag;
   static_assert(sizeof(T) == 2, "16-bit operands");
+  static_assert(NS >= 1 && NS <= kFusedMaxSteps, "query tiles per wave and group");
 
   // per-wave ring of three stages (two in flight while one is read); at a
   // group's end a wave's just-read stage holds its dK/dV partials
@@ -145,7 +136,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   __shared__ __attribute__((aligned(16))) T kv_lds[2 * 2 * 32 * 32];
   // the workgroup's bias region, identity-MFMA fragments of its 32 keys for
   // every query tile: [query tile][chunk c][64 lanes][8], loaded once per part
-  __shared__ __attribute__((aligned(16))) T bias_lds[kFusedMaxQT * 2 * 64 * 8];
+  __shared__ __attribute__((aligned(16))) T bias_lds[NS * kFusedWaves * 2 * 64 * 8];
   // keep bytes of the 32 keys of a group, per lane (lanes 32..63 repeat
   // 0..31): [g parity][64]
   __shared__ uint32_t keep_lds[2][64];
@@ -186,39 +177,46 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   const int g_begin = __builtin_amdgcn_readfirstlane((int)(G * part / P));
   const int g_end = __builtin_amdgcn_readfirstlane((int)(G * (part + 1) / P));
   const int D = a.head_size;
-  const int nqt = (Lq + 31) >> 5;
-  const int NS = (nqt + 7) >> 3;  // steps per group (<= kFusedMaxSteps, checked on the host)
-  const int q_si = __builtin_amdgcn_readfirstlane((int)S.q_si);
-  const int do_si = __builtin_amdgcn_readfirstlane((int)S.do_si);
+  const int nqt = (Lq + 31) >> 5;  // <= NS * 8 (the launch picks NS for the longest sample)
+  // Q and dO rows come from the dQ kernel's compact copies: row
+  // l_off + (g H + h) Lq + q of kCompactRow elements
+  constexpr int q_si = kCompactRow, do_si = kCompactRow;
   const float c1 = a.scale * kLog2e;
-  const float inv_c1 = 1.0f / c1;
   const int key = kb * 32 + lq;  // this lane's key
-  const int ld_q = kappa(lq >> 4, lq & 15);  // query of ring position lq (the inverse of perm32)
   const bool has_mask = MASKED && a.mask != nullptr && S.m_off >= 0;
 
-  const T* const q_h = uptr(a.q + S.q_off + h * S.q_sh);
-  const T* const do_h = uptr(a.dout + S.do_off + h * S.do_sh);
-  const int64_t q_sg = u64(S.q_sg), do_sg = u64(S.do_sg);
-  const uint32_t q_bytes = (uint32_t)(((int64_t)(Lq - 1) * q_si + D) * 2);
-  const uint32_t do_bytes = (uint32_t)(((int64_t)(Lq - 1) * do_si + D) * 2);
-  // LSE (lanes 0..31) and delta (lanes 32..63) rows of (g, h)
-  const float* const lse_h = uptr(a.lse + S.l_off + (int64_t)h * Lq);
-  const float* const dlt_h = uptr(a.delta + S.l_off + (int64_t)h * Lq);
-  const int64_t ld_sg = (int64_t)H * Lq;
+  const int64_t row_h = S.l_off + (int64_t)h * Lq;
+  const T* const q_h = uptr(a.qc + row_h * kCompactRow);
+  const T* const do_h = uptr(a.dc + row_h * kCompactRow);
+  const int64_t q_sg = (int64_t)H * Lq * kCompactRow, do_sg = q_sg;
+  // the (g, h) row of the dQ kernel's pack: -LSE / c of the Lq queries, then -delta
+  const float* const pk_h = uptr(a.ld_pack + 2 * row_h);
+  const int64_t pk_sg = 2 * (int64_t)H * Lq;
   const uint8_t* const m_h = has_mask ? uptr(a.mask + S.m_off) : nullptr;
   const int64_t m_sg = has_mask ? u64(S.m_sg) : 0;
 
-  // ---- per-lane DMA offsets (bytes) of the Q / dO tile rows: load r (0, 1)
-  // of a tile covers rows 16 r .. 16 r + 15; lane l writes slot l = row
-  // 16 r + l / 4, physical chunk l % 4, which holds logical chunk (l % 4) ^ swz(row)
+  // ---- per-lane DMA offsets (bytes) of the Q / dO tile rows, from the
+  // tile's first row: load r (0, 1) of a tile covers rows 16 r .. 16 r + 15;
+  // lane l writes slot l = row 16 r + l / 4, physical chunk l % 4, which holds
+  // logical chunk (l % 4) ^ swz(row)
   uint32_t q_lane_off[2], do_lane_off[2];
-  int st_row[2];
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
-    st_row[r] = 16 * r + (lane >> 2);
-    const int col = ((lane & 3) ^ swz<32>(st_row[r])) * 8;
-    q_lane_off[r] = col < D ? (uint32_t)((st_row[r] * q_si + col) * 2) : kOut;
-    do_lane_off[r] = col < D ? (uint32_t)((st_row[r] * do_si + col) * 2) : kOut;
+    const int row = 16 * r + (lane >> 2);
+    const int col = ((lane & 3) ^ swz<32>(row)) * 8;
+    q_lane_off[r] = col < D ? (uint32_t)((row * q_si + col) * 2) : kOut;
+    do_lane_off[r] = col < D ? (uint32_t)((row * do_si + col) * 2) : kOut;
+  }
+  // pack offsets of step i: lane l reads query (8 i + wave) * 32 + ld_q,
+  // lanes 32..63 from the -delta half, so that ring position l holds the
+  // query the accumulator layout puts there (ld_q inverts perm32); a query
+  // past Lq gets 2^31 added (out of range: it reads 0)
+  const int ld_q = kappa(lq >> 4, lq & 15);
+  uint32_t ld_off[NS];
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    const int q = (8 * i + wave) * 32 + ld_q;
+    ld_off[i] = (uint32_t)((q + g2 * Lq) * 4) | ((uint32_t)(q >= Lq) << 31);
   }
   // K/V block DMA: waves 0..3 load tensor w / 2 (K, V), rows 16 (w % 2) .. +15
   const int kv_t = (wave >> 1) & 1;
@@ -247,52 +245,31 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   identity_frags<T>(ident, 1.0f / a.scale, lane);
   const TrLane trl = tr_lane<32>(lane, 0);
 
-  // a stage is (group g, step i): query tile 8 i + wave of group g; stages
-  // past the part read nothing.  (The fields are wave-uniform; readfirstlane
-  // keeps them, and the address arithmetic on them, in scalar registers.)
-  struct Stage {
-    int g;
-    int i;
+  // The resource of one Q or dO tile of group g: its rows only, so that rows
+  // past Lq, tiles past Lq and groups past the part read 0 (a row's D
+  // elements lie below the next row's start).
+  auto tile_rsrc = [&](const T* base_h, int64_t sg, int si, int g, int qt) {
+    const bool live = g < g_end && qt < nqt;
+    const int64_t gg = live ? g : g_begin;
+    const int rows = live ? min(32, Lq - qt * 32) : 1;
+    return rsrc_words(base_h + gg * sg + (int64_t)(live ? qt : 0) * 32 * si,
+                      live ? (uint32_t)(((rows - 1) * si + D) * 2) : 0u);
   };
-  auto advance = [&](Stage st) {
-    if (++st.i == NS) {
-      st.i = 0;
-      ++st.g;
-    }
-    st.g = __builtin_amdgcn_readfirstlane(st.g);
-    st.i = __builtin_amdgcn_readfirstlane(st.i);
-    return st;
-  };
-  // Q and dO rows of a stage into ring stage rs of this wave (4 DMA loads)
-  // (A stage past the part gets empty buffer ranges, so every load still
-  // issues but reads nothing; per-lane validity goes into the offsets as
-  // arithmetic, never as a branch: the count of issued loads must not vary.)
-  auto dma_stage = [&](Stage st, const RingStage& rs) {
-    const bool live = st.g < g_end;
-    const int64_t gg = live ? st.g : g_begin;
-    const int qt = st.i * 8 + wave;
-    const u32x4 qr = rsrc_words(q_h + gg * q_sg, live ? q_bytes : 0u);
-    const u32x4 dr = rsrc_words(do_h + gg * do_sg, live ? do_bytes : 0u);
-    // the tile offset is the uniform soffset; a row past Lq gets 2^31 added
-    // to its lane offset (out of range; the sum stays below 2^32)
-    const uint32_t qs = (uint32_t)(qt * 32 * q_si * 2), ds = (uint32_t)(qt * 32 * do_si * 2);
+  // stage (group g, step i: query tile 8 i + wave) into ring stage rs: the
+  // pack (1 load) and the Q / dO tiles (4); every stage issues all five
+  auto dma_stage = [&](int g, auto ic, const RingStage& rs) {
+    constexpr int i = decltype(ic)::value;
+    const int qt = 8 * i + wave;
+    const bool live = g < g_end;
+    const int64_t gg = live ? g : g_begin;
+    dma4_asm(rsrc_words(pk_h + gg * pk_sg, live ? (uint32_t)(Lq * 8) : 0u), rs.ld, ld_off[i]);
+    const u32x4 qr = tile_rsrc(q_h, q_sg, q_si, g, qt);
+    const u32x4 dr = tile_rsrc(do_h, do_sg, do_si, g, qt);
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const uint32_t out = (uint32_t)(qt * 32 + st_row[r] >= Lq) << 31;
-      dma16_asm(qr, rs.q + 16 * r * 32, q_lane_off[r] | out, qs);
-      dma16_asm(dr, rs.d + 16 * r * 32, do_lane_off[r] | out, ds);
+      dma16_asm(qr, rs.q + 16 * r * 32, q_lane_off[r], 0u);
+      dma16_asm(dr, rs.d + 16 * r * 32, do_lane_off[r], 0u);
     }
-  };
-  // LSE (ring ld[0..31]) and delta (ld[32..63]) of a stage's 32 queries,
-  // raw: lane l reads query ld_q of the tile, so that position l holds the
-  // query the accumulator layout puts there (a query past Lq reads 0)
-  auto dma_ld = [&](Stage st, const RingStage& rs) {
-    const bool live = st.g < g_end;
-    const int64_t gg = live ? st.g : g_begin;
-    const uint32_t bytes = live ? (uint32_t)(Lq * 4) : 0u;
-    const u32x4 rl = rsrc_words(lse_h + gg * ld_sg, bytes);
-    const u32x4 rd = rsrc_words(dlt_h + gg * ld_sg, bytes);
-    dma_ld_asm(rl, rd, rs.ld, (uint32_t)(((st.i * 8 + wave) * 32 + ld_q) * 4));
   };
   // K/V block of group g into slot g & 1: one DMA load per wave (waves 4..7
   // repeat the loads of waves 0..3, writing the same bytes, so that every
@@ -301,7 +278,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
     const bool live = g < g_end;
     const int64_t gg = live ? g : g_begin;
     const u32x4 r = rsrc_words(kv_h + gg * kv_sg, live ? kv_bytes : 0u);
-    dma16_asm(r, kv_lds + ((g & 1) * 2 + kv_t) * 32 * 32 + 16 * (wave & 1) * 32, kv_lane_off, 0);
+    dma16_asm(r, kv_lds + ((g & 1) * 2 + kv_t) * 32 * 32 + 16 * (wave & 1) * 32, kv_lane_off, 0u);
   };
   // keep bytes of group g's keys into keep_lds[g & 1] (one load)
   auto dma_keep = [&](int g) {
@@ -310,7 +287,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
     const u32x4 r = rsrc_words(has_mask ? m_h + gg * m_sg : nullptr, has_mask && live ? (uint32_t)Lk : 0u);
     dma_u8_asm(r, keep_lds[g & 1], (uint32_t)key);
   };
-  // whether key k (< 32) of group g is attended (its keep byte has landed)
+  // whether key kb * 32 + k of group g is attended (its keep byte has landed)
   auto kv_keep = [&](int g, int k) {
     return g < g_end && kb * 32 + k < Lk && (!has_mask || keep_lds[g & 1][k] != 0);
   };
@@ -351,27 +328,28 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
     __syncthreads();
   };
 
-  float region[kFusedMaxSteps][16];
+  float region[NS][16];
 #pragma unroll
-  for (int i = 0; i < kFusedMaxSteps; ++i)
+  for (int i = 0; i < NS; ++i)
 #pragma unroll
     for (int j = 0; j < 16; ++j) region[i][j] = 0.0f;
   f32x16 dk = f32x16{}, dv = f32x16{};
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
 
-  // ---- prologue: K/V and keep bytes of the first group, stages 0 and 1,
-  // the bias region
-  Stage st{g_begin, 0};  // the stage being computed
+  // ---- prologue: K/V and keep bytes of the first group, the first two
+  // stages, the bias region
   dma_kv(g_begin);
   if constexpr (MASKED) dma_keep(g_begin);
-  dma_ld(st, ring_lds[0][wave]);
-  dma_stage(st, ring_lds[0][wave]);
-  Stage st2 = advance(st);
-  dma_ld(st2, ring_lds[1][wave]);
-  dma_stage(st2, ring_lds[1][wave]);
-  st2 = advance(st2);  // the stage two ahead, whose loads the next step issues
+  dma_stage(g_begin, I0{}, ring_lds[0][wave]);
+  if constexpr (NS == 1) dma_stage(g_begin + 1, I0{}, ring_lds[1][wave]);
+  else dma_stage(g_begin, I1{}, ring_lds[1][wave]);
   // the bias region: wave w loads query tiles w, w + 8, ... (both chunks)
-  // (query tiles past Lq, which the last step's ghost tiles read, are zeros)
-  for (int qt = wave; qt < NS * kFusedWaves; qt += kFusedWaves) {
+  // (query tiles past Lq, which ghost steps read, are zeros)
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    const int qt = 8 * i + wave;
     const bool in = qt < nqt && qt < a.bf_nqt;
 #pragma unroll
     for (int c = 0; c < 2; ++c)
@@ -382,13 +360,13 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   __syncthreads();
 
   // Loads per step, in issue order: [at a group's first step: the next
-  // group's K/V block and keep bytes (1 + MASKED)], LSE/delta (2), Q/dO tiles
-  // (4), all for the stage two ahead.  A step first waits for its own stage,
-  // issued two steps earlier: everything issued after it (the previous
-  // step's loads) may still be in flight.
-  constexpr int kPerStep = 6;
+  // group's K/V block and keep bytes (1 + MASKED)], the pack (1), the Q/dO
+  // tiles (4), all for the stage two ahead.  A step first waits for its own
+  // stage, issued two steps earlier: everything issued after it (the
+  // previous step's loads) may still be in flight.
+  constexpr int kPerStep = 5;
   constexpr int kGroupLoads = MASKED ? 2 : 1;
-  int slot = 0;  // ring slot of the stage being computed
+  int slot = 0;  // ring slot of the stage being computed (always the step index when NS == 3)
   for (int g = g_begin; g < g_end; ++g) {
     // this group's K / V fragments (B operand: lane = key, 8 consecutive d)
     Frag kf[2], vf[2];
@@ -407,31 +385,26 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
       }
     }
 
-    // one step: the region tile is a compile-time index, the step count a
-    // runtime one (a loop over a switch rather than an unrolled loop, which
-    // the compiler would schedule across and keep far more registers live)
+    // one step: query tile 8 i + wave of group g (straight-line code per
+    // step; the scheduling barriers keep each step's temporaries within it,
+    // the register budget being 256 per lane at two waves per SIMD)
     auto step = [&](auto ic) {
       constexpr int i = decltype(ic)::value;
-      // keep each step's temporaries within the step (the register budget
-      // is 256 per lane at two waves per SIMD)
       __builtin_amdgcn_sched_barrier(0);
       // the previous step was a group's first (it issued the group loads too)
-      if (i == 1 || NS == 1) wait_vm<kPerStep + kGroupLoads>();
+      if constexpr (i == 1 || NS == 1) wait_vm<kPerStep + kGroupLoads>();
       else wait_vm<kPerStep>();
-      RingStage& cur = ring_lds[slot][wave];
-      {
-        // -LSE / c (lanes 0..31) and -delta (lanes 32..63)
-        float* const raw = cur.ld + lane;
-        *raw = *raw * (g2 ? -1.0f : -inv_c1);
-      }
-      if (i == 0) {
+      const int cs = NS == 3 ? i : slot;
+      const RingStage& cur = ring_lds[cs][wave];
+      if constexpr (i == 0) {
         dma_kv(g + 1);
         if constexpr (MASKED) dma_keep(g + 1);
       }
-      RingStage& nxt2 = ring_lds[slot == 0 ? 2 : slot - 1][wave];
-      dma_ld(st2, nxt2);
-      dma_stage(st2, nxt2);
-      st2 = advance(st2);
+      {
+        constexpr int ahead = i + 2;
+        const int as = NS == 3 ? ahead % 3 : (slot == 0 ? 2 : slot - 1);
+        dma_stage(g + ahead / NS, std::integral_constant<int, ahead % NS>{}, ring_lds[as][wave]);
+      }
 
       // ---- compute this stage
       const T* qt_ = reinterpret_cast<const T*>(cur.q);
@@ -466,25 +439,19 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
         dv = E::mma(lds_read_tr_frag_sw<T>(dt_ + at, trl), pf, dv);
         dk = E::mma(lds_read_tr_frag_sw<T>(qt_ + at, trl), sf, dk);
       }
-      slot = slot == 2 ? 0 : slot + 1;
+      if constexpr (NS != 3) slot = slot == 2 ? 0 : slot + 1;
     };
-    static_assert(kFusedMaxSteps == 3, "the step switch has three cases");
-    for (int i = 0; i < NS; ++i) {
-      switch (i) {
-        case 0: step(std::integral_constant<int, 0>{}); break;
-        case 1: step(std::integral_constant<int, 1>{}); break;
-        default: step(std::integral_constant<int, 2>{}); break;
-      }
-    }
+    step(I0{});
+    if constexpr (NS > 1) step(I1{});
+    if constexpr (NS > 2) step(I2{});
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- group end: the next group's K/V block and keep bytes have landed
     // (issued at this group's first step, followed by kPerStep loads per
     // step); the waves' dK and dV partials are summed and stored through the
     // ring stage the last step read
-    if (NS == 1) wait_vm<kPerStep>();
-    else if (NS == 2) wait_vm<2 * kPerStep>();
-    else wait_vm<3 * kPerStep>();
-    const int red_slot = slot == 0 ? 2 : slot - 1;
+    wait_vm<NS * kPerStep>();
+    const int red_slot = NS == 3 ? 2 : (slot == 0 ? 2 : slot - 1);
     // (this wave's own load wrote the keep bytes it reads; the other waves'
     // loads write the same bytes)
     const bool kv_ok = MASKED ? kv_keep(g, red_key) : true;
@@ -498,8 +465,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   // kappa(g2, j) of this lane's key
   if (key < Lk) {
 #pragma unroll
-    for (int i = 0; i < kFusedMaxSteps; ++i) {
-      if (i >= NS) break;
+    for (int i = 0; i < NS; ++i) {
       const int q0 = (8 * i + wave) * 32;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
@@ -513,8 +479,8 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
 }  // namespace
 
 bool dkvb_fused_ok(const oops_attn_geometry& geo, const Plan& plan) {
-  return geo.force_generic == 0 && fast_path_ok(geo, plan) && plan.dp == 32 && plan.all_shared && plan.bias_frag &&
-         plan.max_len_q <= kFusedWaves * kFusedMaxSteps * 32 && plan.fused_tiles > 0;
+  return geo.force_generic == 0 && fast_path_ok(geo, plan) && plan.dp == kCompactRow && plan.all_shared &&
+         plan.bias_frag && plan.max_len_q <= kFusedWaves * kFusedMaxSteps * 32 && plan.fused_tiles > 0;
 }
 
 hipError_t launch_dkvb_fused(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L,
@@ -528,10 +494,19 @@ hipError_t launch_dkvb_fused(const oops_attn_geometry& geo, const Plan& plan, co
     a.uniform_tiles = plan.fused_uniform;
     a.total_tiles = plan.fused_tiles;
     const dim3 grid((unsigned)xcd_grid(plan.fused_tiles, xcd_chunk(plan.fused_uniform)));
-    if (geo.has_mask)
-      hipLaunchKernelGGL((attn_dkvb_fast_kernel<T, true>), grid, dim3(512), 0, stream, a);
-    else
-      hipLaunchKernelGGL((attn_dkvb_fast_kernel<T, false>), grid, dim3(512), 0, stream, a);
+    // query tiles per wave and group: that of the longest sample
+    const int ns = (int)((plan.max_len_q + 32 * kFusedWaves - 1) / (32 * kFusedWaves));
+    auto run = [&](auto masked, auto nsc) {
+      hipLaunchKernelGGL((attn_dkvb_fast_kernel<T, decltype(masked)::value, decltype(nsc)::value>), grid, dim3(512),
+                         0, stream, a);
+    };
+    auto by_ns = [&](auto masked) {
+      if (ns == 1) run(masked, std::integral_constant<int, 1>{});
+      else if (ns == 2) run(masked, std::integral_constant<int, 2>{});
+      else run(masked, std::integral_constant<int, 3>{});
+    };
+    if (geo.has_mask) by_ns(std::true_type{});
+    else by_ns(std::false_type{});
     return hipGetLastError();
   };
   return geo.dtype == OOPS_BF16 ? go(Tag<__bf16>{}) : go(Tag<_Float16>{});

@@ -30,6 +30,10 @@ struct FwdArgsT {
   int bf_nqt, bf_nkt;        // 32-query / 32-key tiles per head in bias_frag
 };
 
+// Row length (elements) of the compact Q / dO copies the fast dQ kernel writes
+// for the fused dK/dV + dBias kernel (head size <= 32).
+constexpr int kCompactRow = 32;
+
 template <typename T, typename BT>
 struct BwdArgsT {
   const T* q;
@@ -42,6 +46,9 @@ struct BwdArgsT {
   const uint8_t* mask;
   const float* lse;
   float* delta;
+  float* ld_pack;  // per (g, h) row: -LSE / c of its Lq queries, then -delta (fused dK/dV + dBias)
+  T* qc;           // compact copies of Q and dO (fused dK/dV + dBias): row (l_off + (g H + h) Lq + q)
+  T* dc;           // of kCompactRow elements, d < head_size written
   T* dq;
   T* dk;
   T* dv;
@@ -133,7 +140,7 @@ struct Plan {
   int64_t fast_part_groups = 1;                  // groups per part the fast path aims at
   bool any_full = false, any_shared = false;
   bool all_shared = false;                       // every sample has a row-shared bias
-  // fused dK/dV + shared dBias kernel (attn_bwd_fused.hip): 64-key blocks x group ranges
+  // fused dK/dV + shared dBias kernel (attn_bwd_fused.hip): 32-key blocks x group ranges
   int64_t fused_tiles = 0, fused_uniform = 0;
   int fused_parts = 1;
   int64_t fused_part_groups = 1;
@@ -172,6 +179,8 @@ struct BwdLaunch {
   const uint8_t* mask;
   const float* lse;
   float* delta;
+  float* ld_pack;  // written by the fast dQ kernel when non-null, read by the fused dK/dV + dBias kernel
+  void *qc, *dc;   // likewise: compact Q and dO
   void *dq, *dk, *dv;
   float *dbias, *dbias_part;
   const void* bias_frag;  // fragment-major shared biases (fast kernels), or nullptr
@@ -191,6 +200,9 @@ inline void fill_bwd_args(BwdArgsT<T, BT>& a, const oops_attn_geometry& geo, con
   a.mask = geo.has_mask ? L.mask : nullptr;
   a.lse = L.lse;
   a.delta = L.delta;
+  a.ld_pack = L.ld_pack;
+  a.qc = static_cast<T*>(L.qc);
+  a.dc = static_cast<T*>(L.dc);
   a.dq = static_cast<T*>(L.dq);
   a.dk = static_cast<T*>(L.dk);
   a.dv = static_cast<T*>(L.dv);
@@ -221,7 +233,8 @@ hipError_t launch_dkv_fast(const oops_attn_geometry& geo, const Plan& plan, cons
 // later kernels (no separate delta pass)
 hipError_t launch_dq_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L, bool delta_in_dq,
                           hipStream_t stream);
-// Fused dK, dV and row-shared dBias (head size <= 32, Lq <= 768, every sample a shared bias).
+// Fused dK, dV and row-shared dBias (head size <= 32, Lq <= 768, every sample a shared bias); it
+// reads L.ld_pack, L.qc and L.dc, which the fast dQ kernel writes.
 bool dkvb_fused_ok(const oops_attn_geometry& geo, const Plan& plan);
 hipError_t launch_dkvb_fused(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L,
                              hipStream_t stream);
@@ -231,6 +244,7 @@ hipError_t launch_dbias_fast(const oops_attn_geometry& geo, const Plan& plan, co
 hipError_t launch_backward(const oops_attn_geometry& geo, const Plan& plan, const void* q, const void* k,
                            const void* v, const uint8_t* mask, const void* bias, const void* out,
                            const void* out_lo, const float* lse, const void* dout, void* dq, void* dk, void* dv, float* dbias,
-                           float* delta, float* dbias_part, void* bias_frag, hipStream_t stream);
+                           float* delta, float* ld_pack, void* qdo_compact, float* dbias_part, void* bias_frag,
+                           hipStream_t stream);
 
 }  // namespace oops

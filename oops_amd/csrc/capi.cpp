@@ -200,7 +200,8 @@ int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
         track(c, c_fu, u_fu);
       }
       plan.fused_uniform = u_fu && c_fu > 0 ? c_fu : 0;
-      if (plan.fused_tiles > kMaxGrid) plan.fused_tiles = 0;  // not served by the fused kernel
+      // not served by the fused kernel (16-bit, head size <= 32 only)
+      if (plan.fused_tiles > kMaxGrid || geo->dtype == OOPS_F32 || plan.dp != 32) plan.fused_tiles = 0;
     }
     if (plan.sbias_tiles > kMaxGrid || plan.fast_sbias_tiles > kMaxGrid || plan.sred_tiles > kMaxGrid)
       return fail(OOPS_EINVAL, "dBias launch grid exceeds 2^31-1 workgroups");
@@ -226,14 +227,24 @@ int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
 
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
-// Backward workspace: delta [lse_extent f32] | dBias partial slabs | bias fragment copy.
+// Backward workspace: delta [lse_extent f32] | LSE/delta pack [2 lse_extent f32] and compact
+// Q, dO [2 lse_extent kCompactRow 16-bit] (fused dK/dV + dBias kernel) | dBias partial slabs |
+// bias fragment copy.
+size_t pack_bytes(const oops::Plan& plan) {
+  return plan.fused_tiles > 0 ? align256(sizeof(float) * 2 * (size_t)plan.lse_extent) : 0;
+}
+size_t compact_bytes(const oops::Plan& plan) {
+  return plan.fused_tiles > 0 ? align256(2 * sizeof(uint16_t) * (size_t)plan.lse_extent * oops::kCompactRow) : 0;
+}
+
 size_t parts_bytes(const oops::Plan& plan) {
   const int parts = std::max({plan.parts, plan.fast_parts, plan.fused_parts});
   return plan.any_shared && parts > 1 ? align256(sizeof(float) * (size_t)parts * plan.dbias_extent) : 0;
 }
 
 size_t workspace_bytes(const oops::Plan& plan) {
-  return align256(sizeof(float) * (size_t)plan.lse_extent) + parts_bytes(plan) + align256(plan.bf_bytes);
+  return align256(sizeof(float) * (size_t)plan.lse_extent) + pack_bytes(plan) + compact_bytes(plan) +
+         parts_bytes(plan) + align256(plan.bf_bytes);
 }
 
 size_t forward_workspace_bytes(const oops::Plan& plan) { return align256(plan.bf_bytes); }
@@ -410,11 +421,13 @@ int oops_attn_backward(const oops_attn_geometry* geo, const void* q, const void*
   if (int rc = check_workspace(workspace, ws_bytes, workspace_bytes(plan))) return rc;
   char* ws = static_cast<char*>(workspace);
   float* delta = reinterpret_cast<float*>(ws);
-  const size_t delta_bytes = align256(sizeof(float) * (size_t)plan.lse_extent);
+  const size_t delta_bytes = align256(sizeof(float) * (size_t)plan.lse_extent) + pack_bytes(plan) + compact_bytes(plan);
+  float* pack = pack_bytes(plan) ? delta + align256(sizeof(float) * (size_t)plan.lse_extent) / 4 : nullptr;
+  void* compact = compact_bytes(plan) ? reinterpret_cast<char*>(pack) + pack_bytes(plan) : nullptr;
   float* parts = parts_bytes(plan) ? reinterpret_cast<float*>(ws + delta_bytes) : nullptr;
   void* bias_frag = plan.bias_frag ? ws + delta_bytes + parts_bytes(plan) : nullptr;
   const hipError_t err = oops::launch_backward(*geo, plan, q, k, v, mask, bias, out, out_lo, lse, dout, dq, dk, dv,
-                                               geo->has_bias ? dbias : nullptr, delta, parts, bias_frag,
+                                               geo->has_bias ? dbias : nullptr, delta, pack, compact, parts, bias_frag,
                                                static_cast<hipStream_t>(stream));
   if (err != hipSuccess) {
     g_last_error = std::string("backward launch failed: ") + hipGetErrorString(err);
