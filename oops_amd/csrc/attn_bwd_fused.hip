@@ -51,38 +51,6 @@ constexpr int kFusedMaxSteps = 3;  // query tiles per wave: Lq <= 8 * 3 * 32
 constexpr int kFusedMaxQT = kFusedWaves * kFusedMaxSteps;  // query tiles of the bias region (the step switch has 4 cases)
 constexpr int kQT = 32 * 32;       // elements of one 32 x 32 tile
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// Buffer resource as four scalar dwords (the same descriptor as make_rsrc):
-// the operand form of the inline-assembly load below.
-__device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t bytes) {
-  const uint64_t p = reinterpret_cast<uint64_t>(base);
-  u32x4 r;
-  r[0] = __builtin_amdgcn_readfirstlane((uint32_t)p);
-  r[1] = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32)) & 0xffffu;
-  r[2] = __builtin_amdgcn_readfirstlane(bytes);
-  r[3] = 0x00020000u;
-  return r;
-}
-
-// 16 bytes per lane from a buffer into 64 consecutive 16-byte LDS slots at
-// lds (wave-uniform), like dma16, but issued through inline assembly.  The
-// compiler then does not know that this load writes LDS, so it does not wait
-// for it before every later LDS read it cannot prove disjoint (it cannot
-// tell the ring slots apart, and would wait for each step's own prefetch);
-// the kernel's explicit vmcnt waits order these loads instead.  Nothing else
-// in the kernel uses M0.
-__device__ __forceinline__ void dma16_asm(const u32x4& r, const void* lds, uint32_t voff, uint32_t soff) {
-  const uint32_t m0 =
-      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(lds));
-  asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "s_nop 0\n\t"
-      "buffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(m0),
-      "v"(voff), "s"(r), "s"(soff)
-      : "memory", "m0");
-}
-
 // 4 bytes per lane into 64 consecutive dwords at lds.  Every load of the
 // main loop goes straight to LDS: none leaves a register waiting for its
 // data, which the compiler, not knowing the load, could copy too early.

@@ -175,6 +175,41 @@ __device__ __forceinline__ typename Elem<T>::Frag lds_read_tr_frag_sw(const T* a
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, const void* lds, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds), 16, voff, soff, 0, 0);
 }
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer resource as four scalar dwords (the same descriptor as make_rsrc):
+// the operand form of the inline-assembly load below.
+__device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  u32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  r[1] = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32)) & 0xffffu;
+  r[2] = __builtin_amdgcn_readfirstlane(bytes);
+  r[3] = 0x00020000u;
+  return r;
+}
+
+// 16 bytes per lane from a buffer into 64 consecutive 16-byte LDS slots at
+// lds (wave-uniform), like dma16, but issued through inline assembly.  The
+// compiler then does not know that this load writes LDS, so it does not wait
+// for it before every later LDS read it cannot prove disjoint (it cannot
+// tell ring slots apart, and would wait for each step's own prefetch); the
+// kernel's explicit vmcnt waits order these loads instead.  Two rules for a
+// kernel that uses it: every direct-to-LDS load of the kernel goes this way
+// (the compiler does not know that M0 changes), and no compiler-visible
+// register load is waited for while one of these, issued after it, may be
+// in flight (the compiler's count would leave it out and wait for it too).
+__device__ __forceinline__ void dma16_asm(const u32x4& r, const void* lds, uint32_t voff, uint32_t soff) {
+  const uint32_t m0 =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(lds));
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(m0),
+      "v"(voff), "s"(r), "s"(soff)
+      : "memory", "m0");
+}
+
 // wait until at most N vector-memory operations of this wave are outstanding
 template <int N>
 __device__ __forceinline__ void vmem_wait() {
