@@ -30,6 +30,7 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
 COPY_CAL_BYTES = 256 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "triangle_attention_c3_bf16_traffic.txt")
+MFMA_FILE = os.path.join(ROOT, "profiles", "triangle_attention_c3_bf16_mfma.txt")
 N, H, C = 768, 4, 32
 
 
@@ -152,6 +153,56 @@ def measured_traffic(kernel):
         return None
     fetch, write = rows[kernel]
     return int((fetch * factors.get("fetch_factor", 1.0) + write * factors.get("write_factor", 1.0)) * 1024)
+
+
+def measured_mfma():
+    """Per-kernel MFMA busy % from the committed rocprofv3 counter summary (SQ_VALU_MFMA_BUSY_CYCLES
+    over every SIMD's cycles), or {} if absent."""
+
+    out = {}
+    try:
+        lines = open(MFMA_FILE).read().splitlines()
+    except OSError:
+        return out
+    for ln in lines:
+        parts = ln.split()
+        if len(parts) == 2 and not ln.startswith("#"):
+            out[parts[0]] = float(parts[1])
+    return out
+
+
+def accuracy(q, k, v, bias, dout):
+    """Max-abs and mean-relative error of this step's outputs against the float64 oracle (the checker,
+    never the thing measured): O, dQ, dK, dV on rows 0, 257, 511, 767; the shared dBias, which sums
+    over all 768 rows, on query positions 0, 1, 100, 383, 640, 767 of every head and key."""
+
+    import numpy as np
+    import torch
+
+    from oops_amd import triangle_attention
+    from oracle import attention as ora
+
+    out = triangle_attention(q, k, v, None, bias)
+    grads = torch.autograd.grad(out, (q, k, v, bias), dout)
+    npy = lambda t: t.detach().double().cpu().numpy()
+    qn, kn, vn, don, bn = (npy(t) for t in (q, k, v, dout, bias))
+    rows = [0, 257, 511, 767]
+    o_want, _ = ora.triangle_attention_forward(qn[:, rows], kn[:, rows], vn[:, rows], None, bn)
+    g_want = ora.triangle_attention_backward(qn[:, rows], kn[:, rows], vn[:, rows], don[:, rows], None, bn)
+    qpos = [0, 1, 100, 383, 640, 767]
+    hm = lambda x: np.ascontiguousarray(np.swapaxes(x[0], 1, 2))
+    _, _, _, db_want = ora.pair_bias_attention_backward(
+        hm(qn)[:, :, qpos], hm(kn), hm(vn), hm(don)[:, :, qpos], None, bn[0, 0][:, qpos], dtype=np.float64
+    )
+    res = {"reference": "float64 numpy oracle", "tolerance": "bf16: |err| / max(1, |ref|) <= 2e-2"}
+    pairs = (("out", out[:, rows], o_want), ("dq", grads[0][:, rows], g_want[0]), ("dk", grads[1][:, rows], g_want[1]),
+             ("dv", grads[2][:, rows], g_want[2]), ("dbias", grads[3][0, 0][:, qpos], db_want))
+    for name, got, want in pairs:
+        err = np.abs(npy(got) - want)
+        res[name] = {"max_abs": float(f"{err.max():.4g}"),
+                     "mean_rel": float(f"{err.mean() / max(np.abs(want).mean(), 1e-30):.4g}"),
+                     "max_scaled": float(f"{(err / np.maximum(1.0, np.abs(want))).max():.4g}")}
+    return res
 
 
 # per-kernel MFMA work in units of 2*H*c*N^3 (one N x N x c GEMM per row and head)
@@ -659,7 +710,11 @@ def main():
             "mask": None,
             "parallelism": "single GPU",
         },
-        "mfma_util_pct": round(100 * value / PEAK_BF16_TFLOPS, 2),
+        # algorithmic FLOP/s of the whole step over the dense bf16 peak
+        "flops_frac_of_peak": round(value / PEAK_BF16_TFLOPS, 4),
+        # MFMA busy cycles over all SIMD cycles, per kernel, from the committed rocprofv3 counters
+        # (profiles/triangle_attention_c3_bf16_mfma.txt); includes the identity-MFMA bias adds
+        "mfma_util_pct": measured_mfma() or None,
         "bias_traffic": bias_traffic(kt),
         "peak_mem_bytes": int(peak_mem),
         "kernel_ms": {k_: round(v_, 4) for k_, v_ in kt.items()},
@@ -682,6 +737,8 @@ def main():
                              "trimul_n512": trimul_stage(dev), "layer_norm": layer_norm_stage(dev)}
         _log("bench: " + json.dumps(line["next_rows"]))
     if not args.no_cpu:
+        _log("bench: accuracy against the oracle")
+        line["accuracy"] = accuracy(q, k, v, bias, dout)
         _log("bench: cpu baseline")
         line["cpu_baseline"] = cpu_baseline(args.cpu_budget)
     print(json.dumps(line), flush=True)
