@@ -28,6 +28,7 @@ if ROOT not in sys.path:
 METRIC = "tri-attn fwd+bwd TFLOP/s & ms/call at N=768 bf16; MFMA util % vs peak"
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
+PEAK_F32_TFLOPS = 157.3  # MI355X dense fp32 MFMA
 COPY_CAL_BYTES = 256 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "triangle_attention_c3_bf16_traffic.txt")
 MFMA_FILE = os.path.join(ROOT, "profiles", "triangle_attention_c3_bf16_mfma.txt")
@@ -375,17 +376,17 @@ def nested_msa(device):
     }
 
 
-def trimul_stage(device, n=512, c=128, h=128):
-    """triangle_multiplication (outgoing) fwd+bwd on one (N, N, C) pair, C = H = 128, bf16, a key-padding
-    style mask, projection biases; the row after attention in the Pairformer block.  Reports the whole
-    fwd+bwd and the algorithmic GEMM rate (projections, contraction, output)."""
+def trimul_stage(device, n=512, c=128, h=128, dtype="bf16"):
+    """triangle_multiplication (outgoing) fwd+bwd on one (N, N, C) pair, C = H = 128, bf16 (or float32), a
+    key-padding style mask, projection biases; the row after attention in the Pairformer block.  Reports
+    the whole fwd+bwd and the algorithmic GEMM rate (projections, contraction, output)."""
 
     import torch
 
     from oops_amd import triangle_multiplication
 
     g = torch.Generator().manual_seed(13)
-    dt = torch.bfloat16
+    dt = {"bf16": torch.bfloat16, "f32": torch.float32}[dtype]
 
     def r(*shape, scale=1.0):
         return (torch.randn(*shape, generator=g) * scale).to(dt).to(device).requires_grad_(True)
@@ -452,19 +453,24 @@ def trimul_stage(device, n=512, c=128, h=128):
 
         k_fwd = _median_ms(f_fwd, iters=20, warmup=3)
         k_bwd = _median_ms(f_bwd, iters=20, warmup=3)
-    el = 2
+    el = 2 if dtype == "bf16" else 4
     fwd_bytes = rows * c * el + 2 * h * rows * el
     bwd_bytes = rows * c * el + 2 * h * rows * el + 4 * h * rows * el
+    # matrix-core work of the factor kernels: 4H projections of C (the backward recomputes them)
+    k_flops = 2 * rows * c * 4 * h
+    peak = PEAK_BF16_TFLOPS if dtype == "bf16" else PEAK_F32_TFLOPS
     kern = lambda ms_, b_: {"ms": round(ms_, 4), "achieved_gbps": round(b_ / (ms_ * 1e-3) / 1e9, 1),  # noqa: E731
-                            "frac": round(b_ / (ms_ * 1e-3) / 1e9 / 8000.0, 4)}  # fmt: skip
+                            "frac": round(b_ / (ms_ * 1e-3) / 1e9 / 8000.0, 4),
+                            "mfma_tflops": round(k_flops / (ms_ * 1e-3) / 1e12, 1),
+                            "mfma_frac": round(k_flops / (ms_ * 1e-3) / 1e12 / peak, 4)}  # fmt: skip
     return {
-        "workload": f"triangle_multiplication outgoing fwd+bwd, N={n}, C=H={c}, bf16, mask, biases",
+        "workload": f"triangle_multiplication outgoing fwd+bwd, N={n}, C=H={c}, {dtype}, mask, biases",
         "ms_fwd_bwd": round(ms, 4),
         "ms_fwd": round(ms_fwd, 4),
         "tflops_fwd_bwd": round(flops / ms / 1e9, 2),
         "factor_kernel_fwd": kern(k_fwd, fwd_bytes),
         "factor_kernel_bwd": kern(k_bwd, bwd_bytes),
-        "roofline_bound": "hbm",
+        "roofline_bound": "hbm" if dtype == "bf16" else "mfma (float32)",
     }
 
 
@@ -608,7 +614,7 @@ def main():
     )
     ap.add_argument(
         "--only",
-        choices=("nested_msa", "layer_norm"),
+        choices=("nested_msa", "layer_norm", "trimul_f32"),
         help="only measure one of the rows beside attention (3 repetitions) and print its JSON",
     )
     ap.add_argument(
@@ -646,7 +652,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.only:
-        fn = {"nested_msa": nested_msa, "layer_norm": layer_norm_stage}[args.only]
+        fn = {"nested_msa": nested_msa, "layer_norm": layer_norm_stage,
+              "trimul_f32": lambda d: trimul_stage(d, dtype="f32")}[args.only]
         for _ in range(3):
             res = fn(dev)
         print(json.dumps(res))
@@ -734,7 +741,8 @@ def main():
         _log("bench: " + json.dumps(line["other_configs"]))
         _log("bench: gated output stage")
         line["next_rows"] = {"gate_c4_shape": gate_stage(dev), "nested_msa": nested_msa(dev),
-                             "trimul_n512": trimul_stage(dev), "layer_norm": layer_norm_stage(dev)}
+                             "trimul_n512": trimul_stage(dev), "trimul_n512_f32": trimul_stage(dev, dtype="f32"),
+                             "layer_norm": layer_norm_stage(dev)}
         _log("bench: " + json.dumps(line["next_rows"]))
     if not args.no_cpu:
         _log("bench: accuracy against the oracle")

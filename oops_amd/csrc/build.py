@@ -34,6 +34,7 @@ SOURCES = (
     "attn_bwd_fused.hip",
     "gate.hip",
     "trimul.hip",
+    "trimul_f32.hip",
     "capi.cpp",
 )
 FAST_MATH_SOURCES = ("attn_fwd_fast.hip", "attn_bwd_fast.hip", "attn_bwd_fused.hip")

@@ -285,8 +285,9 @@ int check_row_norm(const oops_row_norm_geometry* g) {
 
 int check_trimul(const oops_trimul_geometry* g) {
   if (g == nullptr) return fail(OOPS_EINVAL, "triangle multiplication geometry is NULL");
-  if (g->dtype != OOPS_BF16 && g->dtype != OOPS_F16)
-    return fail(OOPS_EINVAL, "the triangle multiplication kernels serve bfloat16 and float16 (dtype %lld)", g->dtype);
+  if (g->dtype != OOPS_BF16 && g->dtype != OOPS_F16 && g->dtype != OOPS_F32)
+    return fail(OOPS_EINVAL, "the triangle multiplication kernels serve bfloat16, float16 and float32 (dtype %lld)",
+                g->dtype);
   if (g->channels <= 0 || g->channels > 1024 || g->hidden <= 0 || g->hidden > 1024)
     return fail(OOPS_EINVAL, "channels and hidden must be in 1..1024, got %lld and %lld", g->channels, g->hidden);
   if (g->groups < 0 || g->positions < 0) return fail(OOPS_EINVAL, "groups and positions must be >= 0");

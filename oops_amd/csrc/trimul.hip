@@ -1222,12 +1222,17 @@ FactorPlan factor_plan(const oops_trimul_geometry& g, bool backward) {
 }
 }  // namespace
 
-int64_t trimul_bias_parts(const oops_trimul_geometry& g) { return factor_plan(g, true).groups; }
+int64_t trimul_bias_parts(const oops_trimul_geometry& g) {
+  return g.dtype == OOPS_F32 ? trimul_bias_parts_f32(g) : factor_plan(g, true).groups;
+}
 
 hipError_t launch_trimul_factors(const oops_trimul_geometry& g, const void* normalized, const void* weight,
                                  const float* bias, const void* mask, void* factors, const void* grad_factors,
                                  void* grad_projection, float* grad_mask_parts, float* grad_bias_parts,
                                  hipStream_t stream) {
+  if (g.dtype == OOPS_F32)
+    return launch_trimul_factors_f32(g, normalized, weight, bias, mask, factors, grad_factors, grad_projection,
+                                     grad_mask_parts, grad_bias_parts, stream);
   FactorArgs a{};
   a.xn = normalized, a.w = weight, a.bias = bias, a.mask = g.has_mask ? static_cast<const float*>(mask) : nullptr;
   a.factors = factors, a.grad_factors = grad_factors, a.grad_proj = grad_projection;
@@ -1282,16 +1287,18 @@ hipError_t run_out_norm(const oops_trimul_geometry& g, OutNormArgs& a, bool back
   const int64_t blocks = g.groups * a.pblocks;
   if (blocks == 0) return hipSuccess;
   const size_t lds = (size_t)(backward ? 2 : 1) * g.hidden * (a.npb + 1) * sizeof(float);
-  const bool vec = g.positions % 8 == 0 && a.npb >= 8 && (!backward || g.hidden % 8 == 0);
-  return by_half(g.dtype, [&](auto tag) -> hipError_t {
+  // (the 16-byte paths move eight 16-bit elements; float32 takes the element-wise ones)
+  const bool vec = g.dtype != OOPS_F32 && g.positions % 8 == 0 && a.npb >= 8 && (!backward || g.hidden % 8 == 0);
+  return by_any(g.dtype, [&](auto tag) -> hipError_t {
     using T = decltype(tag);
+    constexpr bool kVecOk = sizeof(T) == 2;
     const dim3 grid((unsigned)blocks);
-    if (backward && vec)
-      hipLaunchKernelGGL((trimul_out_norm_backward_kernel<T, true>), grid, dim3(256), lds, stream, a);
+    if (backward && vec && kVecOk)
+      hipLaunchKernelGGL((trimul_out_norm_backward_kernel<T, kVecOk>), grid, dim3(256), lds, stream, a);
     else if (backward)
       hipLaunchKernelGGL((trimul_out_norm_backward_kernel<T, false>), grid, dim3(256), lds, stream, a);
-    else if (vec)
-      hipLaunchKernelGGL((trimul_out_norm_forward_kernel<T, true>), grid, dim3(256), lds, stream, a);
+    else if (vec && kVecOk)
+      hipLaunchKernelGGL((trimul_out_norm_forward_kernel<T, kVecOk>), grid, dim3(256), lds, stream, a);
     else
       hipLaunchKernelGGL((trimul_out_norm_forward_kernel<T, false>), grid, dim3(256), lds, stream, a);
     return hipGetLastError();
@@ -1321,6 +1328,9 @@ hipError_t launch_trimul_output(const oops_trimul_geometry& g, const void* norma
                                 const void* output_weight, const void* gate_weight, const float* output_bias,
                                 const float* gate_bias, void* out, const void* grad_out, void* grad_value,
                                 void* grad_gate, hipStream_t stream) {
+  if (g.dtype == OOPS_F32)
+    return launch_trimul_output_f32(g, normalized, pair_normalized, output_weight, gate_weight, output_bias,
+                                    gate_bias, out, grad_out, grad_value, grad_gate, stream);
   OutArgs a{};
   a.nrm = normalized, a.xn = pair_normalized, a.wo = output_weight, a.wg = gate_weight;
   a.bo = output_bias, a.bg = gate_bias, a.out = out, a.gout = grad_out, a.gval = grad_value, a.ggate = grad_gate;

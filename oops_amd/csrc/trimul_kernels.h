@@ -35,4 +35,15 @@ hipError_t launch_trimul_output(const oops_trimul_geometry& g, const void* norma
                                 const float* gate_bias, void* out, const void* grad_out, void* grad_value,
                                 void* grad_gate, hipStream_t stream);
 
+// float32 pairs (trimul_f32.hip): the same contracts on the exact float32 matrix core
+hipError_t launch_trimul_factors_f32(const oops_trimul_geometry& g, const void* normalized, const void* weight,
+                                     const float* bias, const void* mask, void* factors, const void* grad_factors,
+                                     void* grad_projection, float* grad_mask_parts, float* grad_bias_parts,
+                                     hipStream_t stream);
+int64_t trimul_bias_parts_f32(const oops_trimul_geometry& g);
+hipError_t launch_trimul_output_f32(const oops_trimul_geometry& g, const void* normalized,
+                                    const void* pair_normalized, const void* output_weight, const void* gate_weight,
+                                    const float* output_bias, const float* gate_bias, void* out, const void* grad_out,
+                                    void* grad_value, void* grad_gate, hipStream_t stream);
+
 }  // namespace oops

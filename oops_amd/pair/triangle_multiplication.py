@@ -37,7 +37,7 @@ from ..attention._runtime import is_nested, require_no_forward_mode, require_sam
 _OPERATOR = "triangle_multiplication"
 _KERNEL_DTYPES = (torch.bfloat16, torch.float16)
 _SERVED_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
-_DTYPE_CODE = {torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
+_DTYPE_CODE = {torch.bfloat16: _lib.BF16, torch.float16: _lib.F16, torch.float32: _lib.F32}
 MAX_FUSED_WIDTH = 1024
 
 _WEIGHT_NAMES = (
@@ -573,40 +573,13 @@ def _prepare(grouped: Tensor, mask: Optional[Tensor], weights, biases):
 
 
 def _run(grouped: Tensor, mask: Optional[Tensor], blocks, direction, weights, biases, eps_in, eps_out) -> Tensor:
+    """One fused pipeline for every served dtype: 16-bit pairs on the bf16/f16 MFMA kernels, float32 pairs
+    on their exact float32 MFMA counterparts (csrc/trimul_f32.hip), the contraction as library GEMMs."""
+
     _admit(grouped, weights, biases)
-    if grouped.dtype == torch.float32:
-        return _run_float32(grouped, mask, blocks, direction, weights, biases, eps_in, eps_out)
     flat = [v for block in blocks for v in block]
     operands = _prepare(grouped, mask, weights, biases)
     return trimul_forward(*operands, flat, direction, float(eps_in), float(eps_out))[0]
-
-
-def _run_float32(grouped, mask, blocks, direction, weights, biases, eps_in, eps_out) -> Tensor:
-    """float32 pairs: both LayerNorms on the HIP row kernels (``layer_norm``), the projections and the
-    contraction as exact float32 library GEMMs (the fused MFMA kernels are 16-bit), the gating as
-    elementwise ops; autograd differentiates the composition."""
-
-    from ..normalization.layer_norm import layer_norm
-
-    in_w, in_b, wlv, wlg, wrv, wrg, on_w, on_b, wo, wog = weights
-    blv, blg, brv, brg, bo, bog = biases
-    G, P, C = grouped.shape
-    H = wlv.shape[0]
-    linear = torch.nn.functional.linear
-    xn = layer_norm(grouped, C, in_w, in_b, eps_in)
-    keep = 1.0 if mask is None else mask.to(torch.float32).unsqueeze(-1)
-    left = keep * linear(xn, wlv, blv) * torch.sigmoid(linear(xn, wlg, blg))
-    right = keep * linear(xn, wrv, brv) * torch.sigmoid(linear(xn, wrg, brg))
-    left, right = left.transpose(1, 2), right.transpose(1, 2)  # (G, H, P)
-    pieces = []
-    for off, n in blocks:
-        lb = left[:, :, off : off + n * n].reshape(G, H, n, n)
-        rb = right[:, :, off : off + n * n].reshape(G, H, n, n)
-        x = lb @ rb.transpose(-1, -2) if direction == "outgoing" else lb.transpose(-1, -2) @ rb
-        pieces.append(x.reshape(G, H, n * n))
-    combined = (pieces[0] if len(pieces) == 1 else torch.cat(pieces, -1)).transpose(1, 2)  # (G, P, H)
-    normalized = layer_norm(combined, H, on_w, on_b, eps_out)
-    return linear(normalized, wo, bo) * torch.sigmoid(linear(xn, wog, bog))
 
 
 # ----------------------------------------------------------------- nested

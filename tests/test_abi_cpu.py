@@ -185,7 +185,7 @@ def test_row_norm_and_trimul_validation(lib):
     assert lib.oops_layer_norm_rows_parts(ctypes.byref(rg)) == 0
 
     tg = _lib.TrimulGeometry()
-    tg.dtype, tg.channels, tg.hidden, tg.has_mask = _lib.F32, 16, 16, 0
+    tg.dtype, tg.channels, tg.hidden, tg.has_mask = 7, 16, 16, 0  # no such dtype
     tg.groups, tg.positions, tg.c_row, tg.h_row, tg.eps = 1, 16, 16, 16, 1e-5
     assert lib.oops_trimul_factors_forward(ctypes.byref(tg), fake, fake, None, None, fake, None) != 0
     assert b"bfloat16" in lib.oops_last_error()

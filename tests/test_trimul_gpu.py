@@ -104,6 +104,9 @@ def _check(pair, mask, weights, bs, direction, dtype, grads=True, mask_grad=Fals
         (torch.bfloat16, 8, 1024, 5, (), "outgoing", True),  # widest hidden (few positions per LDS tile)
         (torch.float32, 17, 24, 7, (2,), "outgoing", True),
         (torch.float32, 8, 12, 9, (), "incoming", False),
+        (torch.float32, 128, 128, 20, (1,), "incoming", True),  # 4 | positions: float4 factor stores
+        (torch.float32, 65, 96, 17, (), "outgoing", True),  # odd widths, two channel blocks of W
+        (torch.float32, 40, 200, 12, (), "outgoing", False),  # four hidden blocks, the last partial
     ],
 )
 def test_trimul_dense(dtype, c, h, n, prefix, direction, biases):
@@ -114,15 +117,34 @@ def test_trimul_dense(dtype, c, h, n, prefix, direction, biases):
     _check(pair, mask, weights, bs, direction, dtype)
 
 
-def test_trimul_float_mask_gradient_and_broadcast():
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_trimul_float_mask_gradient_and_broadcast(dtype):
     """A fractional float mask broadcast over the prefix: its gradient is summed over the prefix."""
 
-    dtype = torch.bfloat16
     g = torch.Generator().manual_seed(4)
     pair = torch.randn(3, 12, 12, 32, generator=g).to(dtype).to(DEV).requires_grad_(True)
     mask = torch.rand(1, 12, 12, generator=g).to(DEV).requires_grad_(True)
     weights, bs = _params(dtype, 32, 48, seed=5)
     _check(pair, mask, weights, bs, "incoming", dtype, mask_grad=True)
+
+
+def test_trimul_float32_runs_the_fused_kernels(monkeypatch):
+    """float32 pairs go through the same fused custom op as 16-bit ones (the float32 MFMA kernels of
+    csrc/trimul_f32.hip), not a composition of library ops."""
+
+    import importlib
+
+    mod = importlib.import_module("oops_amd.pair.triangle_multiplication")
+    calls = []
+    orig = mod.trimul_forward
+    monkeypatch.setattr(mod, "trimul_forward", lambda *a: calls.append(a[0].dtype) or orig(*a))
+    dtype = torch.float32
+    g = torch.Generator().manual_seed(9)
+    pair = torch.randn(2, 9, 9, 24, generator=g).to(DEV).requires_grad_(True)
+    mask = (torch.rand(2, 9, 9, generator=g) > 0.3).to(DEV)
+    weights, bs = _params(dtype, 24, 40, seed=9)
+    _check(pair, mask, weights, bs, "outgoing", dtype)
+    assert calls == [torch.float32]
 
 
 def test_trimul_no_mask_fp32_norm_weights():
