@@ -304,3 +304,16 @@ def test_fused_dkv_dbias(cols, rows, masked, layout):
     for name, a_, b_ in zip(("dq", "dk", "dv", "dbias"), fused, separate):
         err = (a_.float() - b_.float()).abs().max().item()
         assert err <= 2e-2 * max(1.0, b_.float().abs().max().item()), (name, err)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_large_bias_nondefault_scale(dtype):
+    """The fast kernels add the bias through an identity MFMA whose weight 1/scale is rounded to the
+    input dtype: the bias term is scaled by 1 + d with |d| <= 2^-9 (bf16) or 2^-11 (f16), a logit shift of
+    at most |d| |bias|.  With scale 0.3 (bf16 rounds 1/0.3 by 0.1%) and biases of magnitude ~30 the shift
+    reaches ~0.03; the outputs and gradients still meet the 16-bit tolerance against the float64 oracle."""
+
+    q, k, v, mask, bias, dout = make_case(dtype, prefix=(1,), rows=3, cols=96, heads=2, head=32, masked=False,
+                                          layout="swapped", seed=21)  # fmt: skip
+    bias = (bias.float() * 30.0).to(dtype)
+    run_and_check(q, k, v, mask, bias, dout, dtype, scale=0.3)
