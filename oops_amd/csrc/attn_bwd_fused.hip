@@ -25,9 +25,11 @@
 //
 // Data movement: every load of the main loop goes straight from global
 // memory to LDS (buffer_load ... lds, issued through inline assembly and
-// ordered by explicit vmcnt waits).  Each wave has its own 3-stage LDS ring
-// (Q and dO tiles with XOR-swizzled rows, raw LSE and delta), filled two
-// steps ahead, so the steps need no workgroup barrier; each group's K/V
+// ordered by explicit vmcnt waits).  Q and dO come from the head-major
+// compact copies the dQ kernel writes (2 KB contiguous per tile), -LSE/c and
+// -delta from the pack it writes beside them.  Each wave has its own 3-stage
+// LDS ring (Q and dO tiles with XOR-swizzled rows, -LSE/c and -delta), filled
+// two steps ahead, so the steps need no workgroup barrier; each group's K/V
 // block and keep bytes go into 2-buffer slots shared by the waves, one group
 // ahead; the bias of the workgroup's 32 keys and all query tiles (identity-
 // MFMA fragments, from the fragment-major copy made by attn_bias_frag_kernel)
@@ -48,7 +50,7 @@ namespace {
 
 constexpr int kFusedWaves = 8;
 constexpr int kFusedMaxSteps = 3;  // query tiles per wave: Lq <= 8 * 3 * 32
-constexpr int kFusedMaxQT = kFusedWaves * kFusedMaxSteps;  // query tiles of the bias region (the step switch has 4 cases)
+constexpr int kFusedMaxQT = kFusedWaves * kFusedMaxSteps;  // query tiles of the largest bias region
 constexpr int kQT = 32 * 32;       // elements of one 32 x 32 tile
 
 // 4 bytes per lane into 64 consecutive dwords at lds.  Every load of the
