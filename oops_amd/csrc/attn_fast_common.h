@@ -96,10 +96,13 @@ __device__ __forceinline__ void store4(T* row, int d0, float x0, float x1, float
   *reinterpret_cast<v4*>(row + d0) = v;
 }
 
+// two floats rounded to T (to nearest even) in one 32-bit word, x in the low half: a vector
+// conversion, so bf16 pairs become one v_cvt_pk_bf16_f32
 template <typename T>
 __device__ __forceinline__ uint32_t pack2(float x, float y) {
-  const uint32_t lo = __builtin_bit_cast(uint16_t, (T)x), hi = __builtin_bit_cast(uint16_t, (T)y);
-  return lo | (hi << 16);
+  typedef float F2 __attribute__((ext_vector_type(2)));
+  typedef T T2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((F2){x, y}, T2));
 }
 
 // Write one 32x32 accumulator tile's 32 head-dim values (lane (col, g) holds

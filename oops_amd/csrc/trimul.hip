@@ -697,6 +697,273 @@ __global__ __launch_bounds__(256, FULLW ? 2 : OOPS_FACTOR_BWD_OCC) void trimul_f
   }
 }
 
+// trimul_factor_v16_kernel: the factor projections for 16-bit inputs when every
+// 16 consecutive tokens share a group (positions % 16 == 0) and the W block
+// fits in LDS (c_row <= 256): the same work split and MFMA loop as the FULLW
+// form above, with a straight-line epilogue.  A wave's 32 tokens are two
+// 16-token blocks whose (group, position) are wave-uniform and stepped per tile,
+// every global access of the epilogue is 8 bytes (mask: 16) per lane, and each
+// lane stores 32 bytes per channel after the half-wave trade.
+__device__ __forceinline__ void step_block(int64_t& g, int& p, int P, int by) {
+  p += by;
+  while (p >= P) p -= P, ++g;
+}
+
+#ifndef V16_PREFETCH
+#define V16_PREFETCH !BWD
+#endif
+#ifndef V16_FWD_OCC
+#define V16_FWD_OCC 2
+#endif
+// NP: 64-wide k panels (K <= 64 NP; panels past K are zeros); MASKED: a token mask is given
+template <typename T, bool BWD, int NP, bool MASKED>
+__global__ __launch_bounds__(256, BWD ? 2 : V16_FWD_OCC) void trimul_factor_v16_kernel(FactorArgs a) {
+  using E = Elem<T>;
+  using Frag = typename E::Frag;
+  constexpr int WT = 128 * kFK;
+  extern __shared__ __attribute__((aligned(16))) char lds_raw[];
+  T* w_lds = reinterpret_cast<T*>(lds_raw);
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, lq = lane & 31, g2 = lane >> 5;
+  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x, 0);
+  if (tile >= a.tiles) return;
+  const int nb = 2 * a.cblocks;
+  const int fc = (int)(tile % nb);
+  const int f = fc / a.cblocks, cb = fc - f * a.cblocks;
+  const int64_t bmg = tile / nb;
+  const int H = a.H;
+  const int K = (int)a.c_row;
+  const int P = (int)a.positions;
+  const int64_t R = a.rows;
+
+  // the block's 128 W rows (64 value, 64 gate channels) x K, as 64-wide swizzled panels
+  {
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, (uint32_t)((int64_t)4 * H * a.c_row * 2));
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int id = tid + 256 * j, row = id >> 3, ch = id & 7;
+        const int hv = cb * 64 + (row & 63), k = p * kFK + ch * 8;
+        const int64_t o = (int64_t)(f * 2 * H + (row >= 64 ? H : 0) + hv) * a.c_row * 2 + k * 2;
+        const uint4 u = buffer_load16(wr, hv < H && k < K ? (uint32_t)o : kOut);
+        *reinterpret_cast<uint4*>(&w_lds[p * WT + swz_off<kFK>(row, ch * 8)]) = u;
+      }
+    }
+    __syncthreads();
+  }
+
+  // lane channels: tile t in {0, 1} of the accumulator holds value channel hv[t] (tile t + 2 its gate)
+  int hv[2];
+  bool hv_ok[2];
+  float bv[2], bgl[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    hv[t] = cb * 64 + 32 * t + lq;
+    hv_ok[t] = hv[t] < H;
+    const int hc = hv_ok[t] ? hv[t] : H - 1;
+    bv[t] = a.bias ? a.bias[f * 2 * H + hc] : 0.f;
+    bgl[t] = a.bias ? -a.bias[f * 2 * H + H + hc] * kLog2e : 0.f;
+  }
+
+  const int tpw = a.tpw;
+  const uint32_t x_lane = (uint32_t)((wave * 32 + lq) * a.c_row * 2);
+  auto tile_x = [&](int64_t r0, __amdgpu_buffer_rsrc_t& xr, bool& rv) {
+    const int64_t rows_left = R - r0;
+    const int nrows = (int)(rows_left < kFM ? rows_left : kFM);
+    xr = make_rsrc(static_cast<const T*>(a.xn) + r0 * a.c_row, (uint32_t)((int64_t)nrows * a.c_row * 2));
+    rv = wave * 32 + lq < nrows;
+  };
+  auto load_x_of = [&](const __amdgpu_buffer_rsrc_t& xr, bool rv, int k0, uint4 (&xf)[4]) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int k = k0 + 16 * c + 8 * g2;
+      xf[c] = buffer_load16(xr, rv && k < K ? x_lane + (uint32_t)(k * 2) : kOut);
+    }
+  };
+
+  // (group, position) of the wave's two 16-token blocks, wave-uniform
+  int64_t gb[2];
+  int pb[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t rb = bmg * tpw * kFM + wave * 32 + 16 * h;
+    gb[h] = rb / P;
+    pb[h] = (int)(rb - gb[h] * P);
+  }
+  const int64_t fG = (int64_t)f * a.groups;
+  const float* mask = a.mask;
+  float bsum[2][2] = {{0.f, 0.f}, {0.f, 0.f}};  // [t][value, gate] over this lane's tokens
+
+  uint4 xs[2][4];  // panel i of a tile in xs[i % 2]; xs[0] may hold the next tile's first panel
+  bool prefetched = false;
+  for (int it = 0; it < tpw; ++it) {
+    const int64_t r0 = (bmg * tpw + it) * kFM;
+    if (r0 >= R) break;
+    __amdgpu_buffer_rsrc_t xr;
+    bool rv;
+    tile_x(r0, xr, rv);
+    if (!prefetched) load_x_of(xr, rv, 0, xs[0]);
+
+    // the epilogue's loads go out before the MFMA loop (and before the next tile's prefetch, which
+    // the epilogue must not wait for).  Accumulator entry 4q + i is token r0 + 32 wave + 8q + 4 g2 + i,
+    // in block q / 2.
+    const int64_t rw = r0 + wave * 32;
+    const bool blk_ok[2] = {rw < R, rw + 16 < R};  // R % 16 == 0: a block is wholly in or out
+    // element offsets of block h's first token in the [f][G][H][P] factor layout, channel 0
+    const int64_t fbase[2] = {(fG + gb[0]) * H * P + pb[0], (fG + gb[1]) * H * P + pb[1]};
+    float keep[4][4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float4 k4 = make_float4(1.f, 1.f, 1.f, 1.f);
+      if (MASKED && blk_ok[q >> 1]) k4 = *reinterpret_cast<const float4*>(mask + rw + 8 * q + 4 * g2);
+      keep[q][0] = k4.x, keep[q][1] = k4.y, keep[q][2] = k4.z, keep[q][3] = k4.w;
+    }
+    uint2 dpre[2][4];
+    if constexpr (BWD) {
+      const T* gf = static_cast<const T*>(a.grad_factors);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          dpre[t][q] = hv_ok[t] && blk_ok[q >> 1]
+                           ? *reinterpret_cast<const uint2*>(gf + fbase[q >> 1] + (int64_t)hv[t] * P + 8 * (q & 1) + 4 * g2)
+                           : make_uint2(0, 0);
+    }
+
+    // the first panel starts from zero accumulators (no register clear)
+    f32x16 acc[4];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      if (i + 1 < NP) load_x_of(xr, rv, (i + 1) * kFK, xs[(i + 1) & 1]);
+      const T* wt = &w_lds[i * WT];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const Frag afr = __builtin_bit_cast(Frag, xs[i & 1][c]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const Frag bfr = lds_frag<T>(wt + swz_off<kFK>(32 * t + lq, 16 * c + 8 * g2));
+          // the first panel starts from zero accumulators (no register clear)
+          acc[t] = E::mma(afr, bfr, i == 0 && c == 0 ? f32x16{} : acc[t]);
+        }
+      }
+    }
+    // the next tile's first panel loads while this tile's epilogue runs
+    prefetched = V16_PREFETCH && it + 1 < tpw && r0 + kFM < R;
+    if (prefetched) {
+      __amdgpu_buffer_rsrc_t xr_n;
+      bool rv_n;
+      tile_x(r0 + kFM, xr_n, rv_n);
+      load_x_of(xr_n, rv_n, 0, xs[0]);
+    }
+
+    float mp[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) mp[v] = 0.f;
+    const int64_t r16 = rw + 16 * g2;
+    const bool st_ok = g2 ? blk_ok[1] : blk_ok[0];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      uint32_t po[8], pg[8];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float o[4], og[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v = acc[t][4 * q + i] + bv[t];
+          const float s = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(__builtin_fmaf(acc[t + 2][4 * q + i], -kLog2e, bgl[t])));
+          if constexpr (!BWD) {
+            o[i] = v * s * keep[q][i];
+          } else {
+            const uint32_t u = i < 2 ? dpre[t][q].x : dpre[t][q].y;
+            const float d = (i & 1) ? hi_f<T>(u) : lo_f<T>(u);
+            const float dk = d * keep[q][i], vs = v * s;
+            mp[4 * q + i] += d * vs;
+            o[i] = dk * s;                      // value gradient
+            og[i] = dk * vs * (1.f - s);        // gate-logit gradient
+          }
+        }
+        po[2 * q] = pack2<T>(o[0], o[1]), po[2 * q + 1] = pack2<T>(o[2], o[3]);
+        if constexpr (BWD) {
+          pg[2 * q] = pack2<T>(og[0], og[1]), pg[2 * q + 1] = pack2<T>(og[2], og[3]);
+          // the bias gradient sums the float32 values (before their rounding to the dtype)
+          bsum[t][0] += (o[0] + o[1]) + (o[2] + o[3]);
+          bsum[t][1] += (og[0] + og[1]) + (og[2] + og[3]);
+        }
+      }
+      uint4 lo, hi;
+      trade16(po, lo, hi);
+      if constexpr (!BWD) {
+        if (hv_ok[t] && st_ok) {
+          T* dst = static_cast<T*>(a.factors) + (g2 ? fbase[1] : fbase[0]) + (int64_t)hv[t] * P;
+          *reinterpret_cast<uint4*>(dst) = lo;
+          *reinterpret_cast<uint4*>(dst + 8) = hi;
+        }
+      } else {
+        uint4 glo, ghi;
+        trade16(pg, glo, ghi);
+        if (hv_ok[t] && st_ok) {
+          T* gp = static_cast<T*>(a.grad_proj);
+          T* dv16 = gp + (int64_t)(f * 2 * H + hv[t]) * R + r16;
+          T* dg16 = dv16 + (int64_t)H * R;
+          *reinterpret_cast<uint4*>(dv16) = lo;
+          *reinterpret_cast<uint4*>(dv16 + 8) = hi;
+          *reinterpret_cast<uint4*>(dg16) = glo;
+          *reinterpret_cast<uint4*>(dg16 + 8) = ghi;
+        }
+      }
+    }
+    if constexpr (BWD && MASKED) {
+      if (a.mask_parts != nullptr) {
+        // sum over the 32 channels of the half-wave by recursive halving: after the steps over lane
+        // bits 4..1, lane lq holds the sum for entry lq / 2 (bit 4 picks the upper 8 entries, ...)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int half = 8 >> s, bit = 16 >> s;
+          // per-lane select mask (bit arithmetic, so the selection stays on the two registers)
+          const uint32_t up = (lq & bit) ? 0xffffffffu : 0u;
+#pragma unroll
+          for (int j = 0; j < half; ++j) {
+            const uint32_t x = __builtin_bit_cast(uint32_t, mp[j]), y = __builtin_bit_cast(uint32_t, mp[half + j]);
+            const float keep_v = __builtin_bit_cast(float, (y & up) | (x & ~up));
+            const float send = __builtin_bit_cast(float, (x & up) | (y & ~up));
+            mp[j] = keep_v + __shfl_xor(send, bit);
+          }
+        }
+        mp[0] += __shfl_xor(mp[0], 1);
+        const int v = lq >> 1, q = v >> 2;
+        if ((lq & 1) == 0 && blk_ok[q >> 1])
+          a.mask_parts[(int64_t)(f * a.cblocks + cb) * R + rw + 8 * q + 4 * g2 + (v & 3)] = mp[0];
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) step_block(gb[h], pb[h], P, kFM);
+  }
+
+  if constexpr (BWD) {
+    if (a.bias_parts == nullptr) return;
+    // channel sums: the two half-waves, then the four waves through LDS
+    __shared__ float bred[4][2][2][32];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        bsum[t][k] += __shfl_xor(bsum[t][k], 32);
+        if (g2 == 0) bred[wave][t][k][lq] = bsum[t][k];
+      }
+    __syncthreads();
+    if (tid < 128) {
+      const int t = tid >> 6, k = (tid >> 5) & 1, c = tid & 31;
+      const int h = cb * 64 + 32 * t + c;
+      if (h < H) {
+        const float sum = bred[0][t][k][c] + bred[1][t][k][c] + bred[2][t][k][c] + bred[3][t][k][c];
+        a.bias_parts[bmg * 4 * H + f * 2 * H + k * H + h] = sum;
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------ output LayerNorm (channel-major)
 struct OutNormArgs {
   const void* comb;
@@ -1201,7 +1468,7 @@ int64_t trimul_mask_parts(const oops_trimul_geometry& g) { return 2 * factor_cbl
 
 namespace {
 struct FactorPlan {
-  bool fullw;
+  bool fullw, v16;
   int tpw;
   int64_t groups, tiles;
   size_t lds;
@@ -1210,13 +1477,16 @@ FactorPlan factor_plan(const oops_trimul_geometry& g, bool backward) {
   const int64_t cblocks = factor_cblocks(g);
   const int64_t token_tiles = (g.groups * g.positions + kFM - 1) / kFM;
   FactorPlan pl{};
-  // the backward's epilogue holds more live values: the streaming form keeps it under 256 VGPRs
-  pl.fullw = g.c_row <= kFullWMaxK && !backward;
+  // 16-token blocks within one group: the straight-line kernel, W whole in LDS.  Otherwise the
+  // backward's epilogue holds more live values: the streaming form keeps it under 256 VGPRs
+  pl.v16 = g.positions % 16 == 0 && g.c_row <= kFullWMaxK;
+  pl.fullw = g.c_row <= kFullWMaxK && (!backward || pl.v16);
   // about 2048 workgroups: each keeps its W block across several token tiles
   pl.tpw = pl.fullw ? (int)std::max<int64_t>(1, (token_tiles * 2 * cblocks + 2047) / 2048) : 1;
   pl.groups = (token_tiles + pl.tpw - 1) / pl.tpw;
   pl.tiles = pl.groups * 2 * cblocks;
-  const int64_t panels = (g.c_row + kFK - 1) / kFK;
+  int64_t panels = (g.c_row + kFK - 1) / kFK;
+  if (pl.v16 && panels == 3) panels = 4;  // the straight-line kernel is built for 1, 2 or 4 panels
   pl.lds = (size_t)(pl.fullw ? panels : 2) * 128 * kFK * 2;
   return pl;
 }
@@ -1249,7 +1519,24 @@ hipError_t launch_trimul_factors(const oops_trimul_geometry& g, const void* norm
   const dim3 grid((unsigned)xcd_grid(pl.tiles, 0));
   return by_half(g.dtype, [&](auto tag) -> hipError_t {
     using T = decltype(tag);
-    if (bwd && pl.fullw)
+    if (pl.v16) {
+      const int np = (int)((g.c_row + kFK - 1) / kFK);
+      auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(256), pl.lds, stream, a); };
+      auto by_np = [&](auto bwd_tag, auto masked_tag) {
+        constexpr bool B = decltype(bwd_tag)::value, M = decltype(masked_tag)::value;
+        if (np == 1)
+          go(trimul_factor_v16_kernel<T, B, 1, M>);
+        else if (np == 2)
+          go(trimul_factor_v16_kernel<T, B, 2, M>);
+        else
+          go(trimul_factor_v16_kernel<T, B, 4, M>);
+      };
+      const bool m = a.mask != nullptr;
+      if (bwd)
+        m ? by_np(std::true_type{}, std::true_type{}) : by_np(std::true_type{}, std::false_type{});
+      else
+        m ? by_np(std::false_type{}, std::true_type{}) : by_np(std::false_type{}, std::false_type{});
+    } else if (bwd && pl.fullw)
       hipLaunchKernelGGL((trimul_factor_kernel<T, true, true>), grid, dim3(256), pl.lds, stream, a);
     else if (bwd)
       hipLaunchKernelGGL((trimul_factor_kernel<T, true, false>), grid, dim3(256), pl.lds, stream, a);

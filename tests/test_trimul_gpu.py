@@ -94,6 +94,10 @@ def _check(pair, mask, weights, bs, direction, dtype, grads=True, mask_grad=Fals
         (torch.bfloat16, 32, 32, 16, (2,), "incoming", True),
         (torch.bfloat16, 32, 32, 12, (), "incoming", True),  # 4 | positions, 16 does not: 8-byte factor stores
         (torch.float16, 64, 64, 48, (), "outgoing", True),  # 16 | positions: traded 32-byte stores
+        (torch.bfloat16, 32, 96, 48, (), "incoming", True),  # 16 | positions, the second channel block partial
+        (torch.float16, 128, 64, 32, (3,), "outgoing", True),  # 16 | positions, several tiles per workgroup
+        (torch.bfloat16, 192, 64, 16, (2,), "outgoing", True),  # three k panels, run as four (the last zero)
+        (torch.float16, 256, 32, 32, (), "incoming", False),  # four k panels, no mask
         (torch.float16, 8, 12, 9, (), "outgoing", False),
         (torch.bfloat16, 17, 24, 7, (), "outgoing", True),
         (torch.float16, 65, 96, 17, (), "incoming", True),
