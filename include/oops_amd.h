@@ -303,6 +303,33 @@ int oops_trimul_output_backward(const oops_trimul_geometry* geo, const void* nor
                                 const float* output_bias, const float* gate_bias, const void* grad_out,
                                 void* grad_value, void* grad_gate, void* stream);
 
+/* ---- float32 partial sums -------------------------------------------------
+ *
+ * The backward kernels above write float32 partial sums (mask, bias and
+ * LayerNorm affine gradients, per-chunk weight gradients) that still have to
+ * be summed over their leading axis.  The reference sums its partials with
+ * torch reductions (oops/pair/triangle_multiplication/triton/generic.py:824,
+ * :1017-1018, :1092, :1115); this entry point sums up to
+ * OOPS_SUM_MAX_SEGMENTS such arrays:
+ *   out[j] = sum over p = 0 .. count-1 of parts[p * part_stride + j],  j < n,
+ * in a fixed order (bit-identical on every call), rounded once to out_dtype.
+ * Arrays of more than 64 rows are summed in two launches through the caller's
+ * workspace (float32 chunk sums, 256-byte aligned, of
+ * oops_sum_partials_workspace_bytes bytes; NULL when that is 0). */
+#define OOPS_SUM_MAX_SEGMENTS 16
+typedef struct oops_sum_segment {
+  const float* parts;  /* count rows of n float32 values, part_stride elements apart */
+  void* out;           /* n values of out_dtype */
+  int64_t count;
+  int64_t n;
+  int64_t part_stride; /* >= n */
+  int32_t out_dtype;   /* OOPS_F32 / OOPS_BF16 / OOPS_F16 */
+  int32_t reserved;    /* 0 */
+} oops_sum_segment;
+size_t oops_sum_partials_workspace_bytes(const oops_sum_segment* segments, int32_t num_segments);
+int oops_sum_partials(const oops_sum_segment* segments, int32_t num_segments, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
 /* Thread-local description of the last failure (empty string if none). */
 const char* oops_last_error(void);
 

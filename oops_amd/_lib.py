@@ -57,6 +57,8 @@ EXPORTED_SYMBOLS = (
     "oops_trimul_output_norm_backward",
     "oops_trimul_output_forward",
     "oops_trimul_output_backward",
+    "oops_sum_partials_workspace_bytes",
+    "oops_sum_partials",
     "oops_last_error",
     "oops_abi_version",
 )
@@ -121,6 +123,21 @@ class TrimulGeometry(ctypes.Structure):
         ("c_row", ctypes.c_int64),
         ("h_row", ctypes.c_int64),
         ("eps", ctypes.c_float),
+    ]
+
+
+SUM_MAX_SEGMENTS = 16
+
+
+class SumSegment(ctypes.Structure):
+    _fields_ = [
+        ("parts", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("count", ctypes.c_int64),
+        ("n", ctypes.c_int64),
+        ("part_stride", ctypes.c_int64),
+        ("out_dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 
@@ -191,6 +208,10 @@ def load() -> ctypes.CDLL:
         lib.oops_trimul_output_forward.restype = i32
         lib.oops_trimul_output_backward.argtypes = [tg, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
         lib.oops_trimul_output_backward.restype = i32
+        lib.oops_sum_partials_workspace_bytes.argtypes = [ctypes.POINTER(SumSegment), ctypes.c_int32]
+        lib.oops_sum_partials_workspace_bytes.restype = sz
+        lib.oops_sum_partials.argtypes = [ctypes.POINTER(SumSegment), ctypes.c_int32, vp, sz, vp]
+        lib.oops_sum_partials.restype = i32
         lib.oops_last_error.argtypes = []
         lib.oops_last_error.restype = ctypes.c_char_p
         lib.oops_abi_version.argtypes = []

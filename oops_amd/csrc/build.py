@@ -35,6 +35,7 @@ SOURCES = (
     "gate.hip",
     "trimul.hip",
     "trimul_f32.hip",
+    "reduce.hip",
     "capi.cpp",
 )
 FAST_MATH_SOURCES = ("attn_fwd_fast.hip", "attn_bwd_fast.hip", "attn_bwd_fused.hip")

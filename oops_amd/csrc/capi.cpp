@@ -11,6 +11,7 @@
 
 #include "attn_kernels.h"
 #include "gate_kernels.h"
+#include "reduce_kernels.h"
 #include "trimul_kernels.h"
 
 namespace {
@@ -605,6 +606,42 @@ int oops_trimul_output_backward(const oops_trimul_geometry* geo, const void* nor
                                                        output_bias, gate_bias, nullptr, grad_out, grad_value,
                                                        grad_gate, static_cast<hipStream_t>(stream)),
                             "triangle multiplication output backward");
+}
+
+namespace {
+int check_sum_segments(const oops_sum_segment* segments, int32_t num_segments) {
+  if (num_segments < 0 || num_segments > OOPS_SUM_MAX_SEGMENTS)
+    return fail(OOPS_EINVAL, "num_segments %lld outside 0..%lld", num_segments, OOPS_SUM_MAX_SEGMENTS);
+  if (num_segments > 0 && segments == nullptr) return fail(OOPS_EINVAL, "segments must be non-NULL");
+  for (int i = 0; i < num_segments; ++i) {
+    const oops_sum_segment& s = segments[i];
+    if (s.n < 0 || s.count < 0 || s.part_stride < s.n)
+      return fail(OOPS_EINVAL, "segment %lld: need n >= 0, count >= 0 and part_stride >= n", i);
+    if (s.out_dtype != OOPS_F32 && s.out_dtype != OOPS_BF16 && s.out_dtype != OOPS_F16)
+      return fail(OOPS_EINVAL, "segment %lld: unsupported out_dtype %lld", i, s.out_dtype);
+    if (s.n > 0 && (s.out == nullptr || (s.count > 0 && s.parts == nullptr)))
+      return fail(OOPS_EINVAL, "segment %lld: parts and out must be non-NULL", i);
+  }
+  return OOPS_OK;
+}
+}  // namespace
+
+size_t oops_sum_partials_workspace_bytes(const oops_sum_segment* segments, int32_t num_segments) {
+  g_last_error.clear();
+  if (check_sum_segments(segments, num_segments)) return 0;
+  return oops::sum_partials_workspace_bytes(segments, num_segments);
+}
+
+int oops_sum_partials(const oops_sum_segment* segments, int32_t num_segments, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_sum_segments(segments, num_segments)) return rc;
+  const size_t need = oops::sum_partials_workspace_bytes(segments, num_segments);
+  if (workspace_bytes < need || (need > 0 && (workspace == nullptr || reinterpret_cast<uintptr_t>(workspace) % 256)))
+    return fail(OOPS_EINVAL, "workspace of %lld bytes (256-byte aligned) needed, %lld given", (long long)need,
+                (long long)workspace_bytes);
+  return gate_launch_result(
+      oops::launch_sum_partials(segments, num_segments, workspace, static_cast<hipStream_t>(stream)), "partial sums");
 }
 
 }  // extern "C"

@@ -32,6 +32,7 @@ from torch.nn import functional as F
 
 from .. import _lib
 from .._errors import unsupported
+from .._partials import PartialSums
 from ..attention._runtime import is_nested, require_no_forward_mode, require_same_device
 
 _OPERATOR = "triangle_multiplication"
@@ -229,39 +230,33 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def _long_k_matmul(a: Tensor, b: Tensor) -> Tensor:
-    """``a (M, K) @ b (K, N)`` for a long K (weight gradients over every pair cell), rounded once to a's dtype."""
+def _long_k_partials(a: Tensor, b: Tensor) -> Tensor:
+    """float32 partial products of ``a (M, K) @ b (K, N)`` for a long K (weight gradients over every pair
+    cell), (parts, M, N): their sum is the product.
 
-    return _long_k_matmul_f32(a, b).to(a.dtype)
-
-
-def _column_sum(x: Tensor) -> Tensor:
-    """float32 sums over the rows of ``x (K, N)`` (bias gradients): a ones-row GEMM with float32 outputs,
-    faster than a float32 reduction of the 16-bit rows and accumulated in shorter chunks."""
-
-    return _long_k_matmul_f32(x.new_ones(1, x.shape[0]), x)[0]
-
-
-def _long_k_matmul_f32(a: Tensor, b: Tensor) -> Tensor:
-    """``a (M, K) @ b (K, N)`` in float32 for a long K.
-
-    Split into up to 64 K-chunks as one batched GEMM with float32 outputs, the
-    chunks summed in float32: the library's single GEMM of this shape leaves
-    most of the GPU idle.
+    K is split into up to 64 chunks as one batched GEMM with float32 outputs (the library's single GEMM of
+    this shape leaves most of the GPU idle); a remainder of K past the chunks is one more part.
     """
 
     k = a.shape[1]
     chunks = min(64, k // 1024)
     if chunks < 2:
-        return a.float().mm(b.float())
+        return a.float().mm(b.float())[None]
     main = k // chunks * chunks
     step = main // chunks
     a_c = a[:, :main].unflatten(1, (chunks, step)).transpose(0, 1)  # (chunks, M, step), strided view
     b_c = b[:main].view(chunks, step, b.shape[1]) if b.is_contiguous() else b[:main].reshape(chunks, step, -1)
-    out = torch.bmm(a_c, b_c, out_dtype=torch.float32).sum(0)
+    parts = torch.bmm(a_c, b_c, out_dtype=torch.float32)
     if main < k:
-        out = out + a[:, main:].float().mm(b[main:].float())
-    return out
+        parts = torch.cat([parts, a[:, main:].float().mm(b[main:].float())[None]])
+    return parts
+
+
+def _column_partials(x: Tensor) -> Tensor:
+    """float32 partial column sums of ``x (K, N)`` (bias gradients), (parts, 1, N): a ones-row GEMM with
+    float32 outputs, faster than a float32 reduction of the 16-bit rows."""
+
+    return _long_k_partials(x.new_ones(1, x.shape[0]), x)
 
 
 def _geometry(pair: Tensor, hidden: int, has_mask: bool, eps: float) -> _lib.TrimulGeometry:
@@ -454,10 +449,12 @@ def trimul_backward(
         gv, gg = g_val[:, :C], g_gate[:, :C]
         d_nrm = gv.mm(wo[:, :H]).contiguous()  # (R, H)
         d_xn = gg.mm(wog[:, :C])  # (R, C)
-        d_wo = F.pad(_long_k_matmul(gv.t(), nrm[:, :H]), (0, hp - H)) if hp != H else _long_k_matmul(gv.t(), nrm[:, :H])
-        d_wog = F.pad(_long_k_matmul(gg.t(), xn[:, :C]), (0, cp - C)) if cp != C else _long_k_matmul(gg.t(), xn[:, :C])
-        d_bo = _column_sum(gv) if bo is not None else empty()
-        d_bog = _column_sum(gg) if bog is not None else empty()
+        # every float32 partial (K-chunk products, per-workgroup sums) is summed by one launch at the end
+        sums = PartialSums()
+        d_wo = sums.add(_long_k_partials(gv.t(), nrm[:, :H]), dtype)
+        d_wog = sums.add(_long_k_partials(gg.t(), xn[:, :C]), dtype)
+        d_bo = sums.add(_column_partials(gv))[0] if bo is not None else empty()
+        d_bog = sums.add(_column_partials(gg))[0] if bog is not None else empty()
 
         d_comb = torch.empty(G, H, P, dtype=dtype, device=dev)
         on_parts = torch.empty(2, lib.oops_trimul_output_norm_parts(ctypes.byref(geo)), H, dtype=torch.float32,
@@ -478,10 +475,8 @@ def trimul_backward(
                                                     _ptr(bparts), stream),
                    "triangle_multiplication factor backward")  # fmt: skip
         d_xn = torch.addmm(d_xn, d_proj.t(), w_cat[:, :C]).contiguous()
-        d_wcat = _long_k_matmul(d_proj, xn[:, :C])
-        if cp != C:
-            d_wcat = F.pad(d_wcat, (0, cp - C))
-        d_bcat = bparts.sum(0) if b_cat is not None else empty()
+        d_wcat = sums.add(_long_k_partials(d_proj, xn[:, :C]), dtype)
+        d_bcat = sums.add(bparts) if b_cat is not None else empty()
 
         d_pair = torch.empty(G, P, C, dtype=dtype, device=dev)
         rg = _row_geometry(dtype, R, C, C, C, eps_in)
@@ -491,9 +486,16 @@ def trimul_backward(
                                                      _ptr(rstd_in), _ptr(d_xn), _ptr(d_pair), _ptr(in_parts[0]),
                                                      _ptr(in_parts[1]), stream),
                    "triangle_multiplication input LayerNorm backward")  # fmt: skip
-    d_mask = mparts.sum(0).view(G, P) if want_mask else empty()
-    return (d_pair, d_mask, d_wcat, d_bcat, d_wo, d_wog, d_bo, d_bog, in_parts[0].sum(0), in_parts[1].sum(0),
-            on_parts[0].sum(0), on_parts[1].sum(0))  # fmt: skip
+        d_mask = sums.add(mparts).view(G, P) if want_mask else empty()
+        d_in_w, d_in_b = sums.add(in_parts[0]), sums.add(in_parts[1])
+        d_on_w, d_on_b = sums.add(on_parts[0]), sums.add(on_parts[1])
+        sums.run(stream)
+    # projection gradients padded back to the operands' 16-byte rows
+    if cp != C:
+        d_wog, d_wcat = F.pad(d_wog, (0, cp - C)), F.pad(d_wcat, (0, cp - C))
+    if hp != H:
+        d_wo = F.pad(d_wo, (0, hp - H))
+    return (d_pair, d_mask, d_wcat, d_bcat, d_wo, d_wog, d_bo, d_bog, d_in_w, d_in_b, d_on_w, d_on_b)
 
 
 @trimul_backward.register_fake

@@ -212,3 +212,30 @@ def test_forward_noalloc_rejects_oversized_scratch(lib):
     # pointer checks come before any device call
     geo, keep = _geometry(c3_table())
     assert lib.oops_attn_forward_noalloc(ctypes.byref(geo), None, 1, 1, None, 1, 1, None, 1, None) == 1
+
+
+def test_sum_partials_validates_on_the_host(lib):
+    """oops_sum_partials checks its descriptors before any launch; zero segments launch nothing."""
+
+    text = HEADER.read_text()
+    assert int(re.search(r"#define\s+OOPS_SUM_MAX_SEGMENTS\s+(\d+)", text).group(1)) == _lib.SUM_MAX_SEGMENTS
+    assert ctypes.sizeof(_lib.SumSegment) == 48
+    assert lib.oops_sum_partials(None, 0, None, 0, None) == 0
+    segs = (_lib.SumSegment * (_lib.SUM_MAX_SEGMENTS + 1))()
+    assert lib.oops_sum_partials(segs, _lib.SUM_MAX_SEGMENTS + 1, None, 0, None) != 0
+    assert b"num_segments" in lib.oops_last_error()
+    assert lib.oops_sum_partials(None, 1, None, 0, None) != 0
+    seg = segs[0]
+    seg.parts, seg.out, seg.count, seg.n, seg.part_stride, seg.out_dtype = 16, 16, 2, 8, 4, _lib.F32
+    assert lib.oops_sum_partials(segs, 1, None, 0, None) != 0  # part_stride below n
+    assert b"part_stride" in lib.oops_last_error()
+    seg.part_stride, seg.out_dtype = 8, 9
+    assert lib.oops_sum_partials(segs, 1, None, 0, None) != 0
+    assert b"out_dtype" in lib.oops_last_error()
+    seg.out_dtype, seg.out = _lib.BF16, None
+    assert lib.oops_sum_partials(segs, 1, None, 0, None) != 0
+    assert b"non-NULL" in lib.oops_last_error()
+    seg.out, seg.count = 16, 65  # more than 64 rows: a workspace of 2 chunk rows
+    assert lib.oops_sum_partials_workspace_bytes(segs, 1) == 256
+    assert lib.oops_sum_partials(segs, 1, None, 0, None) != 0
+    assert b"workspace" in lib.oops_last_error()
