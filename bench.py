@@ -433,7 +433,8 @@ def trimul_stage(device, n=512, c=128, h=128, dtype="bf16"):
     with torch.no_grad():
         grouped = pair.detach().reshape(1, rows, c)
         ops = tm._prepare(grouped, mask.reshape(1, rows), tuple(list(w.values())[:10]), tuple(list(w.values())[10:]))
-        _pair, mask32, w_cat, b_cat = ops[:4]
+        _pair, mask32, w_cat = ops[:3]
+        b_cat = tm._small_views(ops[5], ops[6])[0]
         saved = tm.trimul_forward(*ops, [0, n], "outgoing", 1e-5, 1e-5)
         xn, factors = saved[1], saved[4]
         geo = tm._geometry(grouped, h, True, 1e-5)

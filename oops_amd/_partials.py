@@ -20,12 +20,13 @@ _OUT_DTYPE = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16:
 
 class PartialSums:
     """``add`` registers ``parts`` (P, *shape) float32 and returns the (still unwritten) ``shape`` result in
-    ``dtype``; ``run`` sums every registered array (several launches only past SUM_MAX_SEGMENTS arrays)."""
+    ``dtype`` (or in the given contiguous ``out``); ``run`` sums every registered array (one launch per
+    SUM_MAX_SEGMENTS arrays, two when an array has more than 64 rows)."""
 
     def __init__(self) -> None:
         self._segs: list[tuple[Tensor, Tensor]] = []
 
-    def add(self, parts: Tensor, dtype: torch.dtype = torch.float32) -> Tensor:
+    def add(self, parts: Tensor, dtype: torch.dtype = torch.float32, out: Tensor | None = None) -> Tensor:
         if parts.dtype != torch.float32 or parts.dim() < 1:
             raise TypeError("partial sums take float32 arrays with a leading parts axis")
         n = 1
@@ -34,7 +35,10 @@ class PartialSums:
         rows = parts.reshape(parts.shape[0], n)
         if rows.numel() and rows.stride(1) != 1:
             rows = rows.contiguous()
-        out = torch.empty(parts.shape[1:], dtype=dtype, device=parts.device)
+        if out is None:
+            out = torch.empty(parts.shape[1:], dtype=dtype, device=parts.device)
+        elif not out.is_contiguous() or out.numel() != rows.shape[1]:
+            raise ValueError("a partial-sum destination must be contiguous with one value per column")
         self._segs.append((rows, out))
         return out
 

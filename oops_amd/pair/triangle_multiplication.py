@@ -327,29 +327,35 @@ def _pairs(blocks: List[int]):
     return [(blocks[i], blocks[i + 1]) for i in range(0, len(blocks), 2)]
 
 
+# The small float32 parameters travel as one buffer ``small`` with ``spans`` = [start, end] per entry of
+# _SMALL (-1, -1 when absent): one operand and one gradient instead of seven slices, whose separate
+# gradients autograd would each scatter into a zero-filled copy of the buffer.
+_SMALL = ("b4", "bo", "bog", "in_w", "in_b", "on_w", "on_b")
+
+
+def _small_views(small: Tensor, spans: List[int]) -> List[Optional[Tensor]]:
+    return [None if spans[2 * i] < 0 else small[spans[2 * i] : spans[2 * i + 1]] for i in range(len(_SMALL))]
+
+
 @torch.library.custom_op("oops_amd::trimul_forward", mutates_args=(), device_types="cuda")
 def trimul_forward(
     pair: Tensor,
     mask: Optional[Tensor],
     w_cat: Tensor,
-    b_cat: Optional[Tensor],
     wo: Tensor,
     wog: Tensor,
-    bo: Optional[Tensor],
-    bog: Optional[Tensor],
-    in_w: Tensor,
-    in_b: Tensor,
-    on_w: Tensor,
-    on_b: Tensor,
+    small: Tensor,
+    spans: List[int],
     blocks: List[int],
     direction: str,
     eps_in: float,
     eps_out: float,
 ) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Forward on prepared operands: pair (G, P, C); float32 mask (G, P); w_cat [4H][c_row]; wo [C][h_row];
-    wog [C][c_row]; float32 biases and LayerNorm affines.  Returns (out, xn, mean_in, rstd_in, factors,
-    combined, nrm, mean_out, rstd_out); all but ``out`` are kept for the backward."""
+    wog [C][c_row]; the float32 biases and LayerNorm affines in ``small`` (``spans``).  Returns (out, xn,
+    mean_in, rstd_in, factors, combined, nrm, mean_out, rstd_out); all but ``out`` are kept for the backward."""
 
+    b_cat, bo, bog, in_w, in_b, on_w, on_b = _small_views(small, spans)
     lib = _lib.load()
     G, P, C = pair.shape
     H = w_cat.shape[0] // 4
@@ -386,7 +392,7 @@ def trimul_forward(
 
 
 @trimul_forward.register_fake
-def _(pair, mask, w_cat, b_cat, wo, wog, bo, bog, in_w, in_b, on_w, on_b, blocks, direction, eps_in, eps_out):
+def _(pair, mask, w_cat, wo, wog, small, spans, blocks, direction, eps_in, eps_out):
     G, P, C = pair.shape
     H = w_cat.shape[0] // 4
     R = G * P
@@ -402,13 +408,10 @@ def trimul_backward(
     pair: Tensor,
     mask: Optional[Tensor],
     w_cat: Tensor,
-    b_cat: Optional[Tensor],
     wo: Tensor,
     wog: Tensor,
-    bo: Optional[Tensor],
-    bog: Optional[Tensor],
-    in_w: Tensor,
-    on_w: Tensor,
+    small: Tensor,
+    spans: List[int],
     xn: Tensor,
     mean_in: Tensor,
     rstd_in: Tensor,
@@ -422,10 +425,13 @@ def trimul_backward(
     eps_in: float,
     eps_out: float,
     need_mask: bool,
-) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """Gradients of every prepared operand: (pair, mask, w_cat, b_cat, wo, wog, bo, bog, in_w, in_b, on_w,
-    on_b); an absent optional operand gets an empty tensor."""
+) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Gradients of the prepared operands: (pair, mask, w_cat, wo, wog, small); the mask gradient is empty
+    when not needed."""
 
+    b_cat, bo, bog, in_w, _in_b, on_w, _on_b = _small_views(small, spans)
+    d_small = torch.empty_like(small)
+    d_views = _small_views(d_small, spans)
     lib = _lib.load()
     G, P, C = pair.shape
     H = factors.shape[2]
@@ -453,8 +459,10 @@ def trimul_backward(
         sums = PartialSums()
         d_wo = sums.add(_long_k_partials(gv.t(), nrm[:, :H]), dtype)
         d_wog = sums.add(_long_k_partials(gg.t(), xn[:, :C]), dtype)
-        d_bo = sums.add(_column_partials(gv))[0] if bo is not None else empty()
-        d_bog = sums.add(_column_partials(gg))[0] if bog is not None else empty()
+        if bo is not None:
+            sums.add(_column_partials(gv), out=d_views[1])
+        if bog is not None:
+            sums.add(_column_partials(gg), out=d_views[2])
 
         d_comb = torch.empty(G, H, P, dtype=dtype, device=dev)
         on_parts = torch.empty(2, lib.oops_trimul_output_norm_parts(ctypes.byref(geo)), H, dtype=torch.float32,
@@ -476,7 +484,8 @@ def trimul_backward(
                    "triangle_multiplication factor backward")  # fmt: skip
         d_xn = torch.addmm(d_xn, d_proj.t(), w_cat[:, :C]).contiguous()
         d_wcat = sums.add(_long_k_partials(d_proj, xn[:, :C]), dtype)
-        d_bcat = sums.add(bparts) if b_cat is not None else empty()
+        if b_cat is not None:
+            sums.add(bparts, out=d_views[0])
 
         d_pair = torch.empty(G, P, C, dtype=dtype, device=dev)
         rg = _row_geometry(dtype, R, C, C, C, eps_in)
@@ -487,37 +496,34 @@ def trimul_backward(
                                                      _ptr(in_parts[1]), stream),
                    "triangle_multiplication input LayerNorm backward")  # fmt: skip
         d_mask = sums.add(mparts).view(G, P) if want_mask else empty()
-        d_in_w, d_in_b = sums.add(in_parts[0]), sums.add(in_parts[1])
-        d_on_w, d_on_b = sums.add(on_parts[0]), sums.add(on_parts[1])
+        for i, parts in ((3, in_parts[0]), (4, in_parts[1]), (5, on_parts[0]), (6, on_parts[1])):
+            sums.add(parts, out=d_views[i])
         sums.run(stream)
     # projection gradients padded back to the operands' 16-byte rows
     if cp != C:
         d_wog, d_wcat = F.pad(d_wog, (0, cp - C)), F.pad(d_wcat, (0, cp - C))
     if hp != H:
         d_wo = F.pad(d_wo, (0, hp - H))
-    return (d_pair, d_mask, d_wcat, d_bcat, d_wo, d_wog, d_bo, d_bog, d_in_w, d_in_b, d_on_w, d_on_b)
+    return d_pair, d_mask, d_wcat, d_wo, d_wog, d_small
 
 
 @trimul_backward.register_fake
-def _(dout, pair, mask, w_cat, b_cat, wo, wog, bo, bog, in_w, on_w, xn, mean_in, rstd_in, factors, combined, nrm,
-      mean_out, rstd_out, blocks, direction, eps_in, eps_out, need_mask):  # fmt: skip
+def _(dout, pair, mask, w_cat, wo, wog, small, spans, xn, mean_in, rstd_in, factors, combined, nrm, mean_out,
+      rstd_out, blocks, direction, eps_in, eps_out, need_mask):  # fmt: skip
     G, P, C = pair.shape
-    H = factors.shape[2]
-    f32 = dict(dtype=torch.float32, device=pair.device)
-    opt = lambda t, *shape: pair.new_empty(0, **f32) if t is None else pair.new_empty(*shape, **f32)  # noqa: E731
-    return (pair.new_empty(G, P, C), opt(mask if need_mask else None, G, P),
-            torch.empty_like(w_cat), opt(b_cat, 4 * H), torch.empty_like(wo), torch.empty_like(wog), opt(bo, C),
-            opt(bog, C), pair.new_empty(C, **f32), pair.new_empty(C, **f32), pair.new_empty(H, **f32),
-            pair.new_empty(H, **f32))  # fmt: skip
+    d_mask = pair.new_empty(G, P, dtype=torch.float32) if mask is not None and need_mask else pair.new_empty(
+        0, dtype=torch.float32)
+    return (pair.new_empty(G, P, C), d_mask, torch.empty_like(w_cat), torch.empty_like(wo), torch.empty_like(wog),
+            torch.empty_like(small))  # fmt: skip
 
 
 def _setup_context(ctx, inputs, output):
-    (pair, mask, w_cat, b_cat, wo, wog, bo, bog, in_w, in_b, on_w, on_b, blocks, direction, eps_in, eps_out) = inputs
+    pair, mask, w_cat, wo, wog, small, spans, blocks, direction, eps_in, eps_out = inputs
     _out, xn, mean_in, rstd_in, factors, combined, nrm, mean_out, rstd_out = output
-    ctx.save_for_backward(pair, mask, w_cat, b_cat, wo, wog, bo, bog, in_w, on_w, xn, mean_in, rstd_in, factors,
-                          combined, nrm, mean_out, rstd_out)  # fmt: skip
-    ctx.args = (blocks, direction, eps_in, eps_out)
-    ctx.optional = (mask is not None, b_cat is not None, bo is not None, bog is not None)
+    ctx.save_for_backward(pair, mask, w_cat, wo, wog, small, xn, mean_in, rstd_in, factors, combined, nrm,
+                          mean_out, rstd_out)  # fmt: skip
+    ctx.args = (spans, blocks, direction, eps_in, eps_out)
+    ctx.has_mask = mask is not None
     for t in output[1:]:
         ctx.mark_non_differentiable(t)
     ctx.set_materialize_grads(False)  # no zero-filled gradients for the saved intermediates
@@ -525,44 +531,42 @@ def _setup_context(ctx, inputs, output):
 
 def _backward(ctx, dout, *_unused):
     if dout is None:
-        return (None,) * 16
-    saved = ctx.saved_tensors
-    blocks, direction, eps_in, eps_out = ctx.args
+        return (None,) * 11
+    pair, mask, w_cat, wo, wog, small, *rest = ctx.saved_tensors
+    spans, blocks, direction, eps_in, eps_out = ctx.args
     need = ctx.needs_input_grad
-    grads = trimul_backward(dout, *saved, blocks, direction, eps_in, eps_out, bool(need[1]))
-    has_mask, has_bcat, has_bo, has_bog = ctx.optional
-    d_pair, d_mask, d_wcat, d_bcat, d_wo, d_wog, d_bo, d_bog, d_in_w, d_in_b, d_on_w, d_on_b = grads
-    return (
-        d_pair, d_mask if has_mask and need[1] else None, d_wcat, d_bcat if has_bcat else None, d_wo, d_wog,
-        d_bo if has_bo else None, d_bog if has_bog else None, d_in_w, d_in_b, d_on_w, d_on_b, None, None, None, None,
-    )  # fmt: skip
+    d_pair, d_mask, d_wcat, d_wo, d_wog, d_small = trimul_backward(
+        dout, pair, mask, w_cat, wo, wog, small, spans, *rest, blocks, direction, eps_in, eps_out, bool(need[1])
+    )
+    d_mask = d_mask if ctx.has_mask and need[1] else None
+    return d_pair, d_mask, d_wcat, d_wo, d_wog, d_small, None, None, None, None, None
 
 
 trimul_forward.register_autograd(_backward, setup_context=_setup_context)
 
 
 def _prepare(grouped: Tensor, mask: Optional[Tensor], weights, biases):
-    """Kernel operands from the caller's tensors, with differentiable torch ops (their autograd maps the
-    operands' gradients back): projections concatenated and zero-padded to 16-byte rows; the small float32
-    parameters (biases, LayerNorm affines) cut from one concatenated buffer, one conversion for all."""
+    """Kernel operands (pair, mask, w_cat, wo, wog, small, spans) from the caller's tensors, with
+    differentiable torch ops (their autograd maps the operands' gradients back): projections concatenated and
+    zero-padded to 16-byte rows; the small parameters (biases, LayerNorm affines) concatenated into one
+    float32 buffer, one conversion for all, located by ``spans`` (in _SMALL order)."""
 
     in_w, in_b, wlv, wlg, wrv, wrg, on_w, on_b, wo, wog = weights
     blv, blg, brv, brg, bo, bog = biases
     C, H = grouped.shape[-1], wlv.shape[0]
     cp, hp = _round8(C), _round8(H)
-    small = (("b4", (blv, blg, brv, brg), H), ("bo", (bo,), C), ("bog", (bog,), C), ("in_w", (in_w,), C),
-             ("in_b", (in_b,), C), ("on_w", (on_w,), H), ("on_b", (on_b,), H))  # fmt: skip
-    pieces, spans, off = [], {}, 0
-    for name, tensors, n in small:
+    small = (((blv, blg, brv, brg), H), ((bo,), C), ((bog,), C), ((in_w,), C), ((in_b,), C), ((on_w,), H),
+             ((on_b,), H))  # fmt: skip
+    pieces, spans, off = [], [], 0
+    for tensors, n in small:
         if all(t is None for t in tensors):
-            spans[name] = None
+            spans += [-1, -1]
             continue
         for t in tensors:
             pieces.append(torch.zeros(n, device=grouped.device) if t is None else t.resolve_neg().reshape(-1))
-        spans[name] = (off, off + n * len(tensors))
+        spans += [off, off + n * len(tensors)]
         off += n * len(tensors)
-    buf = torch.cat(pieces).float()
-    view = lambda name: None if spans[name] is None else buf[spans[name][0] : spans[name][1]]  # noqa: E731
+    buf = torch.cat(pieces).float() if pieces else torch.zeros(1, device=grouped.device)
 
     def padded(w: Tensor, width: int) -> Tensor:
         w = w.resolve_neg()
@@ -570,8 +574,7 @@ def _prepare(grouped: Tensor, mask: Optional[Tensor], weights, biases):
 
     pair = grouped.resolve_neg().contiguous()
     mask32 = None if mask is None else mask.resolve_neg().float().contiguous()
-    return (pair, mask32, padded(torch.cat([wlv, wlg, wrv, wrg]), cp), view("b4"), padded(wo, hp), padded(wog, cp),
-            view("bo"), view("bog"), view("in_w"), view("in_b"), view("on_w"), view("on_b"))  # fmt: skip
+    return pair, mask32, padded(torch.cat([wlv, wlg, wrv, wrg]), cp), padded(wo, hp), padded(wog, cp), buf, spans
 
 
 def _run(grouped: Tensor, mask: Optional[Tensor], blocks, direction, weights, biases, eps_in, eps_out) -> Tensor:
