@@ -482,7 +482,7 @@ def trimul_backward(
                                                     _ptr(mask), _ptr(d_factors), _ptr(d_proj), _ptr(mparts),
                                                     _ptr(bparts), stream),
                    "triangle_multiplication factor backward")  # fmt: skip
-        d_xn = torch.addmm(d_xn, d_proj.t(), w_cat[:, :C]).contiguous()
+        d_xn = d_xn.addmm_(d_proj.t(), w_cat[:, :C])  # in place: no copy of d_xn into a new result
         d_wcat = sums.add(_long_k_partials(d_proj, xn[:, :C]), dtype)
         if b_cat is not None:
             sums.add(bparts, out=d_views[0])
