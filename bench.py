@@ -493,12 +493,40 @@ def layer_norm_stage(device, rows=512 * 512, width=128):
     y = layer_norm(x, width, w, b)
     ms_bwd = _median_ms(lambda: torch.autograd.grad(y, [x, w, b], dy, retain_graph=True), iters=20, warmup=3)
     nbytes = rows * width * 2
+
+    # the row kernels alone through the C ABI (the operator's times above add the custom-op host path and,
+    # in the backward, the two float32 sums of the affine partials)
+    import ctypes
+    import importlib
+
+    from oops_amd import _lib
+
+    ln = importlib.import_module("oops_amd.normalization.layer_norm")
+    lib = _lib.load()
+    with torch.no_grad():
+        xd = x.detach()
+        yk, mean, rstd = (torch.empty_like(xd), torch.empty(rows, device=device), torch.empty(rows, device=device))
+        dx = torch.empty_like(xd)
+        geo = ln._geometry(xd.dtype, rows, width, width, 1e-5)
+        parts = torch.empty(2, lib.oops_layer_norm_rows_parts(ctypes.byref(geo)), width, device=device)
+        stream = torch.cuda.current_stream().cuda_stream
+        k_fwd = _median_ms(lambda: lib.oops_layer_norm_rows_forward(
+            ctypes.byref(geo), xd.data_ptr(), w.data_ptr(), b.data_ptr(), yk.data_ptr(), mean.data_ptr(),
+            rstd.data_ptr(), stream), iters=20, warmup=3)  # fmt: skip
+        k_bwd = _median_ms(lambda: lib.oops_layer_norm_rows_backward(
+            ctypes.byref(geo), xd.data_ptr(), w.data_ptr(), mean.data_ptr(), rstd.data_ptr(), dy.data_ptr(),
+            dx.data_ptr(), parts[0].data_ptr(), parts[1].data_ptr(), stream), iters=20, warmup=3)  # fmt: skip
+    kern = lambda ms_, b_: {"ms": round(ms_, 4), "achieved_gbps": round(b_ / (ms_ * 1e-3) / 1e9, 1),  # noqa: E731
+                            "frac": round(b_ / (ms_ * 1e-3) / 1e9 / 8000.0, 4)}  # fmt: skip
     return {
         "workload": f"layer_norm {rows} x {width} bf16, float32 affine",
         "ms_fwd": round(ms_fwd, 4),
         "fwd_gbps": round(2 * nbytes / (ms_fwd * 1e-3) / 1e9, 1),
         "ms_bwd": round(ms_bwd, 4),
         "bwd_gbps": round(3 * nbytes / (ms_bwd * 1e-3) / 1e9, 1),
+        # forward kernel: x read, y written (+ 2 float32 statistics per row); backward: x, dy read, dx written
+        "forward_kernel": kern(k_fwd, 2 * nbytes + 8 * rows),
+        "backward_kernel": kern(k_bwd, 3 * nbytes + 8 * rows),
         "peak_gbps": 8000.0,
     }
 
