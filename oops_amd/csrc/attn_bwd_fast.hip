@@ -309,8 +309,15 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
 // out-of-range keys (else only the unmasked tile code is compiled);
 // FULL_DBIAS: some sample has a per-group bias whose dBias = dS is written
 // here.  Both only add code that costs registers when compiled in.
+// The lean instances (D <= 32, neither of the two) start dP from a register
+// tile of -delta instead of zero (one VALU add less per score) and are built
+// for four waves per SIMD, which the extra 16 registers still fit.
+template <int DP, bool MASKED_TILES, bool FULL_DBIAS>
+constexpr bool kLeanDq = DP == 32 && !MASKED_TILES && !FULL_DBIAS;
 template <typename T, int DP, bool HAS_BIAS, bool MASKED_TILES, bool FULL_DBIAS>
-__global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT<T, T> a) {
+__global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS> ? 4 : OOPS_DQ_OCC)) void attn_dq_fast_kernel(
+    BwdArgsT<T, T> a) {
+  constexpr bool LEAN = kLeanDq<DP, MASKED_TILES, FULL_DBIAS>;
   using E = Elem<T>;
   using Frag = typename E::Frag;
   constexpr int LD = DP + 8;
@@ -556,6 +563,9 @@ __global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT
   };
 
   const float c1 = a.scale * kLog2e;
+  f32x16 nd_tile;  // LEAN: the dP accumulator's starting value
+#pragma unroll
+  for (int j = 0; j < 16; ++j) nd_tile[j] = LEAN ? ndelta : 0.0f;
   f32x16 acc[NDT];
 #pragma unroll
   for (int t = 0; t < NDT; ++t) acc[t] = f32x16{};
@@ -576,7 +586,7 @@ __global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT
       } else {
         sacc = f32x16{};
       }
-      f32x16 pacc = f32x16{};
+      f32x16 pacc = LEAN ? nd_tile : f32x16{};
 #pragma unroll
       for (int s = 0; s < NQF; ++s) {
         sacc = E::mma(lds_frag<T>(kt + (32 * t2 + lq) * LD + s * 16 + g2 * 8), qf[s], sacc);
@@ -590,7 +600,7 @@ __global__ __launch_bounds__(256, OOPS_DQ_OCC) void attn_dq_fast_kernel(BwdArgsT
           const int kk = 32 * t2 + ((j >> 2) << 3) + (j & 3);
           p = ((lb >> kk) & 1) ? p : 0.0f;
         }
-        ds[j] = p * (pacc[j] + ndelta);
+        ds[j] = LEAN ? p * pacc[j] : p * (pacc[j] + ndelta);
       }
       if (FULL_DBIAS && dbrow) {
         const int k0 = t * 64 + 32 * t2;
