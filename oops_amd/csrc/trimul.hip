@@ -1161,6 +1161,247 @@ __global__ __launch_bounds__(256) void trimul_out_norm_backward_kernel(OutNormAr
   }
 }
 
+// ------------------------------------------------------------------ output LayerNorm, wave tiles
+// trimul_out_norm_t_*: 16-bit pairs, H = 8 NI (NI = 4, 8 or 16), positions a multiple of 8.  Each wave owns
+// tiles of TP consecutive positions (64, or 32 at H = 128) of one group and all H channels, with no
+// workgroup barrier.  Lane (c = lane % CL, j = lane / CL), CL = TP / 8, holds channels h = j + JL i (JL =
+// 64 / CL) of positions 8c .. 8c + 7: 16-byte loads and stores of the channel-major tensors.  Per-position
+// sums run over the lane's channels and then over the JL lanes of one c (xor CL .. 32).  The token-major
+// rows go through a wave-private LDS tile [H][TP] whose rows are rotated by 4 (h / 8) dwords: 16-byte
+// accesses of channel rows, 2-byte column accesses of the token-major side.  Loads are unconditional
+// range-checked buffer loads (positions past P read zeros), so no load sits behind a branch.
+template <int TP>
+__device__ __forceinline__ int tile_elem(int h, int p) {  // element offset of (channel h, position p)
+  constexpr int RW = TP / 2;                              // dwords per row
+  return (h * RW + (((p >> 1) + 4 * (h >> 3)) & (RW - 1))) * 2 + (p & 1);
+}
+
+// A register value the compiler must treat as redefined at this point: what is derived from it is then not
+// hoisted out of the enclosing loop nor reused across passes (which would hold dozens of lane-dependent
+// LDS addresses, or every unpacked element, in registers for the whole loop).
+__device__ __forceinline__ int opaque(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void opaque(uint4 (&u)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(u[i].x), "+v"(u[i].y), "+v"(u[i].z), "+v"(u[i].w));
+}
+
+// Orders a channel loop: the next iteration's reads and unpacking wait for this iteration's sums (so the
+// compiler does not unpack every channel up front).
+__device__ __forceinline__ void chain(int& z, uint4& next, float s, float t) {
+  asm volatile("" : "+v"(z), "+v"(next.x), "+v"(next.y), "+v"(next.z), "+v"(next.w) : "v"(s), "v"(t));
+}
+
+template <int CL>
+__device__ __forceinline__ void reduce_same_c(float (&v)[8]) {  // sums over the lanes of one c
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+#pragma unroll
+    for (int o = CL; o < 64; o <<= 1) v[e] += __shfl_xor(v[e], o);
+}
+
+template <int NI>
+constexpr int out_norm_tp() {
+  return NI == 16 ? 32 : 64;
+}
+
+template <typename T, int NI>
+__global__ __launch_bounds__(256, 2) void trimul_out_norm_t_forward_kernel(OutNormArgs a) {
+  constexpr int H = 8 * NI, TP = out_norm_tp<NI>(), CL = TP / 8, JL = 64 / CL, NC = H / JL;
+  __shared__ __attribute__((aligned(16))) uint16_t tile_lds[4][H * TP];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane % CL, j = lane / CL;
+  uint16_t* lt = tile_lds[wave];
+  const int64_t P = a.positions, tpg = (P + TP - 1) / TP, ntiles = a.groups * tpg;
+  float w[NC], b[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    w[i] = a.w ? a.w[j + JL * i] : 1.f;
+    b[i] = a.b ? a.b[j + JL * i] : 0.f;
+  }
+  constexpr float inv_h = 1.0f / H;
+  for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < ntiles; t += (int64_t)gridDim.x * 4) {
+    const int64_t g = t / tpg, p0 = (t - g * tpg) * TP, p = p0 + 8 * c;
+    const bool pv = p < P;  // P % 8 == 0: a lane's 8 positions are wholly in or out
+    const __amdgpu_buffer_rsrc_t cr = make_rsrc(static_cast<const T*>(a.comb) + g * H * P, (uint32_t)(H * P * 2));
+    uint4 xu[NC];
+#pragma unroll
+    for (int i = 0; i < NC; ++i) xu[i] = buffer_load16(cr, pv ? (uint32_t)(((j + JL * i) * P + p) * 2) : kOut);
+    float mean[8], rstd[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mean[e] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      float x[8];
+      unpack8<T>(xu[i], x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mean[e] += x[e];
+    }
+    reduce_same_c<CL>(mean);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mean[e] *= inv_h, rstd[e] = 0.f;
+    opaque<NC>(xu);
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      float x[8];
+      unpack8<T>(xu[i], x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) rstd[e] += (x[e] - mean[e]) * (x[e] - mean[e]);
+    }
+    reduce_same_c<CL>(rstd);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) rstd[e] = rsqrtf(rstd[e] * inv_h + a.eps);
+    if (j == 0 && pv) {
+      float* mo = a.mean + g * P + p;
+      float* ro = a.rstd + g * P + p;
+      reinterpret_cast<float4*>(mo)[0] = make_float4(mean[0], mean[1], mean[2], mean[3]);
+      reinterpret_cast<float4*>(mo)[1] = make_float4(mean[4], mean[5], mean[6], mean[7]);
+      reinterpret_cast<float4*>(ro)[0] = make_float4(rstd[0], rstd[1], rstd[2], rstd[3]);
+      reinterpret_cast<float4*>(ro)[1] = make_float4(rstd[4], rstd[5], rstd[6], rstd[7]);
+    }
+    // normalized channel rows into the tile
+    opaque<NC>(xu);
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      float x[8];
+      unpack8<T>(xu[i], x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = (x[e] - mean[e]) * rstd[e] * w[i] + b[i];
+      *reinterpret_cast<uint4*>(lt + tile_elem<TP>(j + JL * i, 8 * c)) = pack8<T>(x);
+    }
+    // token-major rows out: instruction k writes position k (64 / NI) + lane / NI, channels 8 (lane % NI) ..
+    T* dst = static_cast<T*>(a.nrm) + (g * P + p0) * a.h_row;
+    const int ln = opaque(lane);
+#pragma unroll
+    for (int k = 0; k < TP * NI / 64; ++k) {
+      const int q = k * (64 / NI) + ln / NI, m = ln % NI;
+      uint32_t u[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        u[e] = (uint32_t)lt[tile_elem<TP>(8 * m + 2 * e, q)] | ((uint32_t)lt[tile_elem<TP>(8 * m + 2 * e + 1, q)] << 16);
+      if (p0 + q < P) *reinterpret_cast<uint4*>(dst + q * a.h_row + 8 * m) = make_uint4(u[0], u[1], u[2], u[3]);
+    }
+  }
+}
+
+template <typename T, int NI>
+__global__ __launch_bounds__(256, 2) void trimul_out_norm_t_backward_kernel(OutNormArgs a) {
+  constexpr int H = 8 * NI, TP = out_norm_tp<NI>(), CL = TP / 8, JL = 64 / CL, NC = H / JL;
+  __shared__ __attribute__((aligned(16))) uint16_t tile_lds[4][H * TP];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane % CL, j = lane / CL;
+  uint16_t* lt = tile_lds[wave];
+  const int64_t P = a.positions, tpg = (P + TP - 1) / TP, ntiles = a.groups * tpg;
+  float w[NC], dw[NC], db[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    w[i] = a.w ? a.w[j + JL * i] : 1.f;
+    dw[i] = 0.f, db[i] = 0.f;
+  }
+  constexpr float inv_h = 1.0f / H;
+  for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < ntiles; t += (int64_t)gridDim.x * 4) {
+    const int64_t g = t / tpg, p0 = (t - g * tpg) * TP, p = p0 + 8 * c;
+    const bool pv = p < P;
+    // the tile's grad rows [R][H] (token-major), the channel-major inputs and the statistics
+    const int np = (int)(P - p0 < TP ? P - p0 : TP);
+    const __amdgpu_buffer_rsrc_t dr =
+        make_rsrc(static_cast<const T*>(a.dn) + (g * P + p0) * H, (uint32_t)(np * H * 2));
+    uint4 du[TP * NI / 64];
+#pragma unroll
+    for (int k = 0; k < TP * NI / 64; ++k) {
+      const int q = k * (64 / NI) + lane / NI, m = lane % NI;
+      du[k] = buffer_load16(dr, (uint32_t)((q * H + 8 * m) * 2));
+    }
+    const __amdgpu_buffer_rsrc_t cr = make_rsrc(static_cast<const T*>(a.comb) + g * H * P, (uint32_t)(H * P * 2));
+    uint4 xu[NC];
+#pragma unroll
+    for (int i = 0; i < NC; ++i) xu[i] = buffer_load16(cr, pv ? (uint32_t)(((j + JL * i) * P + p) * 2) : kOut);
+    const __amdgpu_buffer_rsrc_t mr = make_rsrc(a.mean + g * P + p0, (uint32_t)(np * 4));
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.rstd + g * P + p0, (uint32_t)(np * 4));
+    float mean[8], rstd[8];
+    {
+      const uint4 m0 = buffer_load16(mr, 32 * c), m1 = buffer_load16(mr, 32 * c + 16);
+      const uint4 r0 = buffer_load16(rr, 32 * c), r1 = buffer_load16(rr, 32 * c + 16);
+      const uint32_t mv[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+      const uint32_t rv[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mean[e] = __builtin_bit_cast(float, mv[e]), rstd[e] = __builtin_bit_cast(float, rv[e]);
+    }
+    // grad rows into the tile as column writes
+    const int ln = opaque(lane);
+#pragma unroll
+    for (int k = 0; k < TP * NI / 64; ++k) {
+      const int q = k * (64 / NI) + ln / NI, m = ln % NI;
+      const uint32_t v[4] = {du[k].x, du[k].y, du[k].z, du[k].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        lt[tile_elem<TP>(8 * m + 2 * e, q)] = (uint16_t)(v[e] & 0xffffu);
+        lt[tile_elem<TP>(8 * m + 2 * e + 1, q)] = (uint16_t)(v[e] >> 16);
+      }
+    }
+    // x-hat, w dy and the two per-position means; the grad rows are read from the tile in both passes
+    float s1[8], s2[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s1[e] = 0.f, s2[e] = 0.f;
+    int z = 0;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const uint4 gu = *reinterpret_cast<const uint4*>(lt + z + tile_elem<TP>(j + JL * i, 8 * c));
+      float x[8], d[8];
+      unpack8<T>(xu[i], x);
+      unpack8<T>(gu, d);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float xh = (x[e] - mean[e]) * rstd[e], wdy = d[e] * w[i];
+        s1[e] += wdy;
+        s2[e] += wdy * xh;
+        dw[i] += d[e] * xh;
+        db[i] += d[e];
+      }
+      if (i + 1 < NC) chain(z, xu[i + 1], s2[7], dw[i]);
+    }
+    reduce_same_c<CL>(s1);
+    reduce_same_c<CL>(s2);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s1[e] *= inv_h, s2[e] *= inv_h;
+    opaque<NC>(xu);
+    z = opaque(0);  // a second read of the rows, not the first one kept
+    T* dc = static_cast<T*>(a.dcomb) + g * H * P + p;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const uint4 gu = *reinterpret_cast<const uint4*>(lt + z + tile_elem<TP>(j + JL * i, 8 * c));
+      float x[8], d[8], o[8];
+      unpack8<T>(xu[i], x);
+      unpack8<T>(gu, d);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float xh = (x[e] - mean[e]) * rstd[e];
+        o[e] = rstd[e] * (d[e] * w[i] - s1[e] - xh * s2[e]);
+      }
+      if (pv) *reinterpret_cast<uint4*>(dc + (int64_t)(j + JL * i) * P) = pack8<T>(o);
+      if (i + 1 < NC) chain(z, xu[i + 1], o[7], o[3]);
+    }
+  }
+  // affine partials of this wave: sums over the CL lanes of one j
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+#pragma unroll
+    for (int o = 1; o < CL; o <<= 1) {
+      dw[i] += __shfl_xor(dw[i], o);
+      db[i] += __shfl_xor(db[i], o);
+    }
+  }
+  if (c == 0) {
+    const int64_t part = (int64_t)blockIdx.x * 4 + wave;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      if (a.dw) a.dw[part * H + j + JL * i] = dw[i];
+      if (a.db) a.db[part * H + j + JL * i] = db[i];
+    }
+  }
+}
+
 // ------------------------------------------------------------------ gated output
 struct OutArgs {
   const void* nrm;
@@ -1552,6 +1793,9 @@ namespace {
 #ifndef OOPS_OUTNORM_NPB
 #define OOPS_OUTNORM_NPB 32
 #endif
+#ifndef OOPS_OUTNORM_T_WGS
+#define OOPS_OUTNORM_T_WGS 1024
+#endif
 // positions per output-norm workgroup: a divisor of 256 whose LDS tiles fit
 int out_norm_npb(int H, bool backward) {
   const int tiles = backward ? 2 : 1;
@@ -1559,9 +1803,22 @@ int out_norm_npb(int H, bool backward) {
   while (npb > 1 && (int64_t)tiles * H * (npb + 1) * 4 > 64 * 1024) npb /= 2;
   return npb;
 }
+
+// the wave-tile kernels: 16-bit pairs, H = 32, 64 or 128, positions a multiple of 8; workgroups of 4 waves
+int out_norm_t_ni(const oops_trimul_geometry& g) {
+  const bool ok = g.dtype != OOPS_F32 && g.positions % 8 == 0 && g.h_row == g.hidden &&
+                  (g.hidden == 32 || g.hidden == 64 || g.hidden == 128);
+  return ok ? g.hidden / 8 : 0;
+}
+int64_t out_norm_t_grid(const oops_trimul_geometry& g) {
+  const int tp = g.hidden == 128 ? 32 : 64;  // out_norm_tp
+  const int64_t tiles = g.groups * ((g.positions + tp - 1) / tp);
+  return std::min<int64_t>(OOPS_OUTNORM_T_WGS, (tiles + 3) / 4);
+}
 }  // namespace
 
 int64_t trimul_output_norm_parts(const oops_trimul_geometry& g) {
+  if (out_norm_t_ni(g)) return 4 * out_norm_t_grid(g);
   const int npb = out_norm_npb(g.hidden, true);
   return g.groups * ((g.positions + npb - 1) / npb);
 }
@@ -1569,6 +1826,21 @@ int64_t trimul_output_norm_parts(const oops_trimul_geometry& g) {
 namespace {
 hipError_t run_out_norm(const oops_trimul_geometry& g, OutNormArgs& a, bool backward, hipStream_t stream) {
   a.groups = g.groups, a.positions = g.positions, a.h_row = g.h_row, a.H = g.hidden, a.eps = g.eps;
+  if (const int ni = out_norm_t_ni(g)) {
+    const int64_t grid = out_norm_t_grid(g);
+    if (grid == 0) return hipSuccess;
+    return by_half(g.dtype, [&](auto tag) -> hipError_t {
+      using T = decltype(tag);
+      auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(256), 0, stream, a); };
+      if (backward)
+        ni == 4 ? go(trimul_out_norm_t_backward_kernel<T, 4>)
+        : ni == 8 ? go(trimul_out_norm_t_backward_kernel<T, 8>) : go(trimul_out_norm_t_backward_kernel<T, 16>);
+      else
+        ni == 4 ? go(trimul_out_norm_t_forward_kernel<T, 4>)
+        : ni == 8 ? go(trimul_out_norm_t_forward_kernel<T, 8>) : go(trimul_out_norm_t_forward_kernel<T, 16>);
+      return hipGetLastError();
+    });
+  }
   a.npb = out_norm_npb(g.hidden, backward);
   a.pblocks = (g.positions + a.npb - 1) / a.npb;
   const int64_t blocks = g.groups * a.pblocks;
