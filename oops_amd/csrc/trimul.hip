@@ -813,23 +813,32 @@ __global__ __launch_bounds__(256, BWD ? 2 : V16_FWD_OCC) void trimul_factor_v16_
     const bool blk_ok[2] = {rw < R, rw + 16 < R};  // R % 16 == 0: a block is wholly in or out
     // element offsets of block h's first token in the [f][G][H][P] factor layout, channel 0
     const int64_t fbase[2] = {(fG + gb[0]) * H * P + pb[0], (fG + gb[1]) * H * P + pb[1]};
+    const bool st_ok = g2 ? blk_ok[1] : blk_ok[0];  // this lane's 16 post-trade tokens exist
+    // every load is unconditional (an absent block reads a valid address and is replaced afterwards), so
+    // no load sits behind a branch that waits for it
     float keep[4][4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       float4 k4 = make_float4(1.f, 1.f, 1.f, 1.f);
-      if (MASKED && blk_ok[q >> 1]) k4 = *reinterpret_cast<const float4*>(mask + rw + 8 * q + 4 * g2);
+      if constexpr (MASKED) {
+        const float4 m4 = *reinterpret_cast<const float4*>(mask + (blk_ok[q >> 1] ? rw + 8 * q + 4 * g2 : 0));
+        if (blk_ok[q >> 1]) k4 = m4;
+      }
       keep[q][0] = k4.x, keep[q][1] = k4.y, keep[q][2] = k4.z, keep[q][3] = k4.w;
     }
-    uint2 dpre[2][4];
+    // BWD: the factor gradients of the lane's 16 post-trade tokens (2 x 16 bytes per channel tile),
+    // traded back to the accumulator layout in the epilogue
+    uint4 dlo[2], dhi[2];
     if constexpr (BWD) {
       const T* gf = static_cast<const T*>(a.grad_factors);
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          dpre[t][q] = hv_ok[t] && blk_ok[q >> 1]
-                           ? *reinterpret_cast<const uint2*>(gf + fbase[q >> 1] + (int64_t)hv[t] * P + 8 * (q & 1) + 4 * g2)
-                           : make_uint2(0, 0);
+      for (int t = 0; t < 2; ++t) {
+        const bool ok = hv_ok[t] && st_ok;
+        const T* src = gf + (ok ? (g2 ? fbase[1] : fbase[0]) + (int64_t)hv[t] * P : 0);
+        dlo[t] = *reinterpret_cast<const uint4*>(src);
+        dhi[t] = *reinterpret_cast<const uint4*>(src + 8);
+        if (!ok) dlo[t] = dhi[t] = make_uint4(0, 0, 0, 0);
+      }
     }
 
     // the first panel starts from zero accumulators (no register clear)
@@ -862,10 +871,18 @@ __global__ __launch_bounds__(256, BWD ? 2 : V16_FWD_OCC) void trimul_factor_v16_
 #pragma unroll
     for (int v = 0; v < 16; ++v) mp[v] = 0.f;
     const int64_t r16 = rw + 16 * g2;
-    const bool st_ok = g2 ? blk_ok[1] : blk_ok[0];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      uint32_t po[8], pg[8];
+      uint32_t po[8], pg[8], pd[8];
+      if constexpr (BWD) {
+        // inverse of trade16: pd[2q], pd[2q + 1] hold tokens 8q + 4 g2 + (0, 1), (2, 3)
+        const auto y0 = __builtin_amdgcn_permlane32_swap(dlo[t].x, dlo[t].z, false, false);
+        const auto y1 = __builtin_amdgcn_permlane32_swap(dlo[t].y, dlo[t].w, false, false);
+        const auto y2 = __builtin_amdgcn_permlane32_swap(dhi[t].x, dhi[t].z, false, false);
+        const auto y3 = __builtin_amdgcn_permlane32_swap(dhi[t].y, dhi[t].w, false, false);
+        pd[0] = y0[0], pd[1] = y1[0], pd[2] = y2[0], pd[3] = y3[0];
+        pd[4] = y0[1], pd[5] = y1[1], pd[6] = y2[1], pd[7] = y3[1];
+      }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         float o[4], og[4];
@@ -876,7 +893,7 @@ __global__ __launch_bounds__(256, BWD ? 2 : V16_FWD_OCC) void trimul_factor_v16_
           if constexpr (!BWD) {
             o[i] = v * s * keep[q][i];
           } else {
-            const uint32_t u = i < 2 ? dpre[t][q].x : dpre[t][q].y;
+            const uint32_t u = pd[2 * q + (i >> 1)];
             const float d = (i & 1) ? hi_f<T>(u) : lo_f<T>(u);
             const float dk = d * keep[q][i], vs = v * s;
             mp[4 * q + i] += d * vs;
