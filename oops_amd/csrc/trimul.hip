@@ -113,10 +113,11 @@ __device__ __forceinline__ void load_chunks(const T* row, bool valid, int width,
   for (int c = 0; c < CH; ++c) {
     const int col = (c * lpr + sub) * 8;
     if constexpr (VEC) {
-      // width % 8 == 0: a chunk is wholly inside or outside the row
-      if (valid && col < width) {
-        load8<T>(row + col, x[c]);
-      } else {
+      // width % 8 == 0: a chunk is wholly inside or outside the row.  The load is unconditional (an absent
+      // chunk reads the row's first one and is replaced), so it does not sit behind a branch that waits
+      const bool in = valid && col < width;
+      load8<T>(row + (in ? col : 0), x[c]);
+      if (!in) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[c][e] = 0.f;
       }
