@@ -1459,6 +1459,32 @@ __global__ __launch_bounds__(256) void trimul_output_kernel(OutArgs a) {
   const int nrows = (int)(rows_left < kOM ? rows_left : kOM);
   const bool rv = wave * 32 + lq < nrows;
   const int wrows = C - c0 < kON ? C - c0 : kON;
+  // the block's output bias and -log2(e) x gate bias, read by the epilogue as float4 (visible after the
+  // first W tile's barrier)
+  __shared__ __attribute__((aligned(16))) float b_lds[2][kON];
+  if (tid < 2 * kON) {
+    const int ph = tid / kON, ch = c0 + tid % kON;
+    const float* bsrc = ph == 0 ? a.bo : a.bg;
+    const float bv = bsrc != nullptr && ch < C ? bsrc[ch] : 0.f;
+    b_lds[ph][tid % kON] = ph == 0 ? bv : -bv * kLog2e;
+  }
+  const int64_t r = r0 + wave * 32 + lq;
+  // BWD: grad_out for the lane's 16 post-swap channels n .. n + 15 of each tile t, loaded before the
+  // projections (unconditionally: an absent chunk reads the row's first one and is replaced)
+  uint4 gin[2][2] = {};
+  if (BWD && (C & 7) == 0) {  // 16-byte rows (the element-wise path below reads its own)
+    const T* grow = static_cast<const T*>(a.gout) + (rv ? r : r0) * C;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int n = c0 + 32 * t + 16 * g2;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const bool in = rv && n + 8 * hh < C;
+        gin[t][hh] = *reinterpret_cast<const uint4*>(grow + (in ? n + 8 * hh : 0));
+        if (!in) gin[t][hh] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
 
   f32x16 acc[4];
 #pragma unroll
@@ -1528,21 +1554,23 @@ __global__ __launch_bounds__(256) void trimul_output_kernel(OutArgs a) {
 
   // ---- epilogue: lane (lq, g2) of tile t holds channels c0 + 32t + 8q + 4g2 + i of token r
   if (!rv) return;
-  const int64_t r = r0 + wave * 32 + lq;
   const bool vecc = (C & 7) == 0;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int n = c0 + 32 * t + 16 * g2;  // first of this lane's 16 channels after the swap
     float v[16], s[16];
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int q = 0; q < 4; ++q) {
+      const float4 bo4 = *reinterpret_cast<const float4*>(&b_lds[0][32 * t + 8 * q + 4 * g2]);
+      const float4 bg4 = *reinterpret_cast<const float4*>(&b_lds[1][32 * t + 8 * q + 4 * g2]);
+      const float bo[4] = {bo4.x, bo4.y, bo4.z, bo4.w}, bgl[4] = {bg4.x, bg4.y, bg4.z, bg4.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int ch = c0 + 32 * t + 8 * q + 4 * g2 + i;
-        const bool in = ch < C;
-        v[4 * q + i] = acc[t][4 * q + i] + (in && a.bo ? a.bo[ch] : 0.f);
-        s[4 * q + i] = sigmoid_f(acc[2 + t][4 * q + i] + (in && a.bg ? a.bg[ch] : 0.f));
+        v[4 * q + i] = acc[t][4 * q + i] + bo[i];
+        s[4 * q + i] = __builtin_amdgcn_rcpf(
+            1.0f + __builtin_amdgcn_exp2f(__builtin_fmaf(acc[2 + t][4 * q + i], -kLog2e, bgl[i])));
       }
+    }
     if constexpr (!BWD) {
       uint32_t p[8];
 #pragma unroll
@@ -1574,8 +1602,8 @@ __global__ __launch_bounds__(256) void trimul_output_kernel(OutArgs a) {
       const T* grow = static_cast<const T*>(a.gout) + r * C;
       uint4 lo, hi;
       if (vecc) {
-        lo = n < C ? *reinterpret_cast<const uint4*>(grow + n) : make_uint4(0, 0, 0, 0);
-        hi = n + 8 < C ? *reinterpret_cast<const uint4*>(grow + n + 8) : make_uint4(0, 0, 0, 0);
+        lo = gin[t][0];
+        hi = gin[t][1];
       } else {
         float e[8];
         for (int j = 0; j < 8; ++j) e[j] = n + j < C ? to_f(grow[n + j]) : 0.f;
