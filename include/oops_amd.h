@@ -330,6 +330,21 @@ size_t oops_sum_partials_workspace_bytes(const oops_sum_segment* segments, int32
 int oops_sum_partials(const oops_sum_segment* segments, int32_t num_segments, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/* The products of the gated output's backward that share one operand X [R][128] (16-bit, C = H = 128):
+ *   d = X W              W [128][128] (rows w_row apart) -> d [R][128] (rows d_row apart), the dtype
+ *   g_parts: X^T Y       Y [R][128] (rows y_row apart)   -> float32 partials [parts][128][128]
+ *   s_parts: column sums of X                            -> float32 partials [parts][128]
+ * with parts = oops_trimul_output_grad_parts (0: the geometry is not served; use GEMMs).  With X = the
+ * value gradient, W = W_out, Y = the normalized combined rows these are the normalized-rows gradient,
+ * W_out's gradient and the output bias gradient; with X = the gate-logit gradient, W = W_gate, Y = xn the
+ * pair-rows gradient through the gate, W_gate's gradient and the gate bias gradient.  They replace the
+ * reference's bmm / matmul / _column_sums calls of the output backward
+ * (triangle_multiplication/triton/generic.py:820-824, :842-856) and its fused LayerNorm input product. */
+size_t oops_trimul_output_grad_parts(const oops_trimul_geometry* geo);
+int oops_trimul_output_grad_products(const oops_trimul_geometry* geo, const void* x, int64_t x_row, const void* w,
+                                     int64_t w_row, const void* y, int64_t y_row, void* d, int64_t d_row,
+                                     float* g_parts, float* s_parts, void* stream);
+
 /* Thread-local description of the last failure (empty string if none). */
 const char* oops_last_error(void);
 

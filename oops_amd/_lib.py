@@ -57,6 +57,8 @@ EXPORTED_SYMBOLS = (
     "oops_trimul_output_norm_backward",
     "oops_trimul_output_forward",
     "oops_trimul_output_backward",
+    "oops_trimul_output_grad_parts",
+    "oops_trimul_output_grad_products",
     "oops_sum_partials_workspace_bytes",
     "oops_sum_partials",
     "oops_last_error",
@@ -208,6 +210,11 @@ def load() -> ctypes.CDLL:
         lib.oops_trimul_output_forward.restype = i32
         lib.oops_trimul_output_backward.argtypes = [tg, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
         lib.oops_trimul_output_backward.restype = i32
+        i64 = ctypes.c_int64
+        lib.oops_trimul_output_grad_parts.argtypes = [tg]
+        lib.oops_trimul_output_grad_parts.restype = sz
+        lib.oops_trimul_output_grad_products.argtypes = [tg, vp, i64, vp, i64, vp, i64, vp, i64, vp, vp, vp]
+        lib.oops_trimul_output_grad_products.restype = i32
         lib.oops_sum_partials_workspace_bytes.argtypes = [ctypes.POINTER(SumSegment), ctypes.c_int32]
         lib.oops_sum_partials_workspace_bytes.restype = sz
         lib.oops_sum_partials.argtypes = [ctypes.POINTER(SumSegment), ctypes.c_int32, vp, sz, vp]

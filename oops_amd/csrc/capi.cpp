@@ -608,6 +608,29 @@ int oops_trimul_output_backward(const oops_trimul_geometry* geo, const void* nor
                             "triangle multiplication output backward");
 }
 
+size_t oops_trimul_output_grad_parts(const oops_trimul_geometry* geo) {
+  g_last_error.clear();
+  if (check_trimul(geo)) return 0;
+  return (size_t)oops::trimul_output_grad_parts(*geo);
+}
+
+int oops_trimul_output_grad_products(const oops_trimul_geometry* geo, const void* x, int64_t x_row, const void* w,
+                                     int64_t w_row, const void* y, int64_t y_row, void* d, int64_t d_row,
+                                     float* g_parts, float* s_parts, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_trimul(geo)) return rc;
+  if (!oops::trimul_output_grad_supported(*geo))
+    return fail(OOPS_EINVAL, "the output-gradient products serve 16-bit pairs with C = H = 128");
+  if (!x || !w || !y || !d || !g_parts || !s_parts) return fail(OOPS_EINVAL, "operands must be non-NULL");
+  if (x_row < 128 || w_row < 128 || y_row < 128 || d_row < 128 || x_row % 8 || w_row % 8 || y_row % 8 || d_row % 8)
+    return fail(OOPS_EINVAL, "row strides must be multiples of 8 of at least 128 elements");
+  if (!aligned16(x) || !aligned16(w) || !aligned16(y) || !aligned16(d))
+    return fail(OOPS_EINVAL, "operands must be 16-byte aligned");
+  return gate_launch_result(oops::launch_trimul_output_grad(*geo, x, x_row, w, w_row, y, y_row, d, d_row, g_parts,
+                                                            s_parts, static_cast<hipStream_t>(stream)),
+                            "triangle multiplication output-gradient products");
+}
+
 namespace {
 int check_sum_segments(const oops_sum_segment* segments, int32_t num_segments) {
   if (num_segments < 0 || num_segments > OOPS_SUM_MAX_SEGMENTS)

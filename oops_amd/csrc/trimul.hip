@@ -1648,6 +1648,180 @@ __global__ __launch_bounds__(256) void trimul_output_kernel(OutArgs a) {
   }
 }
 
+// ------------------------------------------------------------------ output-projection gradients
+// trimul_output_grad_kernel: for C = H = 128 and 16-bit rows, the products of the gated output's backward
+// that share one operand X [R][128]:
+//   D = X W          W [128][128]: d_normalized = grad_value W_out, d_pair = grad_gate W_gate
+//   G = sum_r X^T Y  Y [R][128]:   d_W_out = grad_value^T normalized, d_W_gate = grad_gate^T xn
+//   S = sum_r X      the output and gate bias gradients
+// One workgroup = 8 waves walking TPW tiles of 128 rows; the X and Y tiles sit in LDS as 64-element row
+// halves with XOR-swizzled 16-byte chunks, the next tile's rows in registers meanwhile.  Waves 0-3 compute
+// D: wave w holds the W^T fragments of columns 32w .. 32w + 31 in registers (staged through LDS once) and
+// produces those columns for the tile's rows, the row being the MFMA column, so after the half-wave trade
+// each lane stores 32 bytes of one D row.  Waves 4-7 accumulate G and S: wave 4 + v rows 32v .. 32v + 31 of
+// G (X columns) over all of the workgroup's tiles, X^T and Y read with the LDS transpose read (within a
+// 16-row slab the row order of the sum is that read's, the same for both operands), S as one more MFMA
+// against an all-ones operand.  Per-workgroup partials of G and S, summed by oops_sum_partials.
+constexpr int kGT = 128;  // rows per tile
+constexpr int kGN = 128;  // width of X, W, Y and D
+
+struct GradArgs {
+  const void* x;
+  const void* w;
+  const void* y;
+  void* d;
+  float* g_parts;
+  float* s_parts;
+  int64_t rows, x_row, w_row, y_row, d_row;
+  int tpw;
+};
+
+// element offset of (row r, column c) in a tile of `rows` rows stored as two 64-element halves
+__device__ __forceinline__ int half_off(int rows, int r, int c) { return (c >> 6) * rows * 64 + swz_off<64>(r, c & 63); }
+
+template <typename T>
+__global__ __launch_bounds__(512, 2) void trimul_output_grad_kernel(GradArgs a) {
+  using E = Elem<T>;
+  using Frag = typename E::Frag;
+  __shared__ __attribute__((aligned(16))) T x_lds[kGT * kGN];  // X tile [r][c] (first: W^T [n][c])
+  __shared__ __attribute__((aligned(16))) T y_lds[kGT * kGN];  // Y tile [r][n]
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, lq = lane & 31, g2 = lane >> 5;
+  const int64_t R = a.rows;
+  const int64_t tile0 = (int64_t)blockIdx.x * a.tpw;
+
+  // W^T through x_lds: each thread reads 16-byte chunks of W rows and writes their elements transposed
+  {
+    const T* w = static_cast<const T*>(a.w);
+    uint16_t* wt16 = reinterpret_cast<uint16_t*>(x_lds);
+#pragma unroll
+    for (int it = 0; it < kGN * kGN / 8 / 512; ++it) {
+      const int id = tid + 512 * it, c = id >> 4, n0 = (id & 15) * 8;
+      const uint4 u = *reinterpret_cast<const uint4*>(w + (int64_t)c * a.w_row + n0);
+      const uint32_t v[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        wt16[half_off(kGN, n0 + 2 * e, c)] = (uint16_t)(v[e] & 0xffffu);
+        wt16[half_off(kGN, n0 + 2 * e + 1, c)] = (uint16_t)(v[e] >> 16);
+      }
+    }
+  }
+  // a tile's X and Y rows: 128 rows x 16 chunks each, 4 chunks per thread (rows past R read zeros)
+  auto load_tile = [&](int64_t t, uint4 (&xr)[4], uint4 (&yr)[4]) {
+    const int64_t r0 = t * kGT;
+    const int64_t left = R - r0;
+    const int nrows = (int)(left < 0 ? 0 : left < kGT ? left : kGT);
+    const __amdgpu_buffer_rsrc_t xs =
+        make_rsrc(static_cast<const T*>(a.x) + (nrows ? r0 : 0) * a.x_row, (uint32_t)(nrows * a.x_row * 2));
+    const __amdgpu_buffer_rsrc_t ys =
+        make_rsrc(static_cast<const T*>(a.y) + (nrows ? r0 : 0) * a.y_row, (uint32_t)(nrows * a.y_row * 2));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int id = tid + 512 * k, r = id >> 4, ch = (id & 15) * 8;
+      xr[k] = buffer_load16(xs, r < nrows ? (uint32_t)((r * a.x_row + ch) * 2) : kOut);
+      yr[k] = buffer_load16(ys, r < nrows ? (uint32_t)((r * a.y_row + ch) * 2) : kOut);
+    }
+  };
+  // barrier, the prefetched rows into the tiles, the next tile's loads, barrier; false past the rows
+  uint4 xr[4], yr[4];
+  auto stage = [&](int it) {
+    const int64_t r0 = (tile0 + it) * kGT;
+    if (r0 >= R) return false;
+    __syncthreads();  // the previous tile's reads are done
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int id = tid + 512 * k, r = id >> 4, ch = (id & 15) * 8;
+      *reinterpret_cast<uint4*>(&x_lds[half_off(kGT, r, ch)]) = xr[k];
+      *reinterpret_cast<uint4*>(&y_lds[half_off(kGT, r, ch)]) = yr[k];
+    }
+    if (it + 1 < a.tpw) load_tile(tile0 + it + 1, xr, yr);  // in flight during this tile
+    __syncthreads();
+    return true;
+  };
+
+  if (wave < 4) {
+    // ---- D: this wave's W^T fragments (columns 32 wave + lq, k = 16 ks + 8 g2 ..), then per tile the
+    // columns 32 wave + 8q + 4 g2 + i of rows r0 + 32 tt + lq
+    Frag wf[kGN / 16];
+    __syncthreads();  // W^T written
+#pragma unroll
+    for (int ks = 0; ks < kGN / 16; ++ks) wf[ks] = lds_frag<T>(&x_lds[half_off(kGN, 32 * wave + lq, 16 * ks + 8 * g2)]);
+    load_tile(tile0, xr, yr);
+    for (int it = 0; it < a.tpw; ++it) {
+      if (!stage(it)) break;
+      const int64_t r0 = (tile0 + it) * kGT;
+      f32x16 dacc[kGT / 32];
+#pragma unroll
+      for (int tt = 0; tt < kGT / 32; ++tt) dacc[tt] = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < kGN / 16; ++ks)
+#pragma unroll
+        for (int tt = 0; tt < kGT / 32; ++tt)
+          dacc[tt] = E::mma(wf[ks], lds_frag<T>(&x_lds[half_off(kGT, 32 * tt + lq, 16 * ks + 8 * g2)]), dacc[tt]);
+#pragma unroll
+      for (int tt = 0; tt < kGT / 32; ++tt) {
+        uint32_t p[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          p[2 * q] = pack2<T>(dacc[tt][4 * q], dacc[tt][4 * q + 1]);
+          p[2 * q + 1] = pack2<T>(dacc[tt][4 * q + 2], dacc[tt][4 * q + 3]);
+        }
+        uint4 lo, hi;
+        trade16(p, lo, hi);  // columns 32 wave + 16 g2 .. + 15
+        const int64_t row = r0 + 32 * tt + lq;
+        if (row < R) {
+          T* dst = static_cast<T*>(a.d) + row * a.d_row + 32 * wave + 16 * g2;
+          *reinterpret_cast<uint4*>(dst) = lo;
+          *reinterpret_cast<uint4*>(dst + 8) = hi;
+        }
+      }
+    }
+  } else {
+    // ---- G and S: rows 32 v .. + 31 (X columns), over each tile's rows in slabs of 16
+    const int v = wave - 4;
+    Frag ones;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ones[e] = (T)1.0f;
+    f32x16 gacc[kGN / 32], sacc = f32x16{};
+#pragma unroll
+    for (int nb = 0; nb < kGN / 32; ++nb) gacc[nb] = f32x16{};
+    __syncthreads();  // W^T written (the D waves read it before the first tile overwrites it)
+    load_tile(tile0, xr, yr);
+    const TrLane tx = tr_lane<64>(lane, (32 * v) & 63);
+    const T* xa = x_lds + ((32 * v) >> 6) * kGT * 64 + ((32 * v) & 63);
+    for (int it = 0; it < a.tpw; ++it) {
+      if (!stage(it)) break;
+#pragma unroll
+      for (int ks = 0; ks < kGT / 16; ++ks) {
+        const Frag af = lds_read_tr_frag_sw<T>(xa + 16 * ks * 64, tx);
+#pragma unroll
+        for (int nb = 0; nb < kGN / 32; ++nb) {
+          const TrLane ty = tr_lane<64>(lane, (32 * nb) & 63);
+          const Frag bf = lds_read_tr_frag_sw<T>(y_lds + ((32 * nb) >> 6) * kGT * 64 + 16 * ks * 64 + ((32 * nb) & 63), ty);
+          gacc[nb] = E::mma(af, bf, gacc[nb]);
+        }
+        sacc = E::mma(af, ones, sacc);
+      }
+    }
+    // partials: gacc[nb] lane (lq, g2) holds G[32 v + 8q + 4 g2 + i][32 nb + lq]; every column of sacc holds
+    // S[32 v + 8q + 4 g2 + i]
+    float* gp = a.g_parts + (int64_t)blockIdx.x * kGN * kGN;
+#pragma unroll
+    for (int nb = 0; nb < kGN / 32; ++nb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) gp[(32 * v + 8 * q + 4 * g2 + i) * kGN + 32 * nb + lq] = gacc[nb][4 * q + i];
+    if (lq == 0) {
+      float* sp = a.s_parts + (int64_t)blockIdx.x * kGN;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sp[32 * v + 8 * q + 4 * g2 + i] = sacc[4 * q + i];
+    }
+  }
+}
+
 template <typename F>
 hipError_t by_half(int dtype, F&& f) {
   if (dtype == OOPS_BF16) return f(__bf16{});
@@ -1952,6 +2126,48 @@ hipError_t launch_trimul_output(const oops_trimul_geometry& g, const void* norma
       hipLaunchKernelGGL((trimul_output_kernel<T, true>), grid, dim3(256), 0, stream, a);
     else
       hipLaunchKernelGGL((trimul_output_kernel<T, false>), grid, dim3(256), 0, stream, a);
+    return hipGetLastError();
+  });
+}
+
+
+namespace {
+#ifndef OOPS_OUTGRAD_WGS
+#define OOPS_OUTGRAD_WGS 256
+#endif
+struct GradPlan {
+  int tpw;
+  int64_t grid;
+};
+GradPlan grad_plan(const oops_trimul_geometry& g) {
+  const int64_t tiles = (g.groups * g.positions + kGT - 1) / kGT;
+  GradPlan pl{};
+  pl.tpw = (int)std::max<int64_t>(1, (tiles + OOPS_OUTGRAD_WGS - 1) / OOPS_OUTGRAD_WGS);
+  pl.grid = (tiles + pl.tpw - 1) / pl.tpw;
+  return pl;
+}
+}  // namespace
+
+bool trimul_output_grad_supported(const oops_trimul_geometry& g) {
+  return g.dtype != OOPS_F32 && g.channels == kGN && g.hidden == kGN;
+}
+
+int64_t trimul_output_grad_parts(const oops_trimul_geometry& g) {
+  return trimul_output_grad_supported(g) ? grad_plan(g).grid : 0;
+}
+
+hipError_t launch_trimul_output_grad(const oops_trimul_geometry& g, const void* x, int64_t x_row, const void* w,
+                                     int64_t w_row, const void* y, int64_t y_row, void* d, int64_t d_row,
+                                     float* g_parts, float* s_parts, hipStream_t stream) {
+  const GradPlan pl = grad_plan(g);
+  if (pl.grid == 0) return hipSuccess;
+  GradArgs a{};
+  a.x = x, a.w = w, a.y = y, a.d = d, a.g_parts = g_parts, a.s_parts = s_parts;
+  a.rows = g.groups * g.positions, a.x_row = x_row, a.w_row = w_row, a.y_row = y_row, a.d_row = d_row;
+  a.tpw = pl.tpw;
+  return by_half(g.dtype, [&](auto tag) -> hipError_t {
+    using T = decltype(tag);
+    hipLaunchKernelGGL((trimul_output_grad_kernel<T>), dim3((unsigned)pl.grid), dim3(512), 0, stream, a);
     return hipGetLastError();
   });
 }

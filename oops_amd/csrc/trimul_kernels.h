@@ -35,6 +35,13 @@ hipError_t launch_trimul_output(const oops_trimul_geometry& g, const void* norma
                                 const float* gate_bias, void* out, const void* grad_out, void* grad_value,
                                 void* grad_gate, hipStream_t stream);
 
+// the output projection's gradient products for C = H = 128, 16-bit (oops_trimul_output_grad_products)
+bool trimul_output_grad_supported(const oops_trimul_geometry& g);
+int64_t trimul_output_grad_parts(const oops_trimul_geometry& g);
+hipError_t launch_trimul_output_grad(const oops_trimul_geometry& g, const void* x, int64_t x_row, const void* w,
+                                     int64_t w_row, const void* y, int64_t y_row, void* d, int64_t d_row,
+                                     float* g_parts, float* s_parts, hipStream_t stream);
+
 // float32 pairs (trimul_f32.hip): the same contracts on the exact float32 matrix core
 hipError_t launch_trimul_factors_f32(const oops_trimul_geometry& g, const void* normalized, const void* weight,
                                      const float* bias, const void* mask, void* factors, const void* grad_factors,

@@ -453,16 +453,34 @@ def trimul_backward(
                                                    stream),
                    "triangle_multiplication output backward")  # fmt: skip
         gv, gg = g_val[:, :C], g_gate[:, :C]
-        d_nrm = gv.mm(wo[:, :H]).contiguous()  # (R, H)
-        d_xn = gg.mm(wog[:, :C])  # (R, C)
         # every float32 partial (K-chunk products, per-workgroup sums) is summed by one launch at the end
         sums = PartialSums()
-        d_wo = sums.add(_long_k_partials(gv.t(), nrm[:, :H]), dtype)
-        d_wog = sums.add(_long_k_partials(gg.t(), xn[:, :C]), dtype)
-        if bo is not None:
-            sums.add(_column_partials(gv), out=d_views[1])
-        if bog is not None:
-            sums.add(_column_partials(gg), out=d_views[2])
+        parts = lib.oops_trimul_output_grad_parts(ctypes.byref(geo))
+        if parts:
+            # C = H = 128: one pass over each gradient gives its GEMM with the weight, its weight-gradient
+            # and bias-gradient partials (oops_trimul_output_grad_products)
+            d_nrm = torch.empty(R, H, dtype=dtype, device=dev)
+            d_xn = torch.empty(R, C, dtype=dtype, device=dev)
+            g_parts = torch.empty(2, parts, C, C, dtype=torch.float32, device=dev)
+            s_parts = torch.empty(2, parts, C, dtype=torch.float32, device=dev)
+            for i, (x, w, y, d) in enumerate(((g_val, wo, nrm, d_nrm), (g_gate, wog, xn, d_xn))):
+                _lib.check(lib.oops_trimul_output_grad_products(
+                    ctypes.byref(geo), _ptr(x), x.stride(0), _ptr(w), w.stride(0), _ptr(y), y.stride(0), _ptr(d),
+                    d.stride(0), _ptr(g_parts[i]), _ptr(s_parts[i]), stream), "triangle_multiplication output gradients")  # fmt: skip
+            d_wo, d_wog = sums.add(g_parts[0], dtype), sums.add(g_parts[1], dtype)
+            if bo is not None:
+                sums.add(s_parts[0], out=d_views[1])
+            if bog is not None:
+                sums.add(s_parts[1], out=d_views[2])
+        else:
+            d_nrm = gv.mm(wo[:, :H]).contiguous()  # (R, H)
+            d_xn = gg.mm(wog[:, :C])  # (R, C)
+            d_wo = sums.add(_long_k_partials(gv.t(), nrm[:, :H]), dtype)
+            d_wog = sums.add(_long_k_partials(gg.t(), xn[:, :C]), dtype)
+            if bo is not None:
+                sums.add(_column_partials(gv), out=d_views[1])
+            if bog is not None:
+                sums.add(_column_partials(gg), out=d_views[2])
 
         d_comb = torch.empty(G, H, P, dtype=dtype, device=dev)
         on_parts = torch.empty(2, lib.oops_trimul_output_norm_parts(ctypes.byref(geo)), H, dtype=torch.float32,

@@ -239,3 +239,29 @@ def test_sum_partials_validates_on_the_host(lib):
     assert lib.oops_sum_partials_workspace_bytes(segs, 1) == 256
     assert lib.oops_sum_partials(segs, 1, None, 0, None) != 0
     assert b"workspace" in lib.oops_last_error()
+
+
+def test_trimul_output_grad_validation(lib):
+    """The output-gradient products serve 16-bit pairs with C = H = 128 only and check strides on the host."""
+
+    tg = _lib.TrimulGeometry()
+    tg.dtype, tg.channels, tg.hidden, tg.has_mask = _lib.BF16, 128, 128, 0
+    tg.groups, tg.positions, tg.c_row, tg.h_row, tg.eps = 2, 300, 128, 128, 1e-5
+    assert lib.oops_trimul_output_grad_parts(ctypes.byref(tg)) >= 1
+    fake = ctypes.c_void_p(256)
+    args = [fake, 128, fake, 128, fake, 128, fake, 128, fake, fake, None]
+    bad = list(args)
+    bad[1] = 100  # row stride below 128
+    assert lib.oops_trimul_output_grad_products(ctypes.byref(tg), *bad) != 0
+    assert b"stride" in lib.oops_last_error()
+    bad = list(args)
+    bad[4] = ctypes.c_void_p(258)  # misaligned operand
+    assert lib.oops_trimul_output_grad_products(ctypes.byref(tg), *bad) != 0
+    assert b"aligned" in lib.oops_last_error()
+    bad = list(args)
+    bad[8] = None
+    assert lib.oops_trimul_output_grad_products(ctypes.byref(tg), *bad) != 0
+    for dtype, c, h in ((_lib.F32, 128, 128), (_lib.BF16, 64, 128), (_lib.F16, 128, 96)):
+        tg.dtype, tg.channels, tg.hidden = dtype, c, h
+        assert lib.oops_trimul_output_grad_parts(ctypes.byref(tg)) == 0
+        assert lib.oops_trimul_output_grad_products(ctypes.byref(tg), *args) != 0

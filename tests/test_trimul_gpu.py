@@ -254,3 +254,46 @@ def test_trimul_compile_matches_eager():
         results.append((out.detach(), *torch.autograd.grad(out, [p, weights[2], bs[0]], dy)))
     for got, ref in zip(*results):
         torch.testing.assert_close(got, ref, atol=0, rtol=0)
+
+
+@pytest.mark.parametrize("dtype,groups,positions", [(torch.float16, 3, 173), (torch.bfloat16, 1, 128), (torch.bfloat16, 7, 4097)])
+def test_trimul_output_grad_products(dtype, groups, positions):
+    """oops_trimul_output_grad_products through the C-ABI against float64 products of the same 16-bit inputs:
+    D = X W rounded once to 16 bits, the per-workgroup partials of X^T Y and of X's column sums summed in
+    float64.  Ragged row counts (not a multiple of the 128-row tile) and padded row strides."""
+
+    import ctypes
+
+    from oops_amd import _lib
+
+    lib = _lib.load()
+    R, C = groups * positions, 128
+    g = torch.Generator().manual_seed(positions)
+    x = torch.randn(R, C + 8, generator=g).to(dtype).to(DEV)[:, :C]
+    y = torch.randn(R, C + 16, generator=g).to(dtype).to(DEV)[:, 8:8 + C]
+    w = (torch.randn(C, C, generator=g) * C**-0.5).to(dtype).to(DEV)
+    d = torch.full((R, C + 8), 7.0, dtype=dtype, device=DEV)
+    geo = _lib.TrimulGeometry()
+    geo.dtype = _lib.BF16 if dtype == torch.bfloat16 else _lib.F16
+    geo.channels, geo.hidden, geo.has_mask = C, C, 0
+    geo.groups, geo.positions, geo.c_row, geo.h_row, geo.eps = groups, positions, C, C, 1e-5
+    parts = lib.oops_trimul_output_grad_parts(ctypes.byref(geo))
+    assert parts >= 1
+    gp = torch.full((parts, C, C), float("nan"), device=DEV)
+    sp = torch.full((parts, C), float("nan"), device=DEV)
+    rc = lib.oops_trimul_output_grad_products(ctypes.byref(geo), x.data_ptr(), x.stride(0), w.data_ptr(), C,
+                                              y.data_ptr(), y.stride(0), d.data_ptr(), d.stride(0), gp.data_ptr(),
+                                              sp.data_ptr(), torch.cuda.current_stream().cuda_stream)  # fmt: skip
+    assert rc == 0, lib.oops_last_error()
+    torch.cuda.synchronize()
+    xd, yd, wd = x.double().cpu(), y.double().cpu(), w.double().cpu()
+    want_d = (xd @ wd).to(dtype).double()
+    got_d = d[:, :C].double().cpu()
+    # one rounding of a float32 accumulation: within an ulp of the 16-bit result
+    ulp = 2.0 ** (-7 if dtype == torch.bfloat16 else -10)
+    assert ((got_d - want_d).abs() <= ulp * want_d.abs().clamp_min(2.0**-6) + 1e-6).all()
+    assert (d[:, C:] == 7.0).all()  # the padding past each row stays untouched
+    got_g, got_s = gp.double().sum(0).cpu(), sp.double().sum(0).cpu()
+    want_g, want_s = xd.t() @ yd, xd.sum(0)
+    assert (got_g - want_g).abs().max().item() <= 1e-5 * max(1.0, want_g.abs().max().item()) * (R**0.5)
+    assert (got_s - want_s).abs().max().item() <= 1e-5 * max(1.0, want_s.abs().max().item()) * (R**0.5)
