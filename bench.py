@@ -80,6 +80,26 @@ def time_events(fn, iters, warmup, stream):
     return statistics.median(times)
 
 
+def time_events_batched(fn, iters, warmup, stream, batch=10):
+    """Median ms per call of `batch` back-to-back calls between one event pair: the host enqueues the
+    next call while the GPU runs the current one, so host-side work between calls is not counted."""
+
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(iters):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(batch):
+            fn()
+        b.record(stream)
+        b.synchronize()
+        times.append(a.elapsed_time(b) / batch)
+    return statistics.median(times)
+
+
 def kernel_times(q, k, v, bias, dout, iters=20):
     """Median ms of each kernel, each launched alone on the current stream (HIP events)."""
 
@@ -560,10 +580,10 @@ def gate_stage(device):
     stream = torch.cuda.current_stream()
     fwd = lambda: gate_mod.gate_forward(att5, single_rows, w, True)
     _, logits = fwd()
-    fwd_ms = time_events(fwd, 20, 3, stream)
+    fwd_ms = time_events_batched(fwd, 10, 3, stream)
     grad = torch.randn(rows, width, generator=g).to(torch.bfloat16).to(device)
     bwd = lambda: gate_mod.gate_backward(grad, att5, logits, True, True)
-    bwd_ms = time_events(bwd, 20, 3, stream)
+    bwd_ms = time_events_batched(bwd, 10, 3, stream)
     fwd_bytes = 2 * (rows * c + width * c + 3 * rows * width)  # single, W, attention read; gated, logits written
     bwd_bytes = 2 * 5 * rows * width  # logits, grad, attention read; two gradients written
     leaves = [t.requires_grad_(True) for t in (att, single, w, wo)]

@@ -66,6 +66,19 @@ __device__ __forceinline__ uint4 buffer_load16_s(__amdgpu_buffer_rsrc_t r, uint3
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
+// Packed pairs p[2q], p[2q+1] of a lane's tokens (or channels) 8q + 4g .. 8q + 4g + 3 (q = 0..3, g = lane / 32) are
+// traded between the two 32-lane halves with v_permlane32_swap: afterwards the lower half holds
+// tokens 0..15 and the upper half tokens 16..31, lo = the first 8 and hi = the next 8 (one 32-byte
+// run per lane).  Every lane of the wave must execute it.
+__device__ __forceinline__ void trade16(const uint32_t (&p)[8], uint4& lo, uint4& hi) {
+  const auto x0 = __builtin_amdgcn_permlane32_swap(p[0], p[4], false, false);
+  const auto x1 = __builtin_amdgcn_permlane32_swap(p[1], p[5], false, false);
+  const auto x2 = __builtin_amdgcn_permlane32_swap(p[2], p[6], false, false);
+  const auto x3 = __builtin_amdgcn_permlane32_swap(p[3], p[7], false, false);
+  lo = make_uint4(x0[0], x1[0], x0[1], x1[1]);
+  hi = make_uint4(x2[0], x3[0], x2[1], x3[1]);
+}
+
 // Identity k-operand carrying weight w: MFMA c of a 32-wide tile adds the
 // 16 entries 16c .. 16c+15 of the other operand's k axis, each times w.
 template <typename T>

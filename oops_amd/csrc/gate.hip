@@ -17,6 +17,7 @@
 // gate_multiply_*_kernel: elementwise over [rows][H*D], 16 bytes per lane
 // where the layout allows, else one element per lane; the roundings follow
 // _gate_forward / _gate_backward (kernel.py:39-114).
+#include <algorithm>
 #include <initializer_list>
 #include <type_traits>
 
@@ -42,8 +43,9 @@ struct GateArgs {
   int64_t rows, tokens, groups;
   int64_t a_sb, a_sg, a_st, a_sh, a_sd;
   int64_t s_row, w_row;
-  int64_t tiles;  // projection: token tiles x channel tiles
+  int64_t tiles;  // projection: token tiles x channel tiles (W-resident form: token runs x channel tiles)
   int heads, width, channels;
+  int tpw;  // W-resident form: token tiles per workgroup
 };
 
 GateArgs make_args(const oops_gate_geometry& g) {
@@ -88,6 +90,93 @@ __device__ __forceinline__ int64_t att_row(const GateArgs& a, int64_t r) {
 constexpr int kBM = 128;  // tokens per workgroup (32 per wave)
 constexpr int kBN = 128;  // gate channels per workgroup
 constexpr int kBK = 64;   // k per step
+#ifndef OOPS_GATE_WGS
+#define OOPS_GATE_WGS 512  // workgroups of the W-resident projection (two per CU)
+#endif
+
+// epilogue of one token tile: lane (lq, g2) of accumulator tile t owns channels n0 + 32 t + 16 g2 .. +15
+// of token r; logits rounded to T (stored in training), sigmoid rounded to T, times the attention values
+template <typename T, bool STORE_LOGITS>
+__device__ __forceinline__ void gate_epilogue(const GateArgs& a, int64_t r, int n0, int N, int g2,
+                                              const f32x16 (&acc)[4], const uint4 (&att_lo)[4],
+                                              const uint4 (&att_hi)[4]) {
+  T* lrow = STORE_LOGITS ? static_cast<T*>(a.logits) + r * N : nullptr;
+  T* grow = static_cast<T*>(a.gated) + r * N;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    uint32_t p[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      p[2 * q] = pack2<T>(acc[t][4 * q], acc[t][4 * q + 1]);
+      p[2 * q + 1] = pack2<T>(acc[t][4 * q + 2], acc[t][4 * q + 3]);
+    }
+    const auto x0 = __builtin_amdgcn_permlane32_swap(p[0], p[4], false, false);
+    const auto x1 = __builtin_amdgcn_permlane32_swap(p[1], p[5], false, false);
+    const auto x2 = __builtin_amdgcn_permlane32_swap(p[2], p[6], false, false);
+    const auto x3 = __builtin_amdgcn_permlane32_swap(p[3], p[7], false, false);
+    const uint4 lo = make_uint4(x0[0], x1[0], x0[1], x1[1]);  // channels +0 .. +7
+    const uint4 hi = make_uint4(x2[0], x3[0], x2[1], x3[1]);  // channels +8 .. +15
+    const int n = n0 + 32 * t + 16 * g2;
+    if (n >= N) continue;  // N is a multiple of 16: a run is wholly in or out
+    if constexpr (STORE_LOGITS) {
+      *reinterpret_cast<uint4*>(lrow + n) = lo;
+      *reinterpret_cast<uint4*>(lrow + n + 8) = hi;
+    }
+    const uint4 alo = att_lo[t];
+    const uint4 ahi = att_hi[t];
+    const T* le = reinterpret_cast<const T*>(&lo);
+    const T* he = reinterpret_cast<const T*>(&hi);
+    const T* ae = reinterpret_cast<const T*>(&alo);
+    const T* be = reinterpret_cast<const T*>(&ahi);
+    uint32_t o[8];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      o[e / 2] = pack2<T>(rnd<T>(sigmoid_f(to_f(le[e]))) * to_f(ae[e]), rnd<T>(sigmoid_f(to_f(le[e + 1]))) * to_f(ae[e + 1]));
+      o[4 + e / 2] =
+          pack2<T>(rnd<T>(sigmoid_f(to_f(he[e]))) * to_f(be[e]), rnd<T>(sigmoid_f(to_f(he[e + 1]))) * to_f(be[e + 1]));
+    }
+    *reinterpret_cast<uint4*>(grow + n) = make_uint4(o[0], o[1], o[2], o[3]);
+    *reinterpret_cast<uint4*>(grow + n + 8) = make_uint4(o[4], o[5], o[6], o[7]);
+  }
+}
+
+// the same epilogue with range-checked buffer stores and no branches (lane_off is kOut for a lane past
+// the rows): the loop around it then knows how many stores are outstanding and does not drain them
+template <typename T, bool STORE_LOGITS>
+__device__ __forceinline__ void gate_epilogue_buf(const __amdgpu_buffer_rsrc_t& lr, const __amdgpu_buffer_rsrc_t& gr,
+                                                  uint32_t lane_off, int n0, int N, int g2, const f32x16 (&acc)[4],
+                                                  const uint4 (&att_lo)[4], const uint4 (&att_hi)[4]) {
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    uint32_t p[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      p[2 * q] = pack2<T>(acc[t][4 * q], acc[t][4 * q + 1]);
+      p[2 * q + 1] = pack2<T>(acc[t][4 * q + 2], acc[t][4 * q + 3]);
+    }
+    uint4 lo, hi;
+    trade16(p, lo, hi);  // channels n .. n + 7, n + 8 .. n + 15 of the lane's token
+    const int n = n0 + 32 * t + 16 * g2;
+    const uint32_t off = lane_off != kOut && n < N ? lane_off + (uint32_t)(n * 2) : kOut;
+    if constexpr (STORE_LOGITS) {
+      buffer_store16(lr, off, lo);
+      buffer_store16(lr, off + 16, hi);
+    }
+    const T* le = reinterpret_cast<const T*>(&lo);
+    const T* he = reinterpret_cast<const T*>(&hi);
+    const T* ae = reinterpret_cast<const T*>(&att_lo[t]);
+    const T* be = reinterpret_cast<const T*>(&att_hi[t]);
+    uint32_t o[8];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      o[e / 2] = pack2<T>(rnd<T>(sigmoid_f(to_f(le[e]))) * to_f(ae[e]), rnd<T>(sigmoid_f(to_f(le[e + 1]))) * to_f(ae[e + 1]));
+      o[4 + e / 2] =
+          pack2<T>(rnd<T>(sigmoid_f(to_f(he[e]))) * to_f(be[e]), rnd<T>(sigmoid_f(to_f(he[e + 1]))) * to_f(be[e + 1]));
+    }
+    buffer_store16(gr, off, make_uint4(o[0], o[1], o[2], o[3]));
+    buffer_store16(gr, off + 16, make_uint4(o[4], o[5], o[6], o[7]));
+  }
+}
 
 template <typename T, bool STORE_LOGITS>
 __global__ __launch_bounds__(256) void gate_projection_kernel(GateArgs a) {
@@ -151,6 +240,23 @@ __global__ __launch_bounds__(256) void gate_projection_kernel(GateArgs a) {
     }
   };
 
+  // the epilogue's attention runs, loaded before the k loop and unconditionally: an absent run (token
+  // past the rows, channels past N) reads a valid address of row 0 and is never used, so no load waits
+  // at a branch
+  uint4 att_lo[4], att_hi[4];
+  {
+    const T* att = static_cast<const T*>(a.attention) + att_row(a, rv ? r : 0);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int n = n0 + 32 * t + 16 * g2;
+      const int nn = rv && n < N ? n : 0;
+      const int h = nn / a.width, d = nn - h * a.width;
+      const T* arow = att + h * a.a_sh + d;
+      att_lo[t] = *reinterpret_cast<const uint4*>(arow);
+      att_hi[t] = *reinterpret_cast<const uint4*>(arow + 8);
+    }
+  }
+
   f32x16 acc[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) acc[t] = f32x16{};
@@ -182,58 +288,126 @@ __global__ __launch_bounds__(256) void gate_projection_kernel(GateArgs a) {
     for (int c = 0; c < 4; ++c) sf[c] = sn[c];
   }
 
-  // ---- epilogue: lane (lq, g2) of tile t owns channels n0 + 32 t + 16 g2 .. +15 of token r
   if (!rv) return;
-  const T* att = static_cast<const T*>(a.attention) + att_row(a, r);
-  T* lrow = STORE_LOGITS ? static_cast<T*>(a.logits) + r * N : nullptr;
-  T* grow = static_cast<T*>(a.gated) + r * N;
-  // the attention runs are loaded before the first store: a store may alias a later load, so loads
-  // placed after stores would each wait for them
-  uint4 att_lo[4], att_hi[4];
+  gate_epilogue<T, STORE_LOGITS>(a, r, n0, N, g2, acc, att_lo, att_hi);
+}
+
+// gate_projection_w_kernel (C <= 256): the same tile and epilogue, with the workgroup's W block (128
+// channels x C) loaded into LDS once and kept across a run of tpw token tiles (about two workgroups per
+// CU for the whole launch, so no workgroup start-up, W reload or k-step barrier per tile).  While a
+// tile's MFMAs consume k-panel p of its `single` fragments, panel p of the next tile loads into the same
+// registers; the tile's attention runs load before its MFMAs.  Every load is unconditional (past the
+// rows it reads out of range, which returns zeros, or a valid address that is never used).
+template <typename T, bool STORE_LOGITS, int NP>
+__global__ __launch_bounds__(256, 2) void gate_projection_w_kernel(GateArgs a) {
+  using E = Elem<T>;
+  using Frag = typename E::Frag;
+  constexpr int WT = kBN * kBK;
+  extern __shared__ __attribute__((aligned(16))) char lds_raw[];
+  T* w_lds = reinterpret_cast<T*>(lds_raw);
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int lq = lane & 31;
+  const int g2 = lane >> 5;
+  const int N = a.heads * a.width;
+  const int C = a.channels;
+  const int nbn = (N + kBN - 1) / kBN;
+  // the channel tiles of one token run are neighbours in one XCD's range and walk the same rows
+  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x, 0);
+  if (tile >= a.tiles) return;
+  const int bn = (int)(tile % nbn);
+  const int64_t run = tile / nbn;
+  const int n0 = bn * kBN;
+  const int64_t tiles_m = (a.rows + kBM - 1) / kBM;
+
+  {
+    const T* w_base = static_cast<const T*>(a.weight) + (int64_t)n0 * a.w_row;
+    const int w_rows = N - n0 < kBN ? N - n0 : kBN;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(w_base, (uint32_t)(((int64_t)(w_rows - 1) * a.w_row + C) * 2));
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int n = n0 + 32 * t + 16 * g2;
-    if (n >= N) continue;
-    const int h = n / a.width, d = n - h * a.width;
-    const T* arow = att + h * a.a_sh + d;
-    att_lo[t] = *reinterpret_cast<const uint4*>(arow);
-    att_hi[t] = *reinterpret_cast<const uint4*>(arow + 8);
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int id = tid + 256 * j, row = id >> 3, ch = id & 7, k = p * kBK + ch * 8;
+        const uint4 u = buffer_load16(wr, row < w_rows && k < C ? (uint32_t)((row * a.w_row + k) * 2) : kOut);
+        *reinterpret_cast<uint4*>(&w_lds[p * WT + swz_off<kBK>(row, ch * 8)]) = u;
+      }
   }
+
+  // token tile tm's `single` resource and this lane's row offset (kOut past the rows or the run)
+  auto tile_src = [&](int64_t tm, bool live, uint32_t& lane_off) {
+    const int64_t r0 = tm * kBM;
+    const int64_t left = live ? a.rows - r0 : 0;
+    const int nrows = (int)(left < kBM ? left : kBM);
+    lane_off = wave * 32 + lq < nrows ? (uint32_t)((wave * 32 + lq) * a.s_row * 2) : kOut;
+    const T* base = static_cast<const T*>(a.single) + (nrows > 0 ? r0 * a.s_row : 0);
+    return make_rsrc(base, nrows > 0 ? (uint32_t)(((int64_t)(nrows - 1) * a.s_row + C) * 2) : 0u);
+  };
+  auto load_panel = [&](const __amdgpu_buffer_rsrc_t& sr, uint32_t lane_off, int p, uint4 (&x)[4]) {
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    uint32_t p[8];
+    for (int c = 0; c < 4; ++c) {
+      const int k = p * kBK + 16 * c + 8 * g2;
+      x[c] = buffer_load16(sr, k < C && lane_off != kOut ? lane_off + (uint32_t)(k * 2) : kOut);
+    }
+  };
+
+  const int64_t tm0 = run * a.tpw;
+  uint4 xs[NP][4];
+  {
+    uint32_t off;
+    const __amdgpu_buffer_rsrc_t sr = tile_src(tm0, true, off);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      p[2 * q] = pack2<T>(acc[t][4 * q], acc[t][4 * q + 1]);
-      p[2 * q + 1] = pack2<T>(acc[t][4 * q + 2], acc[t][4 * q + 3]);
-    }
-    const auto x0 = __builtin_amdgcn_permlane32_swap(p[0], p[4], false, false);
-    const auto x1 = __builtin_amdgcn_permlane32_swap(p[1], p[5], false, false);
-    const auto x2 = __builtin_amdgcn_permlane32_swap(p[2], p[6], false, false);
-    const auto x3 = __builtin_amdgcn_permlane32_swap(p[3], p[7], false, false);
-    const uint4 lo = make_uint4(x0[0], x1[0], x0[1], x1[1]);  // channels +0 .. +7
-    const uint4 hi = make_uint4(x2[0], x3[0], x2[1], x3[1]);  // channels +8 .. +15
-    const int n = n0 + 32 * t + 16 * g2;
-    if (n >= N) continue;  // N is a multiple of 16: a run is wholly in or out
-    if constexpr (STORE_LOGITS) {
-      *reinterpret_cast<uint4*>(lrow + n) = lo;
-      *reinterpret_cast<uint4*>(lrow + n + 8) = hi;
-    }
-    const uint4 alo = att_lo[t];
-    const uint4 ahi = att_hi[t];
-    const T* le = reinterpret_cast<const T*>(&lo);
-    const T* he = reinterpret_cast<const T*>(&hi);
-    const T* ae = reinterpret_cast<const T*>(&alo);
-    const T* be = reinterpret_cast<const T*>(&ahi);
-    uint32_t o[8];
+    for (int p = 0; p < NP; ++p) load_panel(sr, off, p, xs[p]);
+  }
+  __syncthreads();  // W block written
+
+  for (int it = 0; it < a.tpw; ++it) {
+    const int64_t tm = tm0 + it;
+    if (tm >= tiles_m) break;
+    const int64_t r = tm * kBM + wave * 32 + lq;  // this lane's token
+    const bool rv = r < a.rows;
+    uint4 att_lo[4], att_hi[4];
+    {
+      const T* att = static_cast<const T*>(a.attention) + att_row(a, rv ? r : 0);
 #pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      o[e / 2] = pack2<T>(rnd<T>(sigmoid_f(to_f(le[e]))) * to_f(ae[e]), rnd<T>(sigmoid_f(to_f(le[e + 1]))) * to_f(ae[e + 1]));
-      o[4 + e / 2] =
-          pack2<T>(rnd<T>(sigmoid_f(to_f(he[e]))) * to_f(be[e]), rnd<T>(sigmoid_f(to_f(he[e + 1]))) * to_f(be[e + 1]));
+      for (int t = 0; t < 4; ++t) {
+        const int n = n0 + 32 * t + 16 * g2;
+        const int nn = rv && n < N ? n : 0;
+        const int h = nn / a.width, d = nn - h * a.width;
+        const T* arow = att + h * a.a_sh + d;
+        att_lo[t] = *reinterpret_cast<const uint4*>(arow);
+        att_hi[t] = *reinterpret_cast<const uint4*>(arow + 8);
+      }
     }
-    *reinterpret_cast<uint4*>(grow + n) = make_uint4(o[0], o[1], o[2], o[3]);
-    *reinterpret_cast<uint4*>(grow + n + 8) = make_uint4(o[4], o[5], o[6], o[7]);
+    // keeps the attention loads here, ahead of the MFMAs (the compiler would otherwise sink them into the
+    // epilogue, next to their first use)
+    asm volatile("" ::: "memory");
+    uint32_t noff;
+    const __amdgpu_buffer_rsrc_t nsr = tile_src(tm + 1, it + 1 < a.tpw && tm + 1 < tiles_m, noff);
+    f32x16 acc[4];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const T* wt = &w_lds[p * WT];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const Frag bfr = __builtin_bit_cast(Frag, xs[p][c]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          acc[t] = E::mma(lds_frag<T>(wt + swz_off<kBK>(32 * t + lq, 16 * c + 8 * g2)), bfr,
+                          p == 0 && c == 0 ? f32x16{} : acc[t]);
+      }
+      load_panel(nsr, noff, p, xs[p]);  // the next tile's panel p
+    }
+    const int64_t r0 = tm * kBM;
+    const int64_t left = a.rows - r0;
+    const int nrows = (int)(left < kBM ? left : kBM);
+    const uint32_t out_bytes = (uint32_t)((int64_t)nrows * N * 2);
+    const __amdgpu_buffer_rsrc_t lr = make_rsrc(STORE_LOGITS ? static_cast<T*>(a.logits) + r0 * N : nullptr, out_bytes);
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(static_cast<T*>(a.gated) + r0 * N, out_bytes);
+    gate_epilogue_buf<T, STORE_LOGITS>(lr, gr, rv ? (uint32_t)((wave * 32 + lq) * N * 2) : kOut, n0, N, g2, acc,
+                                       att_lo, att_hi);
   }
 }
 
@@ -369,8 +543,37 @@ hipError_t launch_gate_projection(const oops_gate_geometry& g, const void* singl
   a.gated = gated;
   a.logits = logits;
   const int64_t N = (int64_t)g.heads * g.width;
-  const int64_t blocks = ((g.rows + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
+  const int64_t tiles_m = (g.rows + kBM - 1) / kBM, nbn = (N + kBN - 1) / kBN;
+  const int64_t blocks = tiles_m * nbn;
   if (blocks == 0) return hipSuccess;
+  if (g.channels <= 4 * kBK) {
+    // W-resident form: about OOPS_GATE_WGS workgroups, each a run of token tiles of one channel tile
+    const int runs_max = (int)std::max<int64_t>(1, OOPS_GATE_WGS / nbn);
+    a.tpw = (int)((tiles_m + runs_max - 1) / runs_max);
+    a.tiles = (tiles_m + a.tpw - 1) / a.tpw * nbn;
+    const int np = (int)((g.channels + kBK - 1) / kBK);
+    const size_t lds = (size_t)(np == 3 ? 4 : np) * kBN * kBK * 2;
+    const int64_t grid = xcd_grid(a.tiles, 0);
+    return by_dtype(g.dtype, [&](auto tag) -> hipError_t {
+      using T = typename decltype(tag)::type;
+      if constexpr (std::is_same<T, float>::value) {
+        return hipErrorInvalidValue;
+      } else {
+        auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(256), lds, stream, a); };
+        auto by_np = [&](auto logits_tag) {
+          constexpr bool L = decltype(logits_tag)::value;
+          if (np == 1)
+            go(gate_projection_w_kernel<T, L, 1>);
+          else if (np == 2)
+            go(gate_projection_w_kernel<T, L, 2>);
+          else
+            go(gate_projection_w_kernel<T, L, 4>);
+        };
+        logits != nullptr ? by_np(std::true_type{}) : by_np(std::false_type{});
+        return hipGetLastError();
+      }
+    });
+  }
   a.tiles = blocks;
   const int64_t grid = xcd_grid(blocks, 0);
   return by_dtype(g.dtype, [&](auto tag) -> hipError_t {

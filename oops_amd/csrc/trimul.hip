@@ -294,19 +294,6 @@ __global__ __launch_bounds__(256) void row_norm_backward_kernel(RowNormArgs a) {
   }
 }
 
-// Packed pairs p[2q], p[2q+1] of a lane's tokens 8q + 4g .. 8q + 4g + 3 (q = 0..3, g = lane / 32) are
-// traded between the two 32-lane halves with v_permlane32_swap: afterwards the lower half holds
-// tokens 0..15 and the upper half tokens 16..31, lo = the first 8 and hi = the next 8 (one 32-byte
-// run per lane).  Every lane of the wave must execute it.
-__device__ __forceinline__ void trade16(const uint32_t (&p)[8], uint4& lo, uint4& hi) {
-  const auto x0 = __builtin_amdgcn_permlane32_swap(p[0], p[4], false, false);
-  const auto x1 = __builtin_amdgcn_permlane32_swap(p[1], p[5], false, false);
-  const auto x2 = __builtin_amdgcn_permlane32_swap(p[2], p[6], false, false);
-  const auto x3 = __builtin_amdgcn_permlane32_swap(p[3], p[7], false, false);
-  lo = make_uint4(x0[0], x1[0], x0[1], x1[1]);
-  hi = make_uint4(x2[0], x3[0], x2[1], x3[1]);
-}
-
 // ------------------------------------------------------------------ factors
 struct FactorArgs {
   const void* xn;
@@ -713,6 +700,9 @@ __device__ __forceinline__ void step_block(int64_t& g, int& p, int P, int by) {
 #ifndef V16_PREFETCH
 #define V16_PREFETCH !BWD
 #endif
+#ifndef V16_STAGE
+#define V16_STAGE 1
+#endif
 #ifndef V16_FWD_OCC
 #define V16_FWD_OCC 2
 #endif
@@ -722,6 +712,7 @@ __global__ __launch_bounds__(256, BWD ? 2 : V16_FWD_OCC) void trimul_factor_v16_
   using E = Elem<T>;
   using Frag = typename E::Frag;
   constexpr int WT = 128 * kFK;
+  constexpr bool STAGE = V16_STAGE && !BWD && NP <= 2;
   extern __shared__ __attribute__((aligned(16))) char lds_raw[];
   T* w_lds = reinterpret_cast<T*>(lds_raw);
 
@@ -799,13 +790,37 @@ __global__ __launch_bounds__(256, BWD ? 2 : V16_FWD_OCC) void trimul_factor_v16_
 
   uint4 xs[2][4];  // panel i of a tile in xs[i % 2]; xs[0] may hold the next tile's first panel
   bool prefetched = false;
+  // STAGE: the wave's 32 rows are loaded whole (each instruction reads 64 / (8 NP) complete rows) into
+  // registers one tile ahead, then copied to the wave's own LDS rows and read back as fragments
+  T* x_w = w_lds + NP * WT + wave * NP * 32 * kFK;
+  uint4 xc[STAGE ? 4 * NP : 1];
+  auto load_rows = [&](int64_t r0) {
+    const int64_t left = R - r0 - wave * 32;
+    const int nrows = (int)(left < 0 ? 0 : left < 32 ? left : 32);
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(static_cast<const T*>(a.xn) + (nrows ? r0 + wave * 32 : 0) * a.c_row,
+                                                (uint32_t)((int64_t)nrows * a.c_row * 2));
+#pragma unroll
+    for (int j = 0; j < 4 * NP; ++j) {
+      const int id = lane + 64 * j, row = id / (8 * NP), k = (id % (8 * NP)) * 8;
+      xc[j] = buffer_load16(rr, row < nrows && k < K ? (uint32_t)((row * a.c_row + k) * 2) : kOut);
+    }
+  };
+  if constexpr (STAGE) load_rows(bmg * tpw * kFM);
   for (int it = 0; it < tpw; ++it) {
     const int64_t r0 = (bmg * tpw + it) * kFM;
     if (r0 >= R) break;
     __amdgpu_buffer_rsrc_t xr;
     bool rv;
-    tile_x(r0, xr, rv);
-    if (!prefetched) load_x_of(xr, rv, 0, xs[0]);
+    if constexpr (STAGE) {
+#pragma unroll
+      for (int j = 0; j < 4 * NP; ++j) {
+        const int id = lane + 64 * j, row = id / (8 * NP), ch = id % (8 * NP);
+        *reinterpret_cast<uint4*>(&x_w[(ch >> 3) * 32 * kFK + swz_off<kFK>(row, (ch & 7) * 8)]) = xc[j];
+      }
+    } else {
+      tile_x(r0, xr, rv);
+      if (!prefetched) load_x_of(xr, rv, 0, xs[0]);
+    }
 
     // the epilogue's loads go out before the MFMA loop (and before the next tile's prefetch, which
     // the epilogue must not wait for).  Accumulator entry 4q + i is token r0 + 32 wave + 8q + 4 g2 + i,
@@ -842,15 +857,21 @@ __global__ __launch_bounds__(256, BWD ? 2 : V16_FWD_OCC) void trimul_factor_v16_
       }
     }
 
+    // the next tile's rows load during this tile (after the epilogue's loads, which are waited for first)
+    if constexpr (STAGE) {
+      if (it + 1 < tpw && r0 + kFM < R) load_rows(r0 + kFM);
+    }
+
     // the first panel starts from zero accumulators (no register clear)
     f32x16 acc[4];
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
-      if (i + 1 < NP) load_x_of(xr, rv, (i + 1) * kFK, xs[(i + 1) & 1]);
+      if (!STAGE && i + 1 < NP) load_x_of(xr, rv, (i + 1) * kFK, xs[(i + 1) & 1]);
       const T* wt = &w_lds[i * WT];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const Frag afr = __builtin_bit_cast(Frag, xs[i & 1][c]);
+        const Frag afr = STAGE ? lds_frag<T>(x_w + i * 32 * kFK + swz_off<kFK>(lq, 16 * c + 8 * g2))
+                               : __builtin_bit_cast(Frag, xs[i & 1][c]);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const Frag bfr = lds_frag<T>(wt + swz_off<kFK>(32 * t + lq, 16 * c + 8 * g2));
@@ -860,7 +881,7 @@ __global__ __launch_bounds__(256, BWD ? 2 : V16_FWD_OCC) void trimul_factor_v16_
       }
     }
     // the next tile's first panel loads while this tile's epilogue runs
-    prefetched = V16_PREFETCH && it + 1 < tpw && r0 + kFM < R;
+    prefetched = !STAGE && V16_PREFETCH && it + 1 < tpw && r0 + kFM < R;
     if (prefetched) {
       __amdgpu_buffer_rsrc_t xr_n;
       bool rv_n;
@@ -1934,6 +1955,14 @@ struct FactorPlan {
   int64_t groups, tiles;
   size_t lds;
 };
+// workgroups of the factor kernels (each keeps its W block across its token tiles): the straight-line
+// forward runs best with two resident workgroups per CU and no second round
+#ifndef OOPS_FACTOR_WGS
+#define OOPS_FACTOR_WGS 2048
+#endif
+#ifndef OOPS_FACTOR_FWD_WGS
+#define OOPS_FACTOR_FWD_WGS 512
+#endif
 FactorPlan factor_plan(const oops_trimul_geometry& g, bool backward) {
   const int64_t cblocks = factor_cblocks(g);
   const int64_t token_tiles = (g.groups * g.positions + kFM - 1) / kFM;
@@ -1942,13 +1971,15 @@ FactorPlan factor_plan(const oops_trimul_geometry& g, bool backward) {
   // backward's epilogue holds more live values: the streaming form keeps it under 256 VGPRs
   pl.v16 = g.positions % 16 == 0 && g.c_row <= kFullWMaxK;
   pl.fullw = g.c_row <= kFullWMaxK && (!backward || pl.v16);
-  // about 2048 workgroups: each keeps its W block across several token tiles
-  pl.tpw = pl.fullw ? (int)std::max<int64_t>(1, (token_tiles * 2 * cblocks + 2047) / 2048) : 1;
+  const int64_t wgs = backward || !pl.v16 ? OOPS_FACTOR_WGS : OOPS_FACTOR_FWD_WGS;
+  pl.tpw = pl.fullw ? (int)std::max<int64_t>(1, (token_tiles * 2 * cblocks + wgs - 1) / wgs) : 1;
   pl.groups = (token_tiles + pl.tpw - 1) / pl.tpw;
   pl.tiles = pl.groups * 2 * cblocks;
   int64_t panels = (g.c_row + kFK - 1) / kFK;
   if (pl.v16 && panels == 3) panels = 4;  // the straight-line kernel is built for 1, 2 or 4 panels
   pl.lds = (size_t)(pl.fullw ? panels : 2) * 128 * kFK * 2;
+  // the forward straight-line kernel of one or two panels also stages each wave's 32 x rows
+  if (V16_STAGE && pl.v16 && !backward && panels <= 2) pl.lds += (size_t)panels * 4 * 32 * kFK * 2;
   return pl;
 }
 }  // namespace

@@ -59,6 +59,20 @@ def test_gate_dense(dtype, prefix, d):
     _check(*_inputs(dtype, prefix, heads=4, q=37, d=d, c=72, o=40, seed=len(prefix) + d), dtype)
 
 
+@pytest.mark.parametrize(
+    "dtype,prefix,heads,q,c",
+    [
+        (torch.bfloat16, (171,), 4, 397, 160),  # three k panels (run as four), two token tiles per workgroup, ragged end
+        (torch.float16, (5,), 2, 33, 64),  # one k panel, a partial channel tile (N = 64)
+        (torch.bfloat16, (3,), 12, 50, 320),  # C > 256: the streaming projection kernel
+    ],
+)
+def test_gate_projection_forms(dtype, prefix, heads, q, c):
+    """The W-resident projection (C <= 256, workgroups walking runs of token tiles) and the streaming one."""
+
+    _check(*_inputs(dtype, prefix, heads=heads, q=q, d=32, c=c, o=48, seed=c + q), dtype)
+
+
 def test_gate_large_msa_shape():
     """MSA-row shape (S=64, N=384, H=8, c=32, C=256, O=256), bf16."""
 
