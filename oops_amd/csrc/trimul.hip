@@ -785,7 +785,7 @@ __global__ __launch_bounds__(256, BWD ? 2 : V16_FWD_OCC) void trimul_factor_v16_
     pb[h] = (int)(rb - gb[h] * P);
   }
   const int64_t fG = (int64_t)f * a.groups;
-  const float* mask = a.mask;
+  const __amdgpu_buffer_rsrc_t mask_rs = make_rsrc(a.mask, MASKED ? (uint32_t)(R * 4) : 0u);
   float bsum[2][2] = {{0.f, 0.f}, {0.f, 0.f}};  // [t][value, gate] over this lane's tokens
 
   uint4 xs[2][4];  // panel i of a tile in xs[i % 2]; xs[0] may hold the next tile's first panel
@@ -794,8 +794,8 @@ __global__ __launch_bounds__(256, BWD ? 2 : V16_FWD_OCC) void trimul_factor_v16_
   // registers one tile ahead, then copied to the wave's own LDS rows and read back as fragments
   T* x_w = w_lds + NP * WT + wave * NP * 32 * kFK;
   uint4 xc[STAGE ? 4 * NP : 1];
-  auto load_rows = [&](int64_t r0) {
-    const int64_t left = R - r0 - wave * 32;
+  auto load_rows = [&](int64_t r0, bool live) {
+    const int64_t left = live ? R - r0 - wave * 32 : 0;
     const int nrows = (int)(left < 0 ? 0 : left < 32 ? left : 32);
     const __amdgpu_buffer_rsrc_t rr = make_rsrc(static_cast<const T*>(a.xn) + (nrows ? r0 + wave * 32 : 0) * a.c_row,
                                                 (uint32_t)((int64_t)nrows * a.c_row * 2));
@@ -805,7 +805,7 @@ __global__ __launch_bounds__(256, BWD ? 2 : V16_FWD_OCC) void trimul_factor_v16_
       xc[j] = buffer_load16(rr, row < nrows && k < K ? (uint32_t)((row * a.c_row + k) * 2) : kOut);
     }
   };
-  if constexpr (STAGE) load_rows(bmg * tpw * kFM);
+  if constexpr (STAGE) load_rows(bmg * tpw * kFM, true);
   for (int it = 0; it < tpw; ++it) {
     const int64_t r0 = (bmg * tpw + it) * kFM;
     if (r0 >= R) break;
@@ -832,14 +832,20 @@ __global__ __launch_bounds__(256, BWD ? 2 : V16_FWD_OCC) void trimul_factor_v16_
     const bool st_ok = g2 ? blk_ok[1] : blk_ok[0];  // this lane's 16 post-trade tokens exist
     // every load is unconditional (an absent block reads a valid address and is replaced afterwards), so
     // no load sits behind a branch that waits for it
+    // (absent blocks read out of range: zeros, no request).  The factor layout's accesses go through a
+    // window from block 0's group (block 1 is in that group or the next), so the offsets stay 32-bit.
+    const int64_t fwin = (fG + gb[0]) * H * P;
+    const uint32_t fwin_bytes = (uint32_t)((int64_t)4 * H * P);
+    uint32_t f_off[2];  // byte offset of the lane's 16 post-trade tokens of channel hv[t] in the window
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      f_off[t] = hv_ok[t] && st_ok ? (uint32_t)(((g2 ? fbase[1] : fbase[0]) - fwin + (int64_t)hv[t] * P) * 2) : kOut;
     float keep[4][4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       float4 k4 = make_float4(1.f, 1.f, 1.f, 1.f);
-      if constexpr (MASKED) {
-        const float4 m4 = *reinterpret_cast<const float4*>(mask + (blk_ok[q >> 1] ? rw + 8 * q + 4 * g2 : 0));
-        if (blk_ok[q >> 1]) k4 = m4;
-      }
+      if constexpr (MASKED)
+        k4 = __builtin_bit_cast(float4, buffer_load16(mask_rs, blk_ok[q >> 1] ? (uint32_t)((rw + 8 * q + 4 * g2) * 4) : kOut));
       keep[q][0] = k4.x, keep[q][1] = k4.y, keep[q][2] = k4.z, keep[q][3] = k4.w;
     }
     // BWD: the factor gradients of the lane's 16 post-trade tokens (2 x 16 bytes per channel tile),
@@ -858,9 +864,7 @@ __global__ __launch_bounds__(256, BWD ? 2 : V16_FWD_OCC) void trimul_factor_v16_
     }
 
     // the next tile's rows load during this tile (after the epilogue's loads, which are waited for first)
-    if constexpr (STAGE) {
-      if (it + 1 < tpw && r0 + kFM < R) load_rows(r0 + kFM);
-    }
+    if constexpr (STAGE) load_rows(r0 + kFM, it + 1 < tpw);
 
     // the first panel starts from zero accumulators (no register clear)
     f32x16 acc[4];
@@ -933,12 +937,12 @@ __global__ __launch_bounds__(256, BWD ? 2 : V16_FWD_OCC) void trimul_factor_v16_
       }
       uint4 lo, hi;
       trade16(po, lo, hi);
+      // forward: branch-free range-checked stores (absent lanes store out of range), so the wait counts of
+      // the loop stay exact (the backward measured faster with its plain stores)
       if constexpr (!BWD) {
-        if (hv_ok[t] && st_ok) {
-          T* dst = static_cast<T*>(a.factors) + (g2 ? fbase[1] : fbase[0]) + (int64_t)hv[t] * P;
-          *reinterpret_cast<uint4*>(dst) = lo;
-          *reinterpret_cast<uint4*>(dst + 8) = hi;
-        }
+        const __amdgpu_buffer_rsrc_t fr = make_rsrc(static_cast<T*>(a.factors) + fwin, fwin_bytes);
+        buffer_store16(fr, f_off[t], lo);
+        buffer_store16(fr, f_off[t] + 16, hi);
       } else {
         uint4 glo, ghi;
         trade16(pg, glo, ghi);
@@ -972,8 +976,9 @@ __global__ __launch_bounds__(256, BWD ? 2 : V16_FWD_OCC) void trimul_factor_v16_
         }
         mp[0] += __shfl_xor(mp[0], 1);
         const int v = lq >> 1, q = v >> 2;
-        if ((lq & 1) == 0 && blk_ok[q >> 1])
-          a.mask_parts[(int64_t)(f * a.cblocks + cb) * R + rw + 8 * q + 4 * g2 + (v & 3)] = mp[0];
+        const __amdgpu_buffer_rsrc_t mpr = make_rsrc(a.mask_parts + (int64_t)(f * a.cblocks + cb) * R, (uint32_t)(R * 4));
+        buffer_store4(mpr, (lq & 1) == 0 && blk_ok[q >> 1] ? (uint32_t)((rw + 8 * q + 4 * g2 + (v & 3)) * 4) : kOut,
+                      mp[0]);
       }
     }
 #pragma unroll
