@@ -712,7 +712,7 @@ __global__ __launch_bounds__(256, BWD ? 2 : V16_FWD_OCC) void trimul_factor_v16_
   using E = Elem<T>;
   using Frag = typename E::Frag;
   constexpr int WT = 128 * kFK;
-  constexpr bool STAGE = V16_STAGE && !BWD && NP <= 2;
+  constexpr bool STAGE = V16_STAGE && NP <= 2;
   extern __shared__ __attribute__((aligned(16))) char lds_raw[];
   T* w_lds = reinterpret_cast<T*>(lds_raw);
 
@@ -1984,7 +1984,7 @@ FactorPlan factor_plan(const oops_trimul_geometry& g, bool backward) {
   if (pl.v16 && panels == 3) panels = 4;  // the straight-line kernel is built for 1, 2 or 4 panels
   pl.lds = (size_t)(pl.fullw ? panels : 2) * 128 * kFK * 2;
   // the forward straight-line kernel of one or two panels also stages each wave's 32 x rows
-  if (V16_STAGE && pl.v16 && !backward && panels <= 2) pl.lds += (size_t)panels * 4 * 32 * kFK * 2;
+  if (V16_STAGE && pl.v16 && panels <= 2) pl.lds += (size_t)panels * 4 * 32 * kFK * 2;
   return pl;
 }
 }  // namespace
