@@ -1460,6 +1460,7 @@ struct OutArgs {
   void* ggate;
   int64_t rows, c_row, h_row, tiles;
   int C, cblocks;
+  int tpw;  // W-resident form: token tiles per workgroup
 };
 
 constexpr int kOM = 128;  // tokens per workgroup
@@ -1669,6 +1670,201 @@ __global__ __launch_bounds__(256) void trimul_output_kernel(OutArgs a) {
         T* drow = static_cast<T*>(which == 0 ? a.gval : a.ggate) + r * a.c_row;
         if (n < cr) *reinterpret_cast<uint4*>(drow + n) = make_uint4(z0[0], z1[0], z0[1], z1[1]);
         if (n + 8 < cr) *reinterpret_cast<uint4*>(drow + n + 8) = make_uint4(z2[0], z3[0], z2[1], z3[1]);
+      }
+    }
+  }
+}
+
+// trimul_output_w_kernel: the output kernel for 16-bit rows with h_row, c_row <= 128 and C % 8 == 0.  Same
+// tile, MFMAs and epilogue; both W blocks of the workgroup's 64 channels (two 64-wide k panels each) stay
+// in LDS across a run of tpw token tiles (about two workgroups per CU for the launch, no W reload or k-step
+// barrier per tile).  As a tile's MFMAs finish with k panel j of a projection, panel j of the next tile
+// loads into the same registers; the upstream gradient (backward) loads before the MFMAs.  Loads and stores
+// are range-checked buffer accesses with no branches around them (absent rows and channels use an
+// out-of-range offset), so the loop never drains its outstanding stores.
+#ifndef OOPS_OUTPUT_WGS
+#define OOPS_OUTPUT_WGS 512
+#endif
+template <typename T, bool BWD>
+__global__ __launch_bounds__(256, 2) void trimul_output_w_kernel(OutArgs a) {
+  using E = Elem<T>;
+  using Frag = typename E::Frag;
+  constexpr int WT = kON * kOK;                              // one 64-channel x 64-k panel
+  __shared__ __attribute__((aligned(16))) T w_lds[4 * WT];  // [projection][k panel]
+  __shared__ __attribute__((aligned(16))) float b_lds[2][kON];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, lq = lane & 31, g2 = lane >> 5;
+  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x, 0);
+  if (tile >= a.tiles) return;
+  const int cb = (int)(tile % a.cblocks);
+  const int64_t run = tile / a.cblocks;
+  const int c0 = cb * kON;
+  const int C = a.C;
+  const int wrows = C - c0 < kON ? C - c0 : kON;
+  if (tid < 2 * kON) {
+    const int ph = tid / kON, ch = c0 + tid % kON;
+    const float* bsrc = ph == 0 ? a.bo : a.bg;
+    const float bv = bsrc != nullptr && ch < C ? bsrc[ch] : 0.f;
+    b_lds[ph][tid % kON] = ph == 0 ? bv : -bv * kLog2e;
+  }
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int64_t stride = p == 0 ? a.h_row : a.c_row;
+    const T* wb = static_cast<const T*>(p == 0 ? a.wo : a.wg) + (int64_t)c0 * stride;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, (uint32_t)((int64_t)wrows * stride * 2));
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int id = tid + 256 * q, row = id >> 3, k = 64 * j + (id & 7) * 8;
+        const uint4 u = buffer_load16(wr, row < wrows && k < stride ? (uint32_t)((row * stride + k) * 2) : kOut);
+        *reinterpret_cast<uint4*>(&w_lds[(2 * p + j) * WT + swz_off<kOK>(row, (id & 7) * 8)]) = u;
+      }
+  }
+
+  const int64_t tiles_m = (a.rows + kOM - 1) / kOM;
+  // projection p's rows of token tile tm (none when !live) and this lane's row offset
+  auto src = [&](int p, int64_t tm, bool live, uint32_t& off) {
+    const int64_t stride = p == 0 ? a.h_row : a.c_row;
+    const int64_t r0 = tm * kOM;
+    const int64_t left = live ? a.rows - r0 : 0;
+    const int nrows = (int)(left < 0 ? 0 : left < kOM ? left : kOM);
+    off = wave * 32 + lq < nrows ? (uint32_t)((wave * 32 + lq) * stride * 2) : kOut;
+    const T* act = static_cast<const T*>(p == 0 ? a.nrm : a.xn) + (nrows > 0 ? r0 * stride : 0);
+    return make_rsrc(act, (uint32_t)((int64_t)nrows * stride * 2));
+  };
+  auto load_panel = [&](const __amdgpu_buffer_rsrc_t& sr, uint32_t off, int p, int j, uint4 (&x)[4]) {
+    const int K = (int)(p == 0 ? a.h_row : a.c_row);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int k = 64 * j + 16 * c + 8 * g2;
+      x[c] = buffer_load16(sr, k < K && off != kOut ? off + (uint32_t)(k * 2) : kOut);
+    }
+  };
+  const int64_t tm0 = run * a.tpw;
+  uint4 xs[4][4];  // [2 projection + k panel][fragment]
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    uint32_t off;
+    const __amdgpu_buffer_rsrc_t sr = src(p, tm0, true, off);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) load_panel(sr, off, p, j, xs[2 * p + j]);
+  }
+  __syncthreads();  // W blocks and biases written
+
+  for (int it = 0; it < a.tpw; ++it) {
+    const int64_t tm = tm0 + it;
+    if (tm >= tiles_m) break;
+    const int64_t r0 = tm * kOM;
+    const int64_t left = a.rows - r0;
+    const int nrows = (int)(left < kOM ? left : kOM);
+    const bool rv = wave * 32 + lq < nrows;
+    const uint32_t row_lane = (uint32_t)(wave * 32 + lq);
+    // BWD: grad_out of the lane's 16 post-swap channels n .. n + 15 of each tile t
+    uint4 gin[2][2];
+    if constexpr (BWD) {
+      const __amdgpu_buffer_rsrc_t gr = make_rsrc(static_cast<const T*>(a.gout) + r0 * C, (uint32_t)((int64_t)nrows * C * 2));
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int n = c0 + 32 * t + 16 * g2 + 8 * hh;
+          gin[t][hh] = buffer_load16(gr, rv && n < C ? (row_lane * C + n) * 2 : kOut);
+        }
+      // keeps these loads ahead of the MFMAs (the compiler would sink them to their first use)
+      asm volatile("" ::: "memory");
+    }
+    uint32_t noff[2];
+    __amdgpu_buffer_rsrc_t nsr[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) nsr[p] = src(p, tm + 1, it + 1 < a.tpw && tm + 1 < tiles_m, noff[p]);
+
+    f32x16 acc[4];  // acc[2 p + t]: projection p (0 value, 1 gate logits), channels c0 + 32 t ..
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const T* wt = &w_lds[(2 * p + j) * WT];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const Frag bfr = __builtin_bit_cast(Frag, xs[2 * p + j][c]);
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+            acc[2 * p + t] = E::mma(lds_frag<T>(wt + swz_off<kOK>(32 * t + lq, 16 * c + 8 * g2)), bfr,
+                                    j == 0 && c == 0 ? f32x16{} : acc[2 * p + t]);
+        }
+        load_panel(nsr[p], noff[p], p, j, xs[2 * p + j]);  // the next tile's panel
+      }
+
+    // ---- epilogue: lane (lq, g2) of tile t holds channels c0 + 32t + 8q + 4g2 + i of its token
+    const int cr = (int)a.c_row;
+    const __amdgpu_buffer_rsrc_t o0 = make_rsrc(
+        BWD ? static_cast<void*>(static_cast<T*>(a.gval) + r0 * cr) : static_cast<void*>(static_cast<T*>(a.out) + r0 * C),
+        (uint32_t)((int64_t)nrows * (BWD ? cr : C) * 2));
+    const __amdgpu_buffer_rsrc_t o1 =
+        make_rsrc(BWD ? static_cast<T*>(a.ggate) + r0 * cr : nullptr, BWD ? (uint32_t)((int64_t)nrows * cr * 2) : 0u);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int n = c0 + 32 * t + 16 * g2;  // first of this lane's 16 channels after the swap
+      float v[16], s[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 bo4 = *reinterpret_cast<const float4*>(&b_lds[0][32 * t + 8 * q + 4 * g2]);
+        const float4 bg4 = *reinterpret_cast<const float4*>(&b_lds[1][32 * t + 8 * q + 4 * g2]);
+        const float bo[4] = {bo4.x, bo4.y, bo4.z, bo4.w}, bgl[4] = {bg4.x, bg4.y, bg4.z, bg4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[4 * q + i] = acc[t][4 * q + i] + bo[i];
+          s[4 * q + i] = __builtin_amdgcn_rcpf(
+              1.0f + __builtin_amdgcn_exp2f(__builtin_fmaf(acc[2 + t][4 * q + i], -kLog2e, bgl[i])));
+        }
+      }
+      if constexpr (!BWD) {
+        uint32_t p[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          p[2 * q] = pack2<T>(v[4 * q] * s[4 * q], v[4 * q + 1] * s[4 * q + 1]);
+          p[2 * q + 1] = pack2<T>(v[4 * q + 2] * s[4 * q + 2], v[4 * q + 3] * s[4 * q + 3]);
+        }
+        uint4 lo, hi;
+        trade16(p, lo, hi);
+        const uint32_t off = rv && n < C ? (row_lane * C + n) * 2 : kOut;
+        buffer_store16(o0, off, lo);
+        buffer_store16(o0, rv && n + 8 < C ? off + 16 : kOut, hi);
+      } else {
+        const uint4 lo = gin[t][0], hi = gin[t][1];
+        const auto y0 = __builtin_amdgcn_permlane32_swap(lo.x, lo.z, false, false);
+        const auto y1 = __builtin_amdgcn_permlane32_swap(lo.y, lo.w, false, false);
+        const auto y2 = __builtin_amdgcn_permlane32_swap(hi.x, hi.z, false, false);
+        const auto y3 = __builtin_amdgcn_permlane32_swap(hi.y, hi.w, false, false);
+        const uint32_t p[8] = {y0[0], y1[0], y2[0], y3[0], y0[1], y1[1], y2[1], y3[1]};
+        uint32_t pv[8], pg[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float d[4] = {lo_f<T>(p[2 * q]), hi_f<T>(p[2 * q]), lo_f<T>(p[2 * q + 1]), hi_f<T>(p[2 * q + 1])};
+          float dv[4], dg[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float sv = s[4 * q + i];
+            dv[i] = d[i] * sv;
+            dg[i] = d[i] * v[4 * q + i] * sv * (1.f - sv);
+          }
+          pv[2 * q] = pack2<T>(dv[0], dv[1]);
+          pv[2 * q + 1] = pack2<T>(dv[2], dv[3]);
+          pg[2 * q] = pack2<T>(dg[0], dg[1]);
+          pg[2 * q + 1] = pack2<T>(dg[2], dg[3]);
+        }
+        // channels up to c_row: the padding past C receives zeros (its weights and gradient are zero)
+        const uint32_t off = rv && n < cr ? (row_lane * cr + n) * 2 : kOut;
+        const uint32_t off8 = rv && n + 8 < cr ? off + 16 : kOut;
+        uint4 vlo, vhi, glo, ghi;
+        trade16(pv, vlo, vhi);
+        trade16(pg, glo, ghi);
+        buffer_store16(o0, off, vlo);
+        buffer_store16(o0, off8, vhi);
+        buffer_store16(o1, off, glo);
+        buffer_store16(o1, off8, ghi);
       }
     }
   }
@@ -2153,9 +2349,24 @@ hipError_t launch_trimul_output(const oops_trimul_geometry& g, const void* norma
   a.cblocks = (g.channels + kON - 1) / kON;
   const int64_t tiles = (a.rows + kOM - 1) / kOM * a.cblocks;
   if (tiles == 0) return hipSuccess;
+  const bool bwd = grad_out != nullptr;
+  if (g.h_row <= 2 * kOK && g.c_row <= 2 * kOK && g.channels % 8 == 0) {
+    const int64_t tiles_m = (a.rows + kOM - 1) / kOM;
+    const int64_t runs = std::max<int64_t>(1, OOPS_OUTPUT_WGS / a.cblocks);
+    a.tpw = (int)((tiles_m + runs - 1) / runs);
+    a.tiles = (tiles_m + a.tpw - 1) / a.tpw * a.cblocks;
+    const dim3 wgrid((unsigned)xcd_grid(a.tiles, 0));
+    return by_half(g.dtype, [&](auto tag) -> hipError_t {
+      using T = decltype(tag);
+      if (bwd)
+        hipLaunchKernelGGL((trimul_output_w_kernel<T, true>), wgrid, dim3(256), 0, stream, a);
+      else
+        hipLaunchKernelGGL((trimul_output_w_kernel<T, false>), wgrid, dim3(256), 0, stream, a);
+      return hipGetLastError();
+    });
+  }
   a.tiles = tiles;
   const dim3 grid((unsigned)xcd_grid(tiles, 0));
-  const bool bwd = grad_out != nullptr;
   return by_half(g.dtype, [&](auto tag) -> hipError_t {
     using T = decltype(tag);
     if (bwd)
