@@ -152,8 +152,100 @@ __device__ __forceinline__ float group_sum(float s, int lpr) {
   return s;
 }
 
+// 16-bit rows of at most 16 chunks per lane group (CH <= 2): each wave takes groups of kRowU row sets (rpw
+// rows each, contiguous), the next group's chunks loading while the current one is normalized, with
+// range-checked buffer loads and stores and no branches, so the loop never drains its stores
+#ifndef OOPS_ROW_U
+#define OOPS_ROW_U 4
+#endif
+constexpr int kRowU = OOPS_ROW_U;
+template <typename T, int CH>
+__device__ __forceinline__ void row_norm_forward_pipelined(const RowNormArgs& a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lpr = a.lpr, rpw = 64 / lpr;
+  const int sub = lane & (lpr - 1), rw = lane / lpr;
+  const int W = a.width;
+  constexpr int U = kRowU / CH;
+  float wv[CH][8], bv[CH][8];
+  load_affine<CH>(a.w, 1.f, W, lpr, sub, wv);
+  load_affine<CH>(a.b, 0.f, W, lpr, sub, bv);
+  const int64_t gsize = (int64_t)U * rpw;  // rows per group
+  const int64_t gstep = (int64_t)gridDim.x * 4 * gsize;
+  auto group_rows = [&](int64_t base) {
+    const int64_t left = a.rows - base;
+    return (int)(left < 0 ? 0 : left < gsize ? left : gsize);
+  };
+  auto load_group = [&](int64_t base, uint4 (&raw)[U][CH]) {
+    const int n = group_rows(base);
+    const __amdgpu_buffer_rsrc_t xr =
+        make_rsrc(static_cast<const T*>(a.x) + (n ? base : 0) * a.x_row, (uint32_t)((int64_t)n * a.x_row * 2));
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int r = u * rpw + rw, col = (c * lpr + sub) * 8;
+        raw[u][c] = buffer_load16(xr, r < n && col < W ? (uint32_t)((r * a.x_row + col) * 2) : kOut);
+      }
+  };
+  int64_t base = ((int64_t)blockIdx.x * 4 + wave) * gsize;
+  uint4 raw[U][CH];
+  load_group(base, raw);
+  for (; base < a.rows; base += gstep) {
+    uint4 cur[U][CH];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int c = 0; c < CH; ++c) cur[u][c] = raw[u][c];
+    load_group(base + gstep, raw);  // the next group (out of range past the rows: no request)
+    const int n = group_rows(base);
+    const __amdgpu_buffer_rsrc_t yr =
+        make_rsrc(static_cast<T*>(a.y) + base * a.y_row, (uint32_t)((int64_t)n * a.y_row * 2));
+    const __amdgpu_buffer_rsrc_t mr = make_rsrc(a.mean + base, (uint32_t)(n * 4));
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.rstd + base, (uint32_t)(n * 4));
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int r = u * rpw + rw;
+      float x[CH][8];
+#pragma unroll
+      for (int c = 0; c < CH; ++c) unpack8<T>(cur[u][c], x[c]);
+      float s = 0.f;
+#pragma unroll
+      for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += x[c][e];
+      const float mean = group_sum(s, lpr) / (float)W;
+      float q = 0.f;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int col = (c * lpr + sub) * 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = col + e < W ? x[c][e] - mean : 0.f;
+          q += d * d;
+        }
+      }
+      const float rstd = rsqrtf(group_sum(q, lpr) / (float)W + a.eps);
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int col = (c * lpr + sub) * 8;
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = col + e < W ? (x[c][e] - mean) * rstd * wv[c][e] + bv[c][e] : 0.f;
+        buffer_store16(yr, r < n && col < a.y_row ? (uint32_t)((r * a.y_row + col) * 2) : kOut, pack8<T>(o));
+      }
+      const uint32_t so = r < n && sub == 0 ? (uint32_t)(r * 4) : kOut;
+      buffer_store4(mr, so, mean);
+      buffer_store4(sr, so, rstd);
+    }
+  }
+}
+
 template <typename T, int CH, bool VEC>
 __global__ __launch_bounds__(256) void row_norm_forward_kernel(RowNormArgs a) {
+  if constexpr (VEC && sizeof(T) == 2 && CH <= 2) {
+    row_norm_forward_pipelined<T, CH>(a);
+    return;
+  }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lpr = a.lpr, rpw = 64 / lpr;
   const int sub = lane & (lpr - 1), rw = lane / lpr;
@@ -2070,7 +2162,9 @@ RowPlan row_plan(const oops_row_norm_geometry& g, bool backward, const void* con
   for (int i = 0; i < nptr; ++i)
     if (ptrs[i] && reinterpret_cast<uintptr_t>(ptrs[i]) % 16 != 0) vec = false;
   const int rpw = 64 / lpr;
-  int64_t blocks = (g.rows + 4 * rpw - 1) / (4 * rpw);
+  // the pipelined forward (16-bit rows, vector layout, CH <= 2) takes kRowU / CH row sets per wave and step
+  const int per_wave = !backward && vec && g.dtype != OOPS_F32 && ch <= 2 ? rpw * (kRowU / ch) : rpw;
+  int64_t blocks = (g.rows + 4 * per_wave - 1) / (4 * per_wave);
   if (blocks > 1024) blocks = 1024;  // both kernels walk the rows with a bounded grid
   return {lpr, ch, (int)blocks, vec};
 }
