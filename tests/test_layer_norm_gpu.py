@@ -39,7 +39,7 @@ _CASES = [(d, a) for d in (torch.float32, torch.bfloat16, torch.float16) for a i
 
 
 @pytest.mark.parametrize("dtype,affine", _CASES)
-@pytest.mark.parametrize("width", [1, 17, 128, 384, 4096, 8192])
+@pytest.mark.parametrize("width", [1, 17, 128, 384, 1024, 4096, 8192])
 def test_layer_norm(dtype, width, affine):
     g = torch.Generator().manual_seed(width)
     rows = 3000 if width <= 384 else 200
