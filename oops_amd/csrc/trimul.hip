@@ -2264,7 +2264,9 @@ FactorPlan factor_plan(const oops_trimul_geometry& g, bool backward) {
   FactorPlan pl{};
   // 16-token blocks within one group: the straight-line kernel, W whole in LDS.  Otherwise the
   // backward's epilogue holds more live values: the streaming form keeps it under 256 VGPRs
-  pl.v16 = g.positions % 16 == 0 && g.c_row <= kFullWMaxK;
+  // (its range-checked resources take 32-bit sizes: two groups of the factor layout, and the mask)
+  pl.v16 = g.positions % 16 == 0 && g.c_row <= kFullWMaxK && (int64_t)4 * g.hidden * g.positions < (int64_t(1) << 31) &&
+           g.groups * g.positions * 4 < (int64_t(1) << 31);
   pl.fullw = g.c_row <= kFullWMaxK && (!backward || pl.v16);
   const int64_t wgs = backward || !pl.v16 ? OOPS_FACTOR_WGS : OOPS_FACTOR_FWD_WGS;
   pl.tpw = pl.fullw ? (int)std::max<int64_t>(1, (token_tiles * 2 * cblocks + wgs - 1) / wgs) : 1;
