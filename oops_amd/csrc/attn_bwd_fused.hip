@@ -376,7 +376,10 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
         dma_stage(g + ahead / NS, std::integral_constant<int, ahead % NS>{}, ring_lds[as][wave]);
       }
 
-      // ---- compute this stage
+      // ---- compute this stage, unless its query tile is past Lq (a ghost step of a shorter sample: its
+      // zero Q, dO, pack and bias contribute nothing).  Wave-uniform; the loads above run either way, so
+      // the wait counts stay the same, and the other wave on the SIMD runs its step alone meanwhile
+      if (i * 8 + wave < nqt) {
       const T* qt_ = reinterpret_cast<const T*>(cur.q);
       const T* dt_ = reinterpret_cast<const T*>(cur.d);
       f32x16 sacc = *reinterpret_cast<const f32x16*>(&cur.ld[g2 * 16]);
@@ -408,6 +411,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
         const int at = (16 * m) * 32;
         dv = E::mma(lds_read_tr_frag_sw<T>(dt_ + at, trl), pf, dv);
         dk = E::mma(lds_read_tr_frag_sw<T>(qt_ + at, trl), sf, dk);
+      }
       }
       if constexpr (NS != 3) slot = slot == 2 ? 0 : slot + 1;
     };
