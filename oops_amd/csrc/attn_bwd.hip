@@ -700,15 +700,29 @@ __global__ __launch_bounds__(256) void attn_dbias_reduce_kernel(BwdArgs a) {
   const int64_t e = tile * 256 + threadIdx.x;
   const int64_t Lk = S.Lk, Lq = S.Lq;
   if (e >= H * Lq * Lk) return;
-  const int64_t key = e % Lk;
-  const int64_t q = (e / Lk) % Lq;
-  const int64_t h = e / (Lk * Lq);
-  const int64_t off = S.db_off + h * S.db_sh + q * S.db_si + key;
+  // a contiguous [h][q][k] slab (the usual case) needs no index arithmetic
+  int64_t off = S.db_off + e;
+  if (S.db_si != Lk || S.db_sh != Lq * Lk) {
+    const int64_t key = e % Lk;
+    const int64_t q = (e / Lk) % Lq;
+    const int64_t h = e / (Lk * Lq);
+    off = S.db_off + h * S.db_sh + q * S.db_si + key;
+  }
   // per-sample parts (fast path): a sample with one part wrote dBias directly
   const int parts = a.part_groups > 0 ? parts_for(S.G, a.part_groups, a.parts) : a.parts;
   if (parts < 2) return;
+  // the parts in order, eight loads in flight at a time
+  const float* src = a.dbias_part + off;
   float acc = 0.0f;
-  for (int p = 0; p < parts; ++p) acc += a.dbias_part[(int64_t)p * a.dbias_extent + off];
+  int p = 0;
+  for (; p + 8 <= parts; p += 8) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = src[(int64_t)(p + j) * a.dbias_extent];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc += v[j];
+  }
+  for (; p < parts; ++p) acc += src[(int64_t)p * a.dbias_extent];
   a.dbias[off] = acc;
 }
 
