@@ -4,8 +4,9 @@ One "step" = forward + backward (dQ, dK, dV, dBias) of ``oops_amd.triangle_atten
 q, k, v ``randn(1, 768, 768, 4, 32)`` bf16 passed as ``.transpose(1, 2)``
 views (ending node, swapped pair axes, read in place), bias ``randn(1, 1, 4, 768, 768)`` bf16
 shared over rows, no mask, upstream gradient ``randn`` in the output's layout.  Inputs are
-resident in HBM before timing.  Algorithmic FLOPs per step = 14 * H * c * N^3 (flash
-convention, BASELINE.md).
+resident in HBM before timing.  Algorithmic FLOPs per step = 14 * H * c * N^3 (the flash
+attention convention: seven N x N x c products per row and head, two forward (QK^T, PV) and five
+backward (QK^T again, dO V^T, P^T dO, dS K, dS^T Q), 2 * H * c * N^3 each).
 
 Prints ONE JSON line with the driver's contract fields plus ``roofline`` (dominant kernel,
 timed live with HIP events on the launch stream) and ``cpu_baseline`` (the numpy oracle on
@@ -680,7 +681,7 @@ def main():
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(
             "bench.py measures one GPU only: this build has no multi-GPU path "
-            "(rows shard independently; see DESIGN.md). Run with --gpus 1.",
+            "(rows shard independently across GPUs; one GPU's share is what this measures). Run with --gpus 1.",
             file=sys.stderr,
         )
         sys.exit(2)
