@@ -708,8 +708,11 @@ __global__ __launch_bounds__(256) void attn_dbias_reduce_kernel(BwdArgs a) {
     const int64_t h = e / (Lk * Lq);
     off = S.db_off + h * S.db_sh + q * S.db_si + key;
   }
-  // per-sample parts (fast path): a sample with one part wrote dBias directly
-  const int parts = a.part_groups > 0 ? parts_for(S.G, a.part_groups, a.parts) : a.parts;
+  // per-sample parts (fast path): a sample with one part wrote dBias directly.  In a split batch the
+  // samples longer than fused_max_lq had the separate dBias kernel and its parts
+  const int parts = a.fused_max_lq > 0 && S.Lq > a.fused_max_lq ? parts_for(S.G, a.part_groups_rest, a.parts_rest)
+                    : a.part_groups > 0                        ? parts_for(S.G, a.part_groups, a.parts)
+                                                               : a.parts;
   if (parts < 2) return;
   // the parts in order, eight loads in flight at a time
   const float* src = a.dbias_part + off;
@@ -798,9 +801,17 @@ hipError_t launch_backward(const oops_attn_geometry& geo, const Plan& plan, cons
                        a.dbias != nullptr;
     if (fused) {
       if (err == hipSuccess) err = launch_dkvb_fused(geo, plan, L, stream);
+      // a split batch: the samples too long for the fused kernel take the separate kernels
+      if (plan.fused_split) {
+        if (err == hipSuccess) err = launch_dkv_fast(geo, plan, L, stream, true);
+        if (err == hipSuccess) err = launch_dbias_fast(geo, plan, L, stream, true);
+        a.fused_max_lq = kFusedMaxLen;
+        a.parts_rest = plan.fast_parts;
+        a.part_groups_rest = plan.fast_part_groups;
+      }
       a.parts = plan.fused_parts;
       a.part_groups = plan.fused_part_groups;
-      if (a.parts > 1) {
+      if (a.parts > 1 || (plan.fused_split && plan.fast_parts > 1)) {
         a.uniform_tiles = plan.sred_uniform;
         hipLaunchKernelGGL((attn_dbias_reduce_kernel<T, BT, DP>), dim3((unsigned)plan.sred_tiles), block, 0,
                            stream, a);

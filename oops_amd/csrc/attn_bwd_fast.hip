@@ -52,8 +52,10 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
   if (tile >= a.total_tiles) return;
   const Sample* tab = reinterpret_cast<const Sample*>(a.table);
   const int H = a.num_heads;
-  const int s_idx = find_sample(tile, tab, a.num_samples, a.uniform_tiles,
-                                [&](const Sample& s) { return cdiv(s.G, R) * H * cdiv(s.Lk, 128); });
+  // (a split batch: the samples the fused dK/dV + dBias kernel does not serve)
+  const int s_idx = find_sample(tile, tab, a.num_samples, a.uniform_tiles, [&](const Sample& s) {
+    return a.fused_max_lq > 0 && s.Lq <= a.fused_max_lq ? (int64_t)0 : cdiv(s.G, R) * H * cdiv(s.Lk, 128);
+  });
   if (s_idx < 0) return;
   const Sample& S = tab[__builtin_amdgcn_readfirstlane(s_idx)];
   const int64_t G = S.G;
@@ -402,7 +404,7 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS> ? 4 : O
     }
     if constexpr (DP == kCompactRow) {
       // compact copies of these Q and dO rows for the fused dK/dV + dBias kernel
-      if (a.qc != nullptr) {
+      if (a.qc != nullptr && (a.fused_max_lq == 0 || Lq <= a.fused_max_lq)) {
         const int64_t row0 = S.l_off + ((int64_t)g * H + h) * Lq + q0w;
 #pragma unroll
         for (int i = 0; i < NQR; ++i)
@@ -711,7 +713,7 @@ __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(Bw
   const Sample* tab = reinterpret_cast<const Sample*>(a.table);
   const int H = a.num_heads;
   const int s_idx = find_sample(tile, tab, a.num_samples, a.uniform_tiles, [&](const Sample& s) {
-    return s.bias_mode == OOPS_BIAS_SHARED
+    return s.bias_mode == OOPS_BIAS_SHARED && !(a.fused_max_lq > 0 && s.Lq <= a.fused_max_lq)
                ? H * cdiv(s.Lq, 128) * cdiv(s.Lk, 64) * parts_for(s.G, a.part_groups, a.parts)
                : (int64_t)0;
   });
@@ -986,7 +988,8 @@ hipError_t dispatch_fast(const oops_attn_geometry& geo, const Plan& plan, F&& f)
   return err;
 }
 
-hipError_t launch_dkv_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L, hipStream_t stream) {
+hipError_t launch_dkv_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L, hipStream_t stream,
+                           bool rest) {
   return dispatch_fast(geo, plan, [&](auto tag, auto dpc) {
     using T = typename decltype(tag)::type;
     constexpr int DP = decltype(dpc)::value;
@@ -994,9 +997,15 @@ hipError_t launch_dkv_fast(const oops_attn_geometry& geo, const Plan& plan, cons
     fill_bwd_args(a, geo, plan, L);
     // OOPS_DKV_ROWS=2: two rows per workgroup share each bias fragment (row-shared
     // biases only); it costs a wave of occupancy and measured slower at the headline shape
-    const bool pair = OOPS_DKV_ROWS == 2 && a.bias != nullptr && !plan.any_full && plan.dkv_tiles_r2 > 0;
+    const bool pair = !rest && OOPS_DKV_ROWS == 2 && a.bias != nullptr && !plan.any_full && plan.dkv_tiles_r2 > 0;
     a.uniform_tiles = pair ? plan.dkv_uniform_r2 : plan.dkv_uniform;
     a.total_tiles = pair ? plan.dkv_tiles_r2 : plan.dkv_tiles;
+    if (rest) {
+      a.fused_max_lq = kFusedMaxLen;
+      a.uniform_tiles = 0;
+      a.total_tiles = plan.dkv_rest_tiles;
+    }
+    if (a.total_tiles == 0) return hipSuccess;
     const dim3 grid((unsigned)xcd_grid(a.total_tiles, xcd_chunk(a.uniform_tiles)));
     if (pair)
       hipLaunchKernelGGL((attn_dkv_fast_kernel<T, DP, true, 2>), grid, dim3(256), 0, stream, a);
@@ -1018,6 +1027,8 @@ hipError_t launch_dq_fast(const oops_attn_geometry& geo, const Plan& plan, const
     a.uniform_tiles = plan.fwd_uniform;
     a.total_tiles = plan.fwd_tiles;
     a.delta_in_dq = delta_in_dq ? 1 : 0;
+    // a split batch: compact copies only of the rows the fused kernel reads
+    a.fused_max_lq = L.qc != nullptr && plan.fused_split ? kFusedMaxLen : 0;
     const dim3 grid((unsigned)xcd_grid(plan.fwd_tiles, xcd_chunk(plan.fwd_uniform)));
     const bool full = a.dbias != nullptr && plan.any_full;
     auto go = [&](auto has_bias, auto masked, auto full_db) {
@@ -1040,7 +1051,7 @@ hipError_t launch_dq_fast(const oops_attn_geometry& geo, const Plan& plan, const
 }
 
 hipError_t launch_dbias_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L,
-                             hipStream_t stream) {
+                             hipStream_t stream, bool rest) {
   return dispatch_fast(geo, plan, [&](auto tag, auto dpc) {
     using T = typename decltype(tag)::type;
     constexpr int DP = decltype(dpc)::value;
@@ -1048,9 +1059,11 @@ hipError_t launch_dbias_fast(const oops_attn_geometry& geo, const Plan& plan, co
     fill_bwd_args(a, geo, plan, L);
     a.parts = plan.fast_parts;
     a.part_groups = plan.fast_part_groups;
-    a.uniform_tiles = plan.fast_sbias_uniform;
-    a.total_tiles = plan.fast_sbias_tiles;
-    const dim3 grid((unsigned)xcd_grid(plan.fast_sbias_tiles, xcd_chunk(plan.fast_sbias_uniform)));
+    a.uniform_tiles = rest ? 0 : plan.fast_sbias_uniform;
+    a.total_tiles = rest ? plan.fast_sbias_rest_tiles : plan.fast_sbias_tiles;
+    if (rest) a.fused_max_lq = kFusedMaxLen;
+    if (a.total_tiles == 0) return hipSuccess;
+    const dim3 grid((unsigned)xcd_grid(a.total_tiles, xcd_chunk(a.uniform_tiles)));
     if (plan.masked_tiles)
       hipLaunchKernelGGL((attn_dbias_fast_kernel<T, DP, true>), grid, dim3(256), 0, stream, a);
     else

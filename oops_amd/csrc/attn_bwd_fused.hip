@@ -51,6 +51,7 @@ namespace {
 constexpr int kFusedWaves = 8;
 constexpr int kFusedMaxSteps = 3;  // query tiles per wave: Lq <= 8 * 3 * 32
 constexpr int kFusedMaxQT = kFusedWaves * kFusedMaxSteps;  // query tiles of the largest bias region
+static_assert(kFusedMaxQT * 32 == kFusedMaxLen, "the plan's length limit is the kernel's");
 constexpr int kQT = 32 * 32;       // elements of one 32 x 32 tile
 
 // 4 bytes per lane into 64 consecutive dwords at lds.  Every load of the
@@ -125,7 +126,9 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   const Sample* tab = reinterpret_cast<const Sample*>(a.table);
   const int H = a.num_heads;
   const int s_idx = find_sample(tile, tab, a.num_samples, a.uniform_tiles, [&](const Sample& s) {
-    return (int64_t)H * cdiv(s.Lk, 32) * parts_for(s.G, a.part_groups, a.parts);
+    // (a split batch: only the samples this kernel serves)
+    return a.fused_max_lq == 0 || s.Lq <= a.fused_max_lq ? (int64_t)H * cdiv(s.Lk, 32) * parts_for(s.G, a.part_groups, a.parts)
+                                                          : (int64_t)0;
   });
   if (s_idx < 0) return;
   const Sample& S = tab[__builtin_amdgcn_readfirstlane(s_idx)];
@@ -454,7 +457,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
 
 bool dkvb_fused_ok(const oops_attn_geometry& geo, const Plan& plan) {
   return geo.force_generic == 0 && fast_path_ok(geo, plan) && plan.dp == kCompactRow && plan.all_shared &&
-         plan.bias_frag && plan.max_len_q <= kFusedWaves * kFusedMaxSteps * 32 && plan.fused_tiles > 0;
+         plan.bias_frag && plan.fused_max_len_q > 0 && plan.fused_max_len_q <= kFusedMaxLen && plan.fused_tiles > 0;
 }
 
 hipError_t launch_dkvb_fused(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L,
@@ -469,7 +472,8 @@ hipError_t launch_dkvb_fused(const oops_attn_geometry& geo, const Plan& plan, co
     a.total_tiles = plan.fused_tiles;
     const dim3 grid((unsigned)xcd_grid(plan.fused_tiles, xcd_chunk(plan.fused_uniform)));
     // query tiles per wave and group: that of the longest sample
-    const int ns = (int)((plan.max_len_q + 32 * kFusedWaves - 1) / (32 * kFusedWaves));
+    a.fused_max_lq = plan.fused_split ? kFusedMaxLen : 0;
+    const int ns = (int)((plan.fused_max_len_q + 32 * kFusedWaves - 1) / (32 * kFusedWaves));
     auto run = [&](auto masked, auto nsc) {
       hipLaunchKernelGGL((attn_dkvb_fast_kernel<T, decltype(masked)::value, decltype(nsc)::value>), grid, dim3(512),
                          0, stream, a);

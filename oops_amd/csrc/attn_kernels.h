@@ -64,6 +64,12 @@ struct BwdArgsT {
   int vec_ok;
   int parts;
   int64_t part_groups;  // > 0: per-sample parts, parts_for(G, part_groups, parts) (fast dBias)
+  // > 0: a batch split between the fused dK/dV + dBias kernel (samples with Lq <= fused_max_lq) and the
+  // separate dK/dV and dBias kernels (the longer ones); each kernel skips the other's samples, and the dBias
+  // reduction takes a longer sample's parts from parts_rest / part_groups_rest
+  int fused_max_lq;
+  int parts_rest;
+  int64_t part_groups_rest;
   int head_group;
   float scale;
   const T* bias_frag;        // as in FwdArgsT
@@ -123,6 +129,9 @@ inline bool dispatch_config(int dtype, int bias_dtype, int dp, F&& f) {
   return false;
 }
 
+// longest sample (Lq) the fused dK/dV + dBias kernel serves: 8 waves x 3 query tiles of 32
+constexpr int kFusedMaxLen = 768;
+
 // Host-side launch plan derived from the geometry table.
 struct Plan {
   int dp = 0;
@@ -144,6 +153,9 @@ struct Plan {
   int64_t fused_tiles = 0, fused_uniform = 0;
   int fused_parts = 1;
   int64_t fused_part_groups = 1;
+  int64_t fused_max_len_q = 0;                   // longest sample the fused kernel serves
+  bool fused_split = false;                      // some samples too long for it: separate kernels for those
+  int64_t dkv_rest_tiles = 0, fast_sbias_rest_tiles = 0;  // the separate kernels' tiles of those samples
   bool any_pair_mask = false;                    // a mask that depends on the query
   bool masked_tiles = false;                     // some 64-key tile has masked or out-of-range keys
   bool offsets_32bit = true;                     // every per-(group, head) K/V/bias block < 2 GiB
@@ -218,6 +230,9 @@ inline void fill_bwd_args(BwdArgsT<T, BT>& a, const oops_attn_geometry& geo, con
   a.vec_ok = geo.vec_ok;
   a.parts = plan.parts;
   a.part_groups = 0;
+  a.fused_max_lq = 0;
+  a.parts_rest = 1;
+  a.part_groups_rest = 0;
   a.head_group = head_group_of(geo);
   a.scale = geo.scale;
   a.bias_frag = static_cast<const T*>(L.bias_frag);
@@ -228,7 +243,9 @@ inline void fill_bwd_args(BwdArgsT<T, BT>& a, const oops_attn_geometry& geo, con
 }
 
 bool backward_fast_ok(const oops_attn_geometry& geo, const Plan& plan);
-hipError_t launch_dkv_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L, hipStream_t stream);
+// rest: only the samples of a split batch that the fused dK/dV + dBias kernel does not serve
+hipError_t launch_dkv_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L, hipStream_t stream,
+                           bool rest = false);
 // delta_in_dq: the kernel computes delta = rowsum((O + O_lo) * dO) itself and stores it for the
 // later kernels (no separate delta pass)
 hipError_t launch_dq_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L, bool delta_in_dq,
@@ -239,7 +256,7 @@ bool dkvb_fused_ok(const oops_attn_geometry& geo, const Plan& plan);
 hipError_t launch_dkvb_fused(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L,
                              hipStream_t stream);
 hipError_t launch_dbias_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L,
-                             hipStream_t stream);
+                             hipStream_t stream, bool rest = false);
 
 hipError_t launch_backward(const oops_attn_geometry& geo, const Plan& plan, const void* q, const void* k,
                            const void* v, const uint8_t* mask, const void* bias, const void* out,

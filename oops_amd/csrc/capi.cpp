@@ -181,28 +181,38 @@ int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
     plan.sred_uniform = u_red && c_red > 0 ? c_red : 0;
     // fused dK/dV + dBias kernel: one workgroup per (head, 32-key block, part),
     // about kTargetFusedBlocks workgroups (whole rounds of one per CU)
+    // (samples longer than kFusedMaxLen take the separate dK/dV and dBias kernels: a split batch)
     plan.all_shared = geo->has_bias != 0;
     int64_t fused_units = 0;
     for (int s = 0; s < geo->num_samples; ++s) {
       const Sample& S = tab[s];
       if (S.bias_mode != OOPS_BIAS_SHARED || S.b_off < 0) plan.all_shared = false;
-      fused_units += H * cdiv(S.Lk, 32) * S.G;
+      if (S.Lq <= oops::kFusedMaxLen) fused_units += H * cdiv(S.Lk, 32) * S.G;
     }
     if (plan.all_shared) {
       plan.fused_part_groups = std::max<int64_t>(cdiv(fused_units, kTargetFusedBlocks), kMinFusedPartGroups);
       int64_t c_fu = -1;
-      bool u_fu = true;
+      bool u_fu = true, rest = false;
       for (int s = 0; s < geo->num_samples; ++s) {
         const Sample& S = tab[s];
+        if (S.Lq > oops::kFusedMaxLen) {
+          rest = true;
+          plan.dkv_rest_tiles += S.G * H * cdiv(S.Lk, 128);
+          plan.fast_sbias_rest_tiles +=
+              H * cdiv(S.Lq, 128) * cdiv(S.Lk, 64) * oops::parts_for(S.G, plan.fast_part_groups, kMaxParts);
+          continue;
+        }
         const int p = oops::parts_for(S.G, plan.fused_part_groups, kMaxParts);
         const int64_t c = H * cdiv(S.Lk, 32) * p;
         plan.fused_parts = std::max(plan.fused_parts, p);
         plan.fused_tiles += c;
+        plan.fused_max_len_q = std::max(plan.fused_max_len_q, S.Lq);
         track(c, c_fu, u_fu);
       }
-      plan.fused_uniform = u_fu && c_fu > 0 ? c_fu : 0;
+      plan.fused_uniform = u_fu && !rest && c_fu > 0 ? c_fu : 0;
       // not served by the fused kernel (16-bit, head size <= 32 only)
       if (plan.fused_tiles > kMaxGrid || geo->dtype == OOPS_F32 || plan.dp != 32) plan.fused_tiles = 0;
+      plan.fused_split = rest && plan.fused_tiles > 0;
     }
     if (plan.sbias_tiles > kMaxGrid || plan.fast_sbias_tiles > kMaxGrid || plan.sred_tiles > kMaxGrid)
       return fail(OOPS_EINVAL, "dBias launch grid exceeds 2^31-1 workgroups");
