@@ -313,7 +313,7 @@ int oops_trimul_output_backward(const oops_trimul_geometry* geo, const void* nor
  * OOPS_SUM_MAX_SEGMENTS such arrays:
  *   out[j] = sum over p = 0 .. count-1 of parts[p * part_stride + j],  j < n,
  * in a fixed order (bit-identical on every call), rounded once to out_dtype.
- * Arrays of more than 64 rows are summed in two launches through the caller's
+ * Arrays of more than 256 rows are summed in two launches through the caller's
  * workspace (float32 chunk sums, 256-byte aligned, of
  * oops_sum_partials_workspace_bytes bytes; NULL when that is 0). */
 #define OOPS_SUM_MAX_SEGMENTS 16

@@ -21,7 +21,7 @@ _OUT_DTYPE = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16:
 class PartialSums:
     """``add`` registers ``parts`` (P, *shape) float32 and returns the (still unwritten) ``shape`` result in
     ``dtype`` (or in the given contiguous ``out``); ``run`` sums every registered array (one launch per
-    SUM_MAX_SEGMENTS arrays, two when an array has more than 64 rows)."""
+    SUM_MAX_SEGMENTS arrays, two when an array has more than 256 rows)."""
 
     def __init__(self) -> None:
         self._segs: list[tuple[Tensor, Tensor]] = []

@@ -20,7 +20,7 @@ namespace {
 
 constexpr int kSumCols = 64;
 constexpr int kSumSlices = 4;
-constexpr int64_t kChunkParts = 64;  // rows one workgroup sums
+constexpr int64_t kChunkParts = 256;  // rows one workgroup sums (more: two launches)
 
 struct SumJob {
   const float* parts;

@@ -235,7 +235,7 @@ def test_sum_partials_validates_on_the_host(lib):
     seg.out_dtype, seg.out = _lib.BF16, None
     assert lib.oops_sum_partials(segs, 1, None, 0, None) != 0
     assert b"non-NULL" in lib.oops_last_error()
-    seg.out, seg.count = 16, 65  # more than 64 rows: a workspace of 2 chunk rows
+    seg.out, seg.count = 16, 257  # more than 256 rows: a workspace of 2 chunk rows
     assert lib.oops_sum_partials_workspace_bytes(segs, 1) == 256
     assert lib.oops_sum_partials(segs, 1, None, 0, None) != 0
     assert b"workspace" in lib.oops_last_error()

@@ -15,7 +15,7 @@ DEV = "cuda"
 
 
 def quarter_sum(rows: np.ndarray) -> np.ndarray:
-    """float32 sum of up to 64 rows in the kernel's order: slice s sums the s-th quarter of the rows in
+    """float32 sum of up to 256 rows in the kernel's order: slice s sums the s-th quarter of the rows in
     order (quarters of ceil(rows / 4)), then (s0 + s1) + (s2 + s3)."""
 
     count, n = rows.shape
@@ -30,16 +30,17 @@ def quarter_sum(rows: np.ndarray) -> np.ndarray:
 
 
 def fixed_order_sum(parts: np.ndarray) -> np.ndarray:
-    """Up to 64 rows: one quarter_sum; more: quarter_sum of each 64-row chunk, then of the chunk sums."""
+    """Up to 256 rows: one quarter_sum; more: quarter_sum of each 256-row chunk, then of the chunk sums."""
 
-    if parts.shape[0] <= 64:
+    if parts.shape[0] <= 256:
         return quarter_sum(parts)
-    chunks = np.stack([quarter_sum(parts[c : c + 64]) for c in range(0, parts.shape[0], 64)])
+    chunks = np.stack([quarter_sum(parts[c : c + 256]) for c in range(0, parts.shape[0], 256)])
     return quarter_sum(chunks)
 
 
 @pytest.mark.parametrize(
-    "count,n", [(0, 7), (1, 5), (5, 64), (7, 1000), (64, 65536 * 2 + 3), (65, 33), (2048, 70), (8193, 130)]
+    "count,n", [(0, 7), (1, 5), (5, 64), (7, 1000), (64, 65536 * 2 + 3), (65, 33), (256, 40), (257, 33), (2048, 70),
+                (8193, 130)]
 )
 def test_sum_partials_matches_the_fixed_order(count, n):
     g = torch.Generator().manual_seed(count * 7 + n)
