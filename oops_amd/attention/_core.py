@@ -87,6 +87,25 @@ class separate_dkv_dbias:
         return False
 
 
+_DBIAS_SINK: Optional[list] = None
+
+
+class capture_dbias_f32:
+    """Context manager collecting each backward's float32 dBias (the kernels' output, before the
+    cast to the bias dtype) in ``.values``, in call order (accuracy reporting and tests)."""
+
+    def __enter__(self):
+        global _DBIAS_SINK
+        self.saved, _DBIAS_SINK = _DBIAS_SINK, []
+        self.values = _DBIAS_SINK
+        return self
+
+    def __exit__(self, *exc):
+        global _DBIAS_SINK
+        _DBIAS_SINK = self.saved
+        return False
+
+
 # ----------------------------------------------------------------- tables
 
 class _TableCache:
@@ -403,6 +422,8 @@ def _backward(ctx, dout, dout_lo, dlse):
         [bool(need_q), bool(need_k), bool(need_v), need_b],
     )
     grad_bias = dbias.view(ctx.bias_shape).to(ctx.bias_dtype) if need_b else None
+    if need_b and _DBIAS_SINK is not None:
+        _DBIAS_SINK.append(dbias.view(ctx.bias_shape))
     return (
         dq if need_q else None,
         dk if need_k else None,

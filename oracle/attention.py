@@ -265,3 +265,26 @@ def pair_bias_attention_backward(q, k, v, dout, mask=None, bias=None, scale=None
             if size == 1 and db.shape[axis] != 1:
                 db = db.sum(axis=axis, keepdims=True)
     return dq, dk, dv, db
+
+
+def shared_dbias_at(q, k, v, dout, mask=None, bias=None, qpos=None, scale=None, *, rows_per_chunk=32,
+                    dtype=np.float64):
+    """Row-shared dBias ``(H, len(qpos), K)`` of head-major pair-bias attention ``(S, H, Q, D)`` at the
+    query positions ``qpos`` (all when None), summed over all S rows, chunked over rows.
+
+    Queries are independent (each is one softmax over the keys), so restricting them is exact: this is
+    ``pair_bias_attention_backward(...)[3][0][:, qpos]`` at a fraction of its memory.  ``mask`` is a
+    key mask ``(S, K)`` or None; ``bias`` is ``(1, H, Q, K)``.
+    """
+
+    S, H, Q, D = np.shape(q)
+    qpos = np.arange(Q) if qpos is None else np.asarray(qpos)
+    b = None if bias is None else np.asarray(bias)[:, :, qpos]
+    acc = np.zeros((H, len(qpos), np.shape(k)[-2]), dtype=dtype)
+    for r0 in range(0, S, rows_per_chunk):
+        sl = slice(r0, min(S, r0 + rows_per_chunk))
+        m = None if mask is None else np.asarray(mask)[sl]
+        *_, db = pair_bias_attention_backward(np.asarray(q)[sl][:, :, qpos], np.asarray(k)[sl], np.asarray(v)[sl],
+                                              np.asarray(dout)[sl][:, :, qpos], m, b, scale, dtype=dtype)
+        acc += db[0]
+    return acc

@@ -172,6 +172,25 @@ def test_pair_bias_vs_sdpa(mask_kind):
         np.testing.assert_allclose(mine, theirs.numpy(), atol=1e-11)
 
 
+def test_shared_dbias_at_vs_sdpa():
+    """The chunked query-subset dBias the full-size GPU tests use equals SDPA autograd's bias gradient
+    (bias broadcast over the rows, key mask) restricted to those queries."""
+
+    rng = np.random.default_rng(17)
+    S, H, Q, D = 9, 2, 12, 4
+    q, k, v, do = (_rand(rng, S, H, Q, D) for _ in range(4))
+    bias = _rand(rng, 1, H, Q, Q)
+    mask = rng.random((S, Q)) > 0.3
+    mask[:, 0] = True
+    qpos = [0, 5, 11, 7]
+    got = ora.shared_dbias_at(q, k, v, do, mask, bias, qpos, rows_per_chunk=4)
+    tq, tk, tv, tb = (torch.tensor(x, requires_grad=True) for x in (q, k, v, bias))
+    attn = tb.expand(S, H, Q, Q).masked_fill(~torch.tensor(mask)[:, None, None, :], float("-inf"))
+    ref = F.scaled_dot_product_attention(tq, tk, tv, attn_mask=attn)
+    (tgb,) = torch.autograd.grad(ref, (tb,), torch.tensor(do))
+    np.testing.assert_allclose(got, tgb.numpy()[0][:, qpos], atol=1e-11)
+
+
 # ------------------------------------------------------------------ gate oracle
 
 

@@ -193,7 +193,8 @@ def test_autocast_float32_bias():
 def test_config_c4_msa_rows():
     """BASELINE config 4 at full size: S=512, H=8, N=384, c=32 bf16, key mask, shared bias (seed 3).
 
-    Groups are independent, so the oracle checks a slice of 16 sequences of the full-size call.
+    Groups are independent, so the oracle checks O, dQ, dK and dV on a slice of 16 sequences of the
+    full-size call; the shared dBias (a sum over all 512 groups) on a query subset over every group.
     """
 
     torch.manual_seed(3)
@@ -216,19 +217,12 @@ def test_config_c4_msa_rows():
     assert_close(gq[sl], dq, torch.bfloat16, "dq")
     assert_close(gk[sl], dk, torch.bfloat16, "dk")
     assert_close(gv[sl], dv, torch.bfloat16, "dv")
-    # dBias sums over all 512 groups: compare with a float32 torch restatement, chunked
-    p_db = torch.zeros(h, n, n, dtype=torch.float64, device=DEV)
-    for c0 in range(0, s, 64):
-        qq, kk, vv, dd = (t.detach()[c0 : c0 + 64].float() for t in (q, k, v, dout))
-        sc = qq @ kk.transpose(-1, -2) * c**-0.5 + bias.detach().float()
-        keep = mask[c0 : c0 + 64, None, None, :]
-        sc = sc.masked_fill(~keep, float("-inf"))
-        p = torch.softmax(sc, -1)
-        o = p @ vv
-        ds = p * (dd @ vv.transpose(-1, -2) - (dd * o).sum(-1, keepdim=True))
-        p_db += ds.sum(0).double()
-    want_db = p_db.cpu().numpy()[None]
-    assert_close(gb, want_db, torch.bfloat16, "dbias")
+    # dBias sums over all 512 groups: the float64 oracle over every group, on 48 query positions spread
+    # over all twelve 32-query tiles (exact for those queries: each is its own softmax)
+    qpos = [32 * t + (7 * j + t) % 32 for t in range(12) for j in range(4)]
+    f32 = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
+    want_db = ora.shared_dbias_at(f32(q), f32(k), f32(v), f32(dout), _np(mask), nb, qpos)
+    assert_close(gb[0][:, qpos], want_db, torch.bfloat16, "dbias")
 
 
 def test_errors():
