@@ -68,7 +68,12 @@ extern "C" {
 #define OOPS_BIAS_FULL 1   /* one bias matrix per group: dBias = dS        */
 #define OOPS_BIAS_SHARED 2 /* one bias matrix for all groups: dBias = sum_g dS */
 
-/* backward phases (oops_attn_geometry.phases); 0 runs all of them */
+/* backward phases (oops_attn_geometry.phases); 0 runs all of them.  Phases are
+ * for timing single kernels.  A call whose phases leave out both DQ and DELTA
+ * but keep DKV and DBIAS, on a geometry the fused dK/dV + dBias kernel serves,
+ * reads the delta/LSE pack and the compact Q/dO copies that an earlier full
+ * call's dQ kernel left in the SAME workspace (same geometry, inputs and
+ * workspace pointer); with any other workspace its dK/dV/dBias are undefined. */
 #define OOPS_PHASE_DELTA 1 /* delta = rowsum(O * dO)                 */
 #define OOPS_PHASE_DQ 2    /* dQ and per-group dBias               */
 #define OOPS_PHASE_DKV 4   /* dK and dV                            */

@@ -54,12 +54,26 @@ constexpr int kFusedMaxQT = kFusedWaves * kFusedMaxSteps;  // query tiles of the
 static_assert(kFusedMaxQT * 32 == kFusedMaxLen, "the plan's length limit is the kernel's");
 constexpr int kQT = 32 * 32;       // elements of one 32 x 32 tile
 
-// 4 bytes per lane into 64 consecutive dwords at lds.  Every load of the
-// main loop goes straight to LDS: none leaves a register waiting for its
-// data, which the compiler, not knowing the load, could copy too early.
-__device__ __forceinline__ void dma4_asm(const u32x4& r, const void* lds, uint32_t voff) {
-  const uint32_t m0 =
-      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(lds));
+// LDS byte address of p (a __shared__ object), as a wave-uniform value: the
+// M0 operand of the direct-to-LDS loads below.  The kernel takes the
+// addresses of its LDS arrays once and steps them with constant offsets.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(p));
+}
+// Direct-to-LDS loads through inline assembly (see dma16_asm): 16, 4 or 1
+// byte(s) per lane into 64 consecutive slots at LDS address m0 (bytes, 1
+// byte into a zero-extended dword).  Every load of the main loop goes
+// straight to LDS: none leaves a register waiting for its data, which the
+// compiler, not knowing the load, could copy too early.
+__device__ __forceinline__ void dma16_m0(const u32x4& r, uint32_t m0, uint32_t voff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0),
+      "v"(voff), "s"(r)
+      : "memory", "m0");
+}
+__device__ __forceinline__ void dma4_m0(const u32x4& r, uint32_t m0, uint32_t voff) {
   asm volatile(
       "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
@@ -67,10 +81,7 @@ __device__ __forceinline__ void dma4_asm(const u32x4& r, const void* lds, uint32
       "v"(voff), "s"(r)
       : "memory", "m0");
 }
-// one byte per lane into a zero-extended dword at lds + 4 lane
-__device__ __forceinline__ void dma_u8_asm(const u32x4& r, const void* lds, uint32_t voff) {
-  const uint32_t m0 =
-      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(lds));
+__device__ __forceinline__ void dma_u8_m0(const u32x4& r, uint32_t m0, uint32_t voff) {
   asm volatile(
       "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
@@ -121,6 +132,14 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   const int lq = lane & 31;
   const int g2 = lane >> 5;
 
+  // LDS byte addresses (M0 of the direct-to-LDS loads): this wave's ring
+  // stage 0 (stage s adds s * kStageStride), its K/V slot, the keep bytes
+  constexpr uint32_t kStageStride = kFusedWaves * sizeof(RingStage);
+  const uint32_t ring_m0 = lds_addr(&ring_lds[0][wave]);
+  const uint32_t kv_m0 = lds_addr(kv_lds) + (uint32_t)((((wave >> 1) & 1) * 32 * 32 + 16 * (wave & 1) * 32) * sizeof(T));
+  const uint32_t keep_m0 = lds_addr(keep_lds);
+  const uint32_t bias_m0 = lds_addr(bias_lds);
+
   int64_t tile = xcd_tile(blockIdx.x, gridDim.x, xcd_chunk(a.uniform_tiles));
   if (tile >= a.total_tiles) return;
   const Sample* tab = reinterpret_cast<const Sample*>(a.table);
@@ -153,7 +172,6 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   const int nqt = (Lq + 31) >> 5;  // <= NS * 8 (the launch picks NS for the longest sample)
   // Q and dO rows come from the dQ kernel's compact copies: row
   // l_off + (g H + h) Lq + q of kCompactRow elements
-  constexpr int q_si = kCompactRow, do_si = kCompactRow;
   const float c1 = a.scale * kLog2e;
   const int key = kb * 32 + lq;  // this lane's key
   const bool has_mask = MASKED && a.mask != nullptr && S.m_off >= 0;
@@ -168,18 +186,22 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   const uint8_t* const m_h = has_mask ? uptr(a.mask + S.m_off) : nullptr;
   const int64_t m_sg = has_mask ? u64(S.m_sg) : 0;
 
-  // ---- per-lane DMA offsets (bytes) of the Q / dO tile rows, from the
-  // tile's first row: load r (0, 1) of a tile covers rows 16 r .. 16 r + 15;
-  // lane l writes slot l = row 16 r + l / 4, physical chunk l % 4, which holds
-  // logical chunk (l % 4) ^ swz(row)
-  uint32_t q_lane_off[2], do_lane_off[2];
+  // ---- per-lane DMA offsets (bytes) of the Q / dO tile rows of step i
+  // (query tile 8 i + wave) within the (g, h) block of the compact copies,
+  // which are the same for Q and dO: load r (0, 1) of a tile covers rows
+  // 16 r .. 16 r + 15; lane l writes slot l = row 16 r + l / 4, physical
+  // chunk l % 4, which holds logical chunk (l % 4) ^ swz(row).  Rows past Lq
+  // (and chunks past D) get an offset past the block's range: they read 0.
+  uint32_t tile_off[NS][2];
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int row = 16 * r + (lane >> 2);
-    const int col = ((lane & 3) ^ swz<32>(row)) * 8;
-    q_lane_off[r] = col < D ? (uint32_t)((row * q_si + col) * 2) : kOut;
-    do_lane_off[r] = col < D ? (uint32_t)((row * do_si + col) * 2) : kOut;
-  }
+  for (int i = 0; i < NS; ++i)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int row = 16 * r + (lane >> 2);
+      const int col = ((lane & 3) ^ swz<32>(row)) * 8;
+      const int q = (8 * i + wave) * 32 + row;
+      tile_off[i][r] = col < D && q < Lq ? (uint32_t)((q * kCompactRow + col) * 2) : kOut;
+    }
   // pack offsets of step i: lane l reads query (8 i + wave) * 32 + ld_q,
   // lanes 32..63 from the -delta half, so that ring position l holds the
   // query the accumulator layout puts there (ld_q inverts perm32); a query
@@ -218,30 +240,33 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   identity_frags<T>(ident, 1.0f / a.scale, lane);
   const TrLane trl = tr_lane<32>(lane, 0);
 
-  // The resource of one Q or dO tile of group g: its rows only, so that rows
-  // past Lq, tiles past Lq and groups past the part read 0 (a row's D
-  // elements lie below the next row's start).
-  auto tile_rsrc = [&](const T* base_h, int64_t sg, int si, int g, int qt) {
-    const bool live = g < g_end && qt < nqt;
-    const int64_t gg = live ? g : g_begin;
-    const int rows = live ? min(32, Lq - qt * 32) : 1;
-    return rsrc_words(base_h + gg * sg + (int64_t)(live ? qt : 0) * 32 * si,
-                      live ? (uint32_t)(((rows - 1) * si + D) * 2) : 0u);
+  // The resources of group g's (g, h) blocks of the compact Q and dO copies
+  // and of the pack, built once per group (the loads of a step differ only in
+  // their per-lane offsets); a group past the part gets empty ranges (reads 0)
+  struct GroupDesc {
+    u32x4 q, d, pk;
   };
-  // stage (group g, step i: query tile 8 i + wave) into ring stage rs: the
-  // pack (1 load) and the Q / dO tiles (4); every stage issues all five
-  auto dma_stage = [&](int g, auto ic, const RingStage& rs) {
-    constexpr int i = decltype(ic)::value;
-    const int qt = 8 * i + wave;
+  const uint32_t qd_bytes = (uint32_t)(((Lq - 1) * kCompactRow + D) * 2);
+  auto group_desc = [&](int g) {
     const bool live = g < g_end;
     const int64_t gg = live ? g : g_begin;
-    dma4_asm(rsrc_words(pk_h + gg * pk_sg, live ? (uint32_t)(Lq * 8) : 0u), rs.ld, ld_off[i]);
-    const u32x4 qr = tile_rsrc(q_h, q_sg, q_si, g, qt);
-    const u32x4 dr = tile_rsrc(do_h, do_sg, do_si, g, qt);
+    GroupDesc gd;
+    gd.q = rsrc_words(q_h + gg * q_sg, live ? qd_bytes : 0u);
+    gd.d = rsrc_words(do_h + gg * do_sg, live ? qd_bytes : 0u);
+    gd.pk = rsrc_words(pk_h + gg * pk_sg, live ? (uint32_t)(Lq * 8) : 0u);
+    return gd;
+  };
+  // stage (the group of gd, step i: query tile 8 i + wave) into ring stage
+  // st of this wave: the pack (1 load) and the Q / dO tiles (4); every stage
+  // issues all five
+  auto dma_stage = [&](const GroupDesc& gd, auto ic, int st) {
+    constexpr int i = decltype(ic)::value;
+    const uint32_t m0 = ring_m0 + (uint32_t)st * kStageStride;
+    dma4_m0(gd.pk, m0 + offsetof(RingStage, ld), ld_off[i]);
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      dma16_asm(qr, rs.q + 16 * r * 32, q_lane_off[r], 0u);
-      dma16_asm(dr, rs.d + 16 * r * 32, do_lane_off[r], 0u);
+      dma16_m0(gd.q, m0 + offsetof(RingStage, q) + 16 * r * 32 * 2, tile_off[i][r]);
+      dma16_m0(gd.d, m0 + offsetof(RingStage, d) + 16 * r * 32 * 2, tile_off[i][r]);
     }
   };
   // K/V block of group g into slot g & 1: one DMA load per wave (waves 4..7
@@ -251,52 +276,68 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
     const bool live = g < g_end;
     const int64_t gg = live ? g : g_begin;
     const u32x4 r = rsrc_words(kv_h + gg * kv_sg, live ? kv_bytes : 0u);
-    dma16_asm(r, kv_lds + ((g & 1) * 2 + kv_t) * 32 * 32 + 16 * (wave & 1) * 32, kv_lane_off, 0u);
+    dma16_m0(r, kv_m0 + (uint32_t)((g & 1) * 2 * 32 * 32 * sizeof(T)), kv_lane_off);
   };
   // keep bytes of group g's keys into keep_lds[g & 1] (one load)
   auto dma_keep = [&](int g) {
     const bool live = g < g_end;
     const int64_t gg = live ? g : g_begin;
     const u32x4 r = rsrc_words(has_mask ? m_h + gg * m_sg : nullptr, has_mask && live ? (uint32_t)Lk : 0u);
-    dma_u8_asm(r, keep_lds[g & 1], (uint32_t)key);
+    dma_u8_m0(r, keep_m0 + (uint32_t)((g & 1) * 64 * 4), (uint32_t)key);
   };
   // whether key kb * 32 + k of group g is attended (its keep byte has landed)
   auto kv_keep = [&](int g, int k) {
     return g < g_end && kb * 32 + k < Lk && (!has_mask || keep_lds[g & 1][k] != 0);
   };
 
-  // reducer role of this thread at each group's end: accumulator lane
-  // red_lane (key red_lane % 32) and registers 2 red_jp, 2 red_jp + 1, which
-  // hold head dims red_d0, red_d0 + 1
-  const int red_lane = tid & 63, red_jp = tid >> 6;
-  const int red_key = red_lane & 31;
-  const int red_d0 = 8 * (red_jp >> 1) + 4 * (red_lane >> 5) + 2 * (red_jp & 1);
+  // Group end: the eight waves' dK (then dV) partials are summed through
+  // LDS and stored.  Reader threads: waves 0-3 for dK, waves 4-7 for dV;
+  // thread t of them owns dims 4 red_q .. 4 red_q + 3 of key red_key
+  // (red_q = 2 c + g2 for chunk c and lane half g2 of the accumulator
+  // layout), so eight consecutive lanes write one whole 64-byte key row:
+  // scattered 4-byte stores into rows 196 KB apart (the ending-node
+  // layout) cost the kernel a third of its time.
+  const int red_t = tid & 255;
+  const int red_key = red_t >> 3, red_q = red_t & 7;
+  const int red_c = red_q >> 1, red_g = red_q & 1;
   const int red_gkey = kb * 32 + red_key;
-  const bool red_live = red_gkey < Lk && red_d0 < D;
-  const int64_t red_k = S.k_off + h * S.k_sh + (int64_t)red_gkey * S.k_si + red_d0;
-  const int64_t red_v = S.v_off + h * S.v_sh + (int64_t)red_gkey * S.v_si + red_d0;
+  const bool red_live = red_gkey < Lk && 4 * red_q < D;
+  const int64_t red_k = S.k_off + h * S.k_sh + (int64_t)red_gkey * S.k_si + 4 * red_q;
+  const int64_t red_v = S.v_off + h * S.v_sh + (int64_t)red_gkey * S.v_si + 4 * red_q;
   const int64_t k_sg = S.k_sg, v_sg = S.v_sg;
-  constexpr int kStageFloats = (int)(sizeof(RingStage) / 4);
-  static_assert(16 * 64 <= kStageFloats, "a wave's partials fit its ring stage");
+  constexpr int kStageF4 = (int)(sizeof(RingStage) / 16);
+  static_assert(sizeof(RingStage) % 16 == 0 && 16 * 64 <= 4 * kStageF4, "a wave's partials fit its ring stage");
   // one tensor's partials (acc) -> each wave's ring stage `slot` (read
-  // already), barrier, the fixed-order sum of the eight waves' partials,
-  // scaled, stored; barrier (partials read before that LDS is written again)
-  auto reduce_store = [&](int slot, const f32x16& acc, T* dst, int64_t off, float sc, bool kv_ok) {
-    float* const red = reinterpret_cast<float*>(&ring_lds[slot][0]);
-    float* rw = red + wave * kStageFloats + lane;
+  // already), barrier, the fixed-order sum of the eight waves' partials by
+  // the reader waves, scaled, stored; barrier (partials read before that LDS
+  // is written again).  Lane L's registers 4 c .. 4 c + 3 (dims 8 c + 4 g2
+  // .. + 3 of its key) sit at float4 64 c + (L ^ 4 c) of its wave's block:
+  // the writes of a wave are a permutation of consecutive 16-byte slots, and
+  // the reads of eight consecutive lanes (one key, four c, two g2) fall into
+  // four bank groups, two lanes each.
+  const int red_src = 64 * red_c + ((red_key + 32 * red_g) ^ (4 * red_c));
+  auto reduce_store = [&](int slot, const f32x16& acc, T* dst, int64_t off, float sc, bool kv_ok, int rd) {
+    float4* const red = reinterpret_cast<float4*>(&ring_lds[slot][0]);
+    float4* const rw = red + wave * kStageF4;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) rw[j * 64] = acc[j];
+    for (int c = 0; c < 4; ++c)
+      rw[64 * c + (lane ^ (4 * c))] = make_float4(acc[4 * c], acc[4 * c + 1], acc[4 * c + 2], acc[4 * c + 3]);
     __syncthreads();
-    const float* src = red + 2 * red_jp * 64 + red_lane;
-    float o0 = src[0], o1 = src[64];
+    if ((wave >> 2) == rd) {
+      const float4* src = red + red_src;
+      float4 o = src[0];
 #pragma unroll
-    for (int w = 1; w < kFusedWaves; ++w) {
-      o0 += src[w * kStageFloats];
-      o1 += src[w * kStageFloats + 64];
-    }
-    if (dst != nullptr && red_live) {
-      const float f = kv_ok ? sc : 0.0f;
-      *reinterpret_cast<uint32_t*>(dst + off) = pack2<T>(o0 * f, o1 * f);
+      for (int w = 1; w < kFusedWaves; ++w) {
+        const float4 x = src[w * kStageF4];
+        o.x += x.x;
+        o.y += x.y;
+        o.z += x.z;
+        o.w += x.w;
+      }
+      if (dst != nullptr && red_live) {
+        const float f = kv_ok ? sc : 0.0f;
+        *reinterpret_cast<uint2*>(dst + off) = make_uint2(pack2<T>(o.x * f, o.y * f), pack2<T>(o.z * f, o.w * f));
+      }
     }
     __syncthreads();
   };
@@ -315,9 +356,15 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   // stages, the bias region
   dma_kv(g_begin);
   if constexpr (MASKED) dma_keep(g_begin);
-  dma_stage(g_begin, I0{}, ring_lds[0][wave]);
-  if constexpr (NS == 1) dma_stage(g_begin + 1, I0{}, ring_lds[1][wave]);
-  else dma_stage(g_begin, I1{}, ring_lds[1][wave]);
+  // (gd: the resources of the group whose stage was issued last)
+  GroupDesc gd = group_desc(g_begin);
+  dma_stage(gd, I0{}, 0);
+  if constexpr (NS == 1) {
+    gd = group_desc(g_begin + 1);
+    dma_stage(gd, I0{}, 1);
+  } else {
+    dma_stage(gd, I1{}, 1);
+  }
   // the bias region: wave w loads query tiles w, w + 8, ... (both chunks)
   // (query tiles past Lq, which ghost steps read, are zeros)
 #pragma unroll
@@ -326,8 +373,8 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
     const bool in = qt < nqt && qt < a.bf_nqt;
 #pragma unroll
     for (int c = 0; c < 2; ++c)
-      dma16_asm(b_rsrc, bias_lds + (qt * 2 + c) * 64 * 8, in ? b_lane : kOut,
-                in ? (uint32_t)(qt * bf_step + c * 1024) : 0u);
+      dma16_m0(b_rsrc, bias_m0 + (uint32_t)((qt * 2 + c) * 64 * 8 * sizeof(T)),
+               in ? b_lane + (uint32_t)(qt * bf_step + c * 1024) : kOut);
   }
   wait_vm<0>();
   __syncthreads();
@@ -376,7 +423,9 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
       {
         constexpr int ahead = i + 2;
         const int as = NS == 3 ? ahead % 3 : (slot == 0 ? 2 : slot - 1);
-        dma_stage(g + ahead / NS, std::integral_constant<int, ahead % NS>{}, ring_lds[as][wave]);
+        // the first stage of a group: that group's resources
+        if constexpr (ahead % NS == 0) gd = group_desc(g + ahead / NS);
+        dma_stage(gd, std::integral_constant<int, ahead % NS>{}, as);
       }
 
       // ---- compute this stage, unless its query tile is past Lq (a ghost step of a shorter sample: its
@@ -432,8 +481,8 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
     // (this wave's own load wrote the keep bytes it reads; the other waves'
     // loads write the same bytes)
     const bool kv_ok = MASKED ? kv_keep(g, red_key) : true;
-    reduce_store(red_slot, dk, a.dk, red_k + (int64_t)g * k_sg, a.scale, kv_ok);
-    reduce_store(red_slot, dv, a.dv, red_v + (int64_t)g * v_sg, 1.0f, kv_ok);
+    reduce_store(red_slot, dk, a.dk, red_k + (int64_t)g * k_sg, a.scale, kv_ok, 0);
+    reduce_store(red_slot, dv, a.dv, red_v + (int64_t)g * v_sg, 1.0f, kv_ok, 1);
     dk = f32x16{};
     dv = f32x16{};
   }
