@@ -49,8 +49,9 @@ using namespace fast;
 namespace {
 
 constexpr int kFusedWaves = 8;
-constexpr int kFusedMaxSteps = 3;  // query tiles per wave: Lq <= 8 * 3 * 32
-constexpr int kFusedMaxQT = kFusedWaves * kFusedMaxSteps;  // query tiles of the largest bias region
+constexpr int kRowWaves = 4;       // waves per group: two groups in flight
+constexpr int kFusedMaxSteps = 6;  // query tiles per wave and group: Lq <= 4 * 6 * 32
+constexpr int kFusedMaxQT = kRowWaves * kFusedMaxSteps;  // query tiles of the largest bias region
 static_assert(kFusedMaxQT * 32 == kFusedMaxLen, "the plan's length limit is the kernel's");
 constexpr int kQT = 32 * 32;       // elements of one 32 x 32 tile
 
@@ -112,15 +113,15 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   static_assert(NS >= 1 && NS <= kFusedMaxSteps, "query tiles per wave and group");
 
   // per-wave ring of three stages (two in flight while one is read); at a
-  // group's end a wave's just-read stage holds its dK/dV partials
+  // pair's end a wave's just-read stage holds its dK/dV partials
   __shared__ __attribute__((aligned(16))) RingStage ring_lds[3][kFusedWaves];
-  // K / V block of a group: [g parity][K, V][32 keys][32]
+  // K / V blocks of the pair's two groups: [group of the pair][K, V][32 keys][32]
   __shared__ __attribute__((aligned(16))) T kv_lds[2 * 2 * 32 * 32];
   // the workgroup's bias region, identity-MFMA fragments of its 32 keys for
   // every query tile: [query tile][chunk c][64 lanes][8], loaded once per part
-  __shared__ __attribute__((aligned(16))) T bias_lds[NS * kFusedWaves * 2 * 64 * 8];
-  // keep bytes of the 32 keys of a group, per lane (lanes 32..63 repeat
-  // 0..31): [g parity][64]
+  __shared__ __attribute__((aligned(16))) T bias_lds[NS * kRowWaves * 2 * 64 * 8];
+  // keep bytes of the 32 keys of the pair's groups, per lane (lanes 32..63
+  // repeat 0..31): [group of the pair][64]
   __shared__ uint32_t keep_lds[2][64];
 
   const int tid = threadIdx.x;
@@ -128,16 +129,19 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   // wave-uniform and lives in scalar registers, e.g. the LDS base of the
   // direct-to-LDS loads, which must be a scalar)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rs = wave >> 2;  // group of the pair this wave works on
+  const int wq = wave & 3;   // its quarter of the query tiles
   const int lane = tid & 63;
   const int lq = lane & 31;
   const int g2 = lane >> 5;
 
   // LDS byte addresses (M0 of the direct-to-LDS loads): this wave's ring
-  // stage 0 (stage s adds s * kStageStride), its K/V slot, the keep bytes
+  // stage 0 (stage s adds s * kStageStride), its K/V rows, its keep bytes
   constexpr uint32_t kStageStride = kFusedWaves * sizeof(RingStage);
   const uint32_t ring_m0 = lds_addr(&ring_lds[0][wave]);
-  const uint32_t kv_m0 = lds_addr(kv_lds) + (uint32_t)((((wave >> 1) & 1) * 32 * 32 + 16 * (wave & 1) * 32) * sizeof(T));
-  const uint32_t keep_m0 = lds_addr(keep_lds);
+  const uint32_t kv_m0 =
+      lds_addr(kv_lds) + (uint32_t)(((rs * 2 + ((wq >> 1) & 1)) * 32 * 32 + 16 * (wq & 1) * 32) * sizeof(T));
+  const uint32_t keep_m0 = lds_addr(keep_lds) + (uint32_t)(rs * 64 * 4);
   const uint32_t bias_m0 = lds_addr(bias_lds);
 
   int64_t tile = xcd_tile(blockIdx.x, gridDim.x, xcd_chunk(a.uniform_tiles));
@@ -169,13 +173,13 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   const int g_begin = __builtin_amdgcn_readfirstlane((int)(G * part / P));
   const int g_end = __builtin_amdgcn_readfirstlane((int)(G * (part + 1) / P));
   const int D = a.head_size;
-  const int nqt = (Lq + 31) >> 5;  // <= NS * 8 (the launch picks NS for the longest sample)
-  // Q and dO rows come from the dQ kernel's compact copies: row
-  // l_off + (g H + h) Lq + q of kCompactRow elements
+  const int nqt = (Lq + 31) >> 5;  // <= NS * 4 (the launch picks NS for the longest sample)
   const float c1 = a.scale * kLog2e;
   const int key = kb * 32 + lq;  // this lane's key
   const bool has_mask = MASKED && a.mask != nullptr && S.m_off >= 0;
 
+  // Q and dO rows come from the dQ kernel's compact copies: row
+  // l_off + (g H + h) Lq + q of kCompactRow elements
   const int64_t row_h = S.l_off + (int64_t)h * Lq;
   const T* const q_h = uptr(a.qc + row_h * kCompactRow);
   const T* const do_h = uptr(a.dc + row_h * kCompactRow);
@@ -187,7 +191,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   const int64_t m_sg = has_mask ? u64(S.m_sg) : 0;
 
   // ---- per-lane DMA offsets (bytes) of the Q / dO tile rows of step i
-  // (query tile 8 i + wave) within the (g, h) block of the compact copies,
+  // (query tile 4 i + wq) within the (g, h) block of the compact copies,
   // which are the same for Q and dO: load r (0, 1) of a tile covers rows
   // 16 r .. 16 r + 15; lane l writes slot l = row 16 r + l / 4, physical
   // chunk l % 4, which holds logical chunk (l % 4) ^ swz(row).  Rows past Lq
@@ -199,10 +203,10 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
     for (int r = 0; r < 2; ++r) {
       const int row = 16 * r + (lane >> 2);
       const int col = ((lane & 3) ^ swz<32>(row)) * 8;
-      const int q = (8 * i + wave) * 32 + row;
+      const int q = (kRowWaves * i + wq) * 32 + row;
       tile_off[i][r] = col < D && q < Lq ? (uint32_t)((q * kCompactRow + col) * 2) : kOut;
     }
-  // pack offsets of step i: lane l reads query (8 i + wave) * 32 + ld_q,
+  // pack offsets of step i: lane l reads query (4 i + wq) * 32 + ld_q,
   // lanes 32..63 from the -delta half, so that ring position l holds the
   // query the accumulator layout puts there (ld_q inverts perm32); a query
   // past Lq gets 2^31 added (out of range: it reads 0)
@@ -210,12 +214,13 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   uint32_t ld_off[NS];
 #pragma unroll
   for (int i = 0; i < NS; ++i) {
-    const int q = (8 * i + wave) * 32 + ld_q;
+    const int q = (kRowWaves * i + wq) * 32 + ld_q;
     ld_off[i] = (uint32_t)((q + g2 * Lq) * 4) | ((uint32_t)(q >= Lq) << 31);
   }
-  // K/V block DMA: waves 0..3 load tensor w / 2 (K, V), rows 16 (w % 2) .. +15
-  const int kv_t = (wave >> 1) & 1;
-  const int kv_row = 16 * (wave & 1) + (lane >> 2);
+  // K/V block DMA of a group: the group's four waves load tensor wq / 2
+  // (K, V), rows 16 (wq % 2) .. + 15
+  const int kv_t = (wq >> 1) & 1;
+  const int kv_row = 16 * (wq & 1) + (lane >> 2);
   const int kv_col = (lane & 3) * 8;
   const int64_t kv_si = u64(kv_t ? S.v_si : S.k_si);
   const int64_t kv_sg = u64(kv_t ? S.v_sg : S.k_sg);
@@ -256,8 +261,8 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
     gd.pk = rsrc_words(pk_h + gg * pk_sg, live ? (uint32_t)(Lq * 8) : 0u);
     return gd;
   };
-  // stage (the group of gd, step i: query tile 8 i + wave) into ring stage
-  // st of this wave: the pack (1 load) and the Q / dO tiles (4); every stage
+  // stage (the group of gd, step i: query tile 4 i + wq) into ring stage st
+  // of this wave: the pack (1 load) and the Q / dO tiles (4); every stage
   // issues all five
   auto dma_stage = [&](const GroupDesc& gd, auto ic, int st) {
     constexpr int i = decltype(ic)::value;
@@ -269,34 +274,32 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
       dma16_m0(gd.d, m0 + offsetof(RingStage, d) + 16 * r * 32 * 2, tile_off[i][r]);
     }
   };
-  // K/V block of group g into slot g & 1: one DMA load per wave (waves 4..7
-  // repeat the loads of waves 0..3, writing the same bytes, so that every
-  // wave issues the same loads)
+  // K/V block of this wave's group g into its slot of kv_lds (one DMA load)
   auto dma_kv = [&](int g) {
     const bool live = g < g_end;
     const int64_t gg = live ? g : g_begin;
     const u32x4 r = rsrc_words(kv_h + gg * kv_sg, live ? kv_bytes : 0u);
-    dma16_m0(r, kv_m0 + (uint32_t)((g & 1) * 2 * 32 * 32 * sizeof(T)), kv_lane_off);
+    dma16_m0(r, kv_m0, kv_lane_off);
   };
-  // keep bytes of group g's keys into keep_lds[g & 1] (one load)
+  // keep bytes of group g's keys into keep_lds[rs] (one load)
   auto dma_keep = [&](int g) {
     const bool live = g < g_end;
     const int64_t gg = live ? g : g_begin;
     const u32x4 r = rsrc_words(has_mask ? m_h + gg * m_sg : nullptr, has_mask && live ? (uint32_t)Lk : 0u);
-    dma_u8_m0(r, keep_m0 + (uint32_t)((g & 1) * 64 * 4), (uint32_t)key);
+    dma_u8_m0(r, keep_m0, (uint32_t)key);
   };
-  // whether key kb * 32 + k of group g is attended (its keep byte has landed)
+  // whether key kb * 32 + k of this wave's group g is attended (its keep bytes have landed)
   auto kv_keep = [&](int g, int k) {
-    return g < g_end && kb * 32 + k < Lk && (!has_mask || keep_lds[g & 1][k] != 0);
+    return g < g_end && kb * 32 + k < Lk && (!has_mask || keep_lds[rs][k] != 0);
   };
 
-  // Group end: the eight waves' dK (then dV) partials are summed through
-  // LDS and stored.  Reader threads: waves 0-3 for dK, waves 4-7 for dV;
-  // thread t of them owns dims 4 red_q .. 4 red_q + 3 of key red_key
+  // Pair end: each group's four waves' dK (then dV) partials are summed
+  // through LDS and stored.  The reader threads of a group are its own four
+  // waves; thread t of them owns dims 4 red_q .. 4 red_q + 3 of key red_key
   // (red_q = 2 c + g2 for chunk c and lane half g2 of the accumulator
   // layout), so eight consecutive lanes write one whole 64-byte key row:
-  // scattered 4-byte stores into rows 196 KB apart (the ending-node
-  // layout) cost the kernel a third of its time.
+  // scattered 4-byte stores into rows 196 KB apart (the ending-node layout)
+  // cost the kernel a third of its time.
   const int red_t = tid & 255;
   const int red_key = red_t >> 3, red_q = red_t & 7;
   const int red_c = red_q >> 1, red_g = red_q & 1;
@@ -308,36 +311,35 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   constexpr int kStageF4 = (int)(sizeof(RingStage) / 16);
   static_assert(sizeof(RingStage) % 16 == 0 && 16 * 64 <= 4 * kStageF4, "a wave's partials fit its ring stage");
   // one tensor's partials (acc) -> each wave's ring stage `slot` (read
-  // already), barrier, the fixed-order sum of the eight waves' partials by
-  // the reader waves, scaled, stored; barrier (partials read before that LDS
-  // is written again).  Lane L's registers 4 c .. 4 c + 3 (dims 8 c + 4 g2
+  // already), barrier, the fixed-order sum of the group's four partials by
+  // its waves, scaled, stored; barrier (partials read before that LDS is
+  // written again).  Lane L's registers 4 c .. 4 c + 3 (dims 8 c + 4 g2
   // .. + 3 of its key) sit at float4 64 c + (L ^ 4 c) of its wave's block:
   // the writes of a wave are a permutation of consecutive 16-byte slots, and
   // the reads of eight consecutive lanes (one key, four c, two g2) fall into
   // four bank groups, two lanes each.
   const int red_src = 64 * red_c + ((red_key + 32 * red_g) ^ (4 * red_c));
-  auto reduce_store = [&](int slot, const f32x16& acc, T* dst, int64_t off, float sc, bool kv_ok, int rd) {
+  // (a masked key's rows are written as zeros; a dead group writes nothing)
+  auto reduce_store = [&](int slot, const f32x16& acc, T* dst, int64_t off, float sc, bool live, bool ok) {
     float4* const red = reinterpret_cast<float4*>(&ring_lds[slot][0]);
     float4* const rw = red + wave * kStageF4;
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       rw[64 * c + (lane ^ (4 * c))] = make_float4(acc[4 * c], acc[4 * c + 1], acc[4 * c + 2], acc[4 * c + 3]);
     __syncthreads();
-    if ((wave >> 2) == rd) {
-      const float4* src = red + red_src;
-      float4 o = src[0];
+    const float4* src = red + kRowWaves * rs * kStageF4 + red_src;
+    float4 o = src[0];
 #pragma unroll
-      for (int w = 1; w < kFusedWaves; ++w) {
-        const float4 x = src[w * kStageF4];
-        o.x += x.x;
-        o.y += x.y;
-        o.z += x.z;
-        o.w += x.w;
-      }
-      if (dst != nullptr && red_live) {
-        const float f = kv_ok ? sc : 0.0f;
-        *reinterpret_cast<uint2*>(dst + off) = make_uint2(pack2<T>(o.x * f, o.y * f), pack2<T>(o.z * f, o.w * f));
-      }
+    for (int w = 1; w < kRowWaves; ++w) {
+      const float4 x = src[w * kStageF4];
+      o.x += x.x;
+      o.y += x.y;
+      o.z += x.z;
+      o.w += x.w;
+    }
+    if (dst != nullptr && red_live && live) {
+      const float f = ok ? sc : 0.0f;
+      *reinterpret_cast<uint2*>(dst + off) = make_uint2(pack2<T>(o.x * f, o.y * f), pack2<T>(o.z * f, o.w * f));
     }
     __syncthreads();
   };
@@ -350,26 +352,26 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   f32x16 dk = f32x16{}, dv = f32x16{};
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
 
-  // ---- prologue: K/V and keep bytes of the first group, the first two
+  // ---- prologue: K/V and keep bytes of the first pair, the first two
   // stages, the bias region
-  dma_kv(g_begin);
-  if constexpr (MASKED) dma_keep(g_begin);
+  dma_kv(g_begin + rs);
+  if constexpr (MASKED) dma_keep(g_begin + rs);
   // (gd: the resources of the group whose stage was issued last)
-  GroupDesc gd = group_desc(g_begin);
+  GroupDesc gd = group_desc(g_begin + rs);
   dma_stage(gd, I0{}, 0);
   if constexpr (NS == 1) {
-    gd = group_desc(g_begin + 1);
+    gd = group_desc(g_begin + 2 + rs);
     dma_stage(gd, I0{}, 1);
   } else {
     dma_stage(gd, I1{}, 1);
   }
-  // the bias region: wave w loads query tiles w, w + 8, ... (both chunks)
-  // (query tiles past Lq, which ghost steps read, are zeros)
+  // the bias region: wave w loads query tiles 4 i + w % 4 (both chunks; the
+  // two groups' waves write the same bytes); query tiles past Lq, which
+  // ghost steps read, are zeros
 #pragma unroll
   for (int i = 0; i < NS; ++i) {
-    const int qt = 8 * i + wave;
+    const int qt = kRowWaves * i + wq;
     const bool in = qt < nqt && qt < a.bf_nqt;
 #pragma unroll
     for (int c = 0; c < 2; ++c)
@@ -379,21 +381,26 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   wait_vm<0>();
   __syncthreads();
 
-  // Loads per step, in issue order: [at a group's first step: the next
-  // group's K/V block and keep bytes (1 + MASKED)], the pack (1), the Q/dO
+  // Loads per step, in issue order: [at a pair's first step: the next
+  // pair's K/V block and keep bytes (1 + MASKED)], the pack (1), the Q/dO
   // tiles (4), all for the stage two ahead.  A step first waits for its own
   // stage, issued two steps earlier: everything issued after it (the
   // previous step's loads) may still be in flight.
   constexpr int kPerStep = 5;
   constexpr int kGroupLoads = MASKED ? 2 : 1;
-  int slot = 0;  // ring slot of the stage being computed (always the step index when NS == 3)
-  for (int g = g_begin; g < g_end; ++g) {
-    // this group's K / V fragments (B operand: lane = key, 8 consecutive d)
+  int slot = 0;  // ring slot of the stage being computed (the step index mod 3 when 3 divides NS)
+  constexpr bool kFixedSlots = NS % 3 == 0;
+  for (int gp = g_begin; gp < g_end; gp += 2) {
+    const int g = gp + rs;  // this wave's group (past g_end: a dead group, all zeros, nothing stored)
+    const bool g_live = g < g_end;
+    // this group's K / V fragments (B operand: lane = key, 8 consecutive d),
+    // its keep bits, and those of the key whose dK / dV this thread stores
     Frag kf[2], vf[2];
     const bool kvalid = MASKED ? kv_keep(g, lq) : true;
     const bool wave_masked = MASKED && __any(!kvalid);
+    const bool red_ok = MASKED ? kv_keep(g, red_key) : true;
     {
-      const T* kb_ = kv_lds + ((g & 1) * 2) * 32 * 32 + lq * 32;
+      const T* kb_ = kv_lds + (rs * 2) * 32 * 32 + lq * 32;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         kf[s] = lds_frag<T>(kb_ + 16 * s + 8 * g2);
@@ -404,39 +411,42 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
         }
       }
     }
+    // every wave has its K / V in registers and its keep bits: the next
+    // pair's loads (issued at this pair's first step) may overwrite them
+    __syncthreads();
 
-    // one step: query tile 8 i + wave of group g (straight-line code per
+    // one step: query tile 4 i + wq of group g (straight-line code per
     // step; the scheduling barriers keep each step's temporaries within it,
     // the register budget being 256 per lane at two waves per SIMD)
     auto step = [&](auto ic) {
       constexpr int i = decltype(ic)::value;
       __builtin_amdgcn_sched_barrier(0);
-      // the previous step was a group's first (it issued the group loads too)
+      // the previous step was a pair's first (it issued the pair loads too)
       if constexpr (i == 1 || NS == 1) wait_vm<kPerStep + kGroupLoads>();
       else wait_vm<kPerStep>();
-      const int cs = NS == 3 ? i : slot;
+      const int cs = kFixedSlots ? i % 3 : slot;
       const RingStage& cur = ring_lds[cs][wave];
       if constexpr (i == 0) {
-        dma_kv(g + 1);
-        if constexpr (MASKED) dma_keep(g + 1);
+        dma_kv(gp + 2 + rs);
+        if constexpr (MASKED) dma_keep(gp + 2 + rs);
       }
       {
         constexpr int ahead = i + 2;
-        const int as = NS == 3 ? ahead % 3 : (slot == 0 ? 2 : slot - 1);
+        const int as = kFixedSlots ? ahead % 3 : (slot == 0 ? 2 : slot - 1);
         // the first stage of a group: that group's resources
-        if constexpr (ahead % NS == 0) gd = group_desc(g + ahead / NS);
+        if constexpr (ahead % NS == 0) gd = group_desc(gp + 2 * (ahead / NS) + rs);
         dma_stage(gd, std::integral_constant<int, ahead % NS>{}, as);
       }
 
-      // ---- compute this stage, unless its query tile is past Lq (a ghost step of a shorter sample: its
-      // zero Q, dO, pack and bias contribute nothing).  Wave-uniform; the loads above run either way, so
-      // the wait counts stay the same, and the other wave on the SIMD runs its step alone meanwhile
-      if (i * 8 + wave < nqt) {
+      // ---- compute this stage, unless its query tile is past Lq (a ghost step of a shorter sample) or
+      // its group is dead: its zero Q, dO, pack and bias contribute nothing.  Wave-uniform; the loads above
+      // run either way, so the wait counts stay the same, and the other wave on the SIMD runs alone meanwhile
+      if (i * kRowWaves + wq < nqt && g_live) {
       const T* qt_ = reinterpret_cast<const T*>(cur.q);
       const T* dt_ = reinterpret_cast<const T*>(cur.d);
       f32x16 sacc = *reinterpret_cast<const f32x16*>(&cur.ld[g2 * 16]);
       {
-        const T* bq = bias_lds + (i * 8 + wave) * 2 * 64 * 8 + lane * 8;
+        const T* bq = bias_lds + (i * kRowWaves + wq) * 2 * 64 * 8 + lane * 8;
         sacc = E::mma(lds_frag<T>(bq), ident[0], sacc);
         sacc = E::mma(lds_frag<T>(bq + 64 * 8), ident[1], sacc);
       }
@@ -465,38 +475,52 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
         dk = E::mma(lds_read_tr_frag_sw<T>(qt_ + at, trl), sf, dk);
       }
       }
-      if constexpr (NS != 3) slot = slot == 2 ? 0 : slot + 1;
+      if constexpr (!kFixedSlots) slot = slot == 2 ? 0 : slot + 1;
     };
     step(I0{});
     if constexpr (NS > 1) step(I1{});
-    if constexpr (NS > 2) step(I2{});
+    if constexpr (NS > 2) step(std::integral_constant<int, 2>{});
+    if constexpr (NS > 3) step(std::integral_constant<int, 3>{});
+    if constexpr (NS > 4) step(std::integral_constant<int, 4>{});
+    if constexpr (NS > 5) step(std::integral_constant<int, 5>{});
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- group end: the next group's K/V block and keep bytes have landed
-    // (issued at this group's first step, followed by kPerStep loads per
-    // step); the waves' dK and dV partials are summed and stored through the
-    // ring stage the last step read
+    // ---- pair end: the next pair's K/V blocks and keep bytes have landed
+    // (issued at this pair's first step, followed by kPerStep loads per
+    // step); each group's dK and dV partials are summed and stored through
+    // the ring stage the last step read
     wait_vm<NS * kPerStep>();
-    const int red_slot = NS == 3 ? 2 : (slot == 0 ? 2 : slot - 1);
-    // (this wave's own load wrote the keep bytes it reads; the other waves'
-    // loads write the same bytes)
-    const bool kv_ok = MASKED ? kv_keep(g, red_key) : true;
-    reduce_store(red_slot, dk, a.dk, red_k + (int64_t)g * k_sg, a.scale, kv_ok, 0);
-    reduce_store(red_slot, dv, a.dv, red_v + (int64_t)g * v_sg, 1.0f, kv_ok, 1);
+    const int red_slot = kFixedSlots ? (NS - 1) % 3 : (slot == 0 ? 2 : slot - 1);
+    reduce_store(red_slot, dk, a.dk, red_k + (int64_t)g * k_sg, a.scale, g_live, red_ok);
+    reduce_store(red_slot, dv, a.dv, red_v + (int64_t)g * v_sg, 1.0f, g_live, red_ok);
     dk = f32x16{};
     dv = f32x16{};
   }
 
-  // ---- the part's dBias slab: region[i] holds queries (8 i + wave) * 32 +
-  // kappa(g2, j) of this lane's key
-  if (key < Lk) {
+  // ---- the part's dBias slab.  Waves w and w + 4 hold the same query tiles
+  // (their groups' halves of the part's sum): the second group's regions go
+  // through LDS (the ring, idle once its loads have drained) to the first's
+  // waves, which add them and store; region[i] holds queries
+  // (4 i + wq) * 32 + kappa(g2, j) of this lane's key
+  wait_vm<0>();
+  __syncthreads();
+  float* const xr = reinterpret_cast<float*>(&ring_lds[0][0]) + (wq * NS * 16) * 64 + lane;
+  static_assert(kRowWaves * NS * 16 * 64 * 4 <= sizeof(RingStage) * 3 * kFusedWaves, "regions fit the ring");
+  if (rs == 1) {
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) xr[(i * 16 + j) * 64] = region[i][j];
+  }
+  __syncthreads();
+  if (rs == 0 && key < Lk) {
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
-      const int q0 = (8 * i + wave) * 32;
+      const int q0 = (kRowWaves * i + wq) * 32;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const int q = q0 + kappa(g2, j);
-        if (q < Lq) db_col[(int64_t)q * db_si] = region[i][j];
+        if (q < Lq) db_col[(int64_t)q * db_si] = region[i][j] + xr[(i * 16 + j) * 64];
       }
     }
   }
@@ -522,7 +546,7 @@ hipError_t launch_dkvb_fused(const oops_attn_geometry& geo, const Plan& plan, co
     const dim3 grid((unsigned)xcd_grid(plan.fused_tiles, xcd_chunk(plan.fused_uniform)));
     // query tiles per wave and group: that of the longest sample
     a.fused_max_lq = plan.fused_split ? kFusedMaxLen : 0;
-    const int ns = (int)((plan.fused_max_len_q + 32 * kFusedWaves - 1) / (32 * kFusedWaves));
+    const int ns = (int)((plan.fused_max_len_q + 32 * kRowWaves - 1) / (32 * kRowWaves));
     auto run = [&](auto masked, auto nsc) {
       hipLaunchKernelGGL((attn_dkvb_fast_kernel<T, decltype(masked)::value, decltype(nsc)::value>), grid, dim3(512),
                          0, stream, a);
@@ -530,7 +554,10 @@ hipError_t launch_dkvb_fused(const oops_attn_geometry& geo, const Plan& plan, co
     auto by_ns = [&](auto masked) {
       if (ns == 1) run(masked, std::integral_constant<int, 1>{});
       else if (ns == 2) run(masked, std::integral_constant<int, 2>{});
-      else run(masked, std::integral_constant<int, 3>{});
+      else if (ns == 3) run(masked, std::integral_constant<int, 3>{});
+      else if (ns == 4) run(masked, std::integral_constant<int, 4>{});
+      else if (ns == 5) run(masked, std::integral_constant<int, 5>{});
+      else run(masked, std::integral_constant<int, 6>{});
     };
     if (geo.has_mask) by_ns(std::true_type{});
     else by_ns(std::false_type{});
