@@ -262,14 +262,17 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
           sacc[t2][j] = ((lb >> kk) & 1) ? sacc[t2][j] : kNegInf;
         }
     }
-    // tile max as a tree (short dependency chain), then across the halves
-    float m8[8];
+    // tile max: two chains of three-operand maxima (v_max3, two new values
+    // per operation: 17 operations for 32 values), then across the halves
+    float mc[2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      m8[i] = fmaxf(fmaxf(sacc[i >> 2][4 * (i & 3)], sacc[i >> 2][4 * (i & 3) + 1]),
-                    fmaxf(sacc[i >> 2][4 * (i & 3) + 2], sacc[i >> 2][4 * (i & 3) + 3]));
-    float mx = fmaxf(fmaxf(fmaxf(m8[0], m8[1]), fmaxf(m8[2], m8[3])), fmaxf(fmaxf(m8[4], m8[5]), fmaxf(m8[6], m8[7])));
-    mx = max_halves(mx) * c1;
+    for (int t2 = 0; t2 < 2; ++t2) {
+      float x = fmaxf(fmaxf(sacc[t2][0], sacc[t2][1]), sacc[t2][2]);
+#pragma unroll
+      for (int j = 3; j < 15; j += 2) x = fmaxf(fmaxf(x, sacc[t2][j]), sacc[t2][j + 1]);
+      mc[t2] = fmaxf(x, sacc[t2][15]);
+    }
+    float mx = max_halves(fmaxf(mc[0], mc[1])) * c1;
     const bool grow = mx > m_run + kLazyRescale;
     if (__any(grow)) {
       const float m_new = grow ? mx : m_run;
@@ -281,7 +284,8 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
     }
     const float neg_m = m_run == kNegInf ? 0.0f : -m_run;
     // row sum in four independent chains, added to l_run at the end
-    float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // (each chain's first v_dot2 adds to a literal zero: no register to clear)
+    float ls[4];
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
@@ -292,7 +296,7 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
           P2 pr;
           pr[0] = (T)__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t2][8 * m + e], c1, neg_m));
           pr[1] = (T)__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t2][8 * m + e + 1], c1, neg_m));
-          ls[e >> 1] = Pair<T>::dot(pr, ones, ls[e >> 1]);
+          ls[e >> 1] = Pair<T>::dot(pr, ones, t2 == 0 && m == 0 ? 0.0f : ls[e >> 1]);
           pf[e] = pr[0];
           pf[e + 1] = pr[1];
         }
