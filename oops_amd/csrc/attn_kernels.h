@@ -151,6 +151,7 @@ struct Plan {
   bool all_shared = false;                       // every sample has a row-shared bias
   // fused dK/dV + shared dBias kernel (attn_bwd_fused.hip): 32-key blocks x group ranges
   int64_t fused_tiles = 0, fused_uniform = 0;
+  bool fused_ok = false;  // the fused dK/dV + dBias kernel serves this geometry (sizes its workspace)
   int fused_parts = 1;
   int64_t fused_part_groups = 1;
   int64_t fused_max_len_q = 0;                   // longest sample the fused kernel serves

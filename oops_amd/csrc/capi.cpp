@@ -233,6 +233,7 @@ int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
       plan.bf_bytes = bytes;
     }
   }
+  plan.fused_ok = oops::dkvb_fused_ok(*geo, plan);
   return OOPS_OK;
 }
 
@@ -241,11 +242,13 @@ size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 // Backward workspace: delta [lse_extent f32] | LSE/delta pack [2 lse_extent f32] and compact
 // Q, dO [2 lse_extent kCompactRow 16-bit] (fused dK/dV + dBias kernel) | dBias partial slabs |
 // bias fragment copy.
+// (only when the fused dK/dV + dBias kernel serves the geometry: 8 bytes of pack and
+// 4 kCompactRow = 128 bytes of compact Q and dO per (sample, group, head, query) row)
 size_t pack_bytes(const oops::Plan& plan) {
-  return plan.fused_tiles > 0 ? align256(sizeof(float) * 2 * (size_t)plan.lse_extent) : 0;
+  return plan.fused_ok ? align256(sizeof(float) * 2 * (size_t)plan.lse_extent) : 0;
 }
 size_t compact_bytes(const oops::Plan& plan) {
-  return plan.fused_tiles > 0 ? align256(2 * sizeof(uint16_t) * (size_t)plan.lse_extent * oops::kCompactRow) : 0;
+  return plan.fused_ok ? align256(2 * sizeof(uint16_t) * (size_t)plan.lse_extent * oops::kCompactRow) : 0;
 }
 
 size_t parts_bytes(const oops::Plan& plan) {
@@ -402,7 +405,14 @@ int oops_attn_forward_noalloc(const oops_attn_geometry* geo, const void* q, cons
   g_last_error.clear();
   oops::Plan plan;
   if (int rc = make_plan(geo, plan)) return rc;
-  const size_t need = forward_workspace_bytes(plan);
+  size_t need = forward_workspace_bytes(plan);
+  if (need > kNoAllocScratchBytes) {
+    // The fragment-major bias copy is the only scratch the forward uses, and
+    // it is an optimisation: without it the kernels read the bias rows.
+    plan.bias_frag = false;
+    plan.bf_bytes = 0;
+    need = forward_workspace_bytes(plan);
+  }
   if (need > kNoAllocScratchBytes)
     return fail(OOPS_EWORKSPACE, "this geometry needs %lld bytes of scratch; the no-allocation forward has %lld",
                 (long long)need, (long long)kNoAllocScratchBytes);

@@ -150,7 +150,12 @@ def layer_norm_backward(
 
     lib = _lib.load()
     rows, width = x.shape
-    dy = dy.resolve_neg().to(x.dtype).reshape(rows, width).contiguous()
+    if dy.is_neg():
+        dy = dy.resolve_neg()
+    if dy.dtype != x.dtype:
+        dy = dy.to(x.dtype)
+    if dy.dim() != 2 or not dy.is_contiguous():
+        dy = dy.reshape(rows, width).contiguous()
     geo = _geometry(x.dtype, rows, width, x.stride(0) if rows > 1 else width, eps)
     # grad_x is written with x's row stride
     dx = torch.empty_strided(x.shape, x.stride(), dtype=x.dtype, device=x.device)

@@ -200,15 +200,18 @@ def test_row_norm_and_trimul_validation(lib):
     assert lib.oops_trimul_output_norm_parts(ctypes.byref(tg)) >= 1
 
 
-def test_forward_noalloc_rejects_oversized_scratch(lib):
-    """The no-allocation forward refuses, on the host, a geometry whose bias copy exceeds its static scratch."""
+def test_forward_noalloc_scratch_limit(lib):
+    """A geometry whose bias copy exceeds the no-allocation forward's static scratch is not refused: that
+    forward then reads the bias rows directly and needs no scratch (here, with no GPU, the launch itself
+    fails, after the host checks)."""
 
     text = HEADER.read_text()
     assert int(re.search(r"#define\s+OOPS_NOALLOC_SCRATCH_BYTES\s+(\d+)", text).group(1)) == _lib.NOALLOC_SCRATCH_BYTES
     geo, keep = _geometry(c3_table(n=2080))
     assert lib.oops_attn_forward_workspace_bytes(ctypes.byref(geo)) > _lib.NOALLOC_SCRATCH_BYTES
-    assert lib.oops_attn_forward_noalloc(ctypes.byref(geo), 1, 1, 1, None, 1, 1, None, 1, None) == 3
-    assert "scratch" in lib.oops_last_error().decode()
+    rc = lib.oops_attn_forward_noalloc(ctypes.byref(geo), 1, 1, 1, None, 1, 1, None, 1, None)
+    assert rc not in (0, 3), rc  # 3: OOPS_EWORKSPACE
+    assert "scratch" not in lib.oops_last_error().decode()
     # pointer checks come before any device call
     geo, keep = _geometry(c3_table())
     assert lib.oops_attn_forward_noalloc(ctypes.byref(geo), None, 1, 1, None, 1, 1, None, 1, None) == 1
