@@ -188,7 +188,7 @@ def measured_mfma():
         return out
     for ln in lines:
         parts = ln.split()
-        if len(parts) == 2 and not ln.startswith("#"):
+        if len(parts) >= 2 and not ln.startswith("#"):
             out[parts[0]] = float(parts[1])
     return out
 
