@@ -239,6 +239,17 @@ size_t oops_layer_norm_rows_parts(const oops_row_norm_geometry* geo);
 int oops_layer_norm_rows_backward(const oops_row_norm_geometry* geo, const void* x, const float* weight,
                                   const float* mean, const float* rstd, const void* grad_y, void* grad_x,
                                   float* grad_weight_parts, float* grad_bias_parts, void* stream);
+/* The same backward with the affine gradients summed in the library: grad_weight and grad_bias receive
+ * `width` float32 sums each (either may be NULL), added up in a fixed order (bit-identical on every call).
+ * The partials and their chunk sums live in the caller's workspace of
+ * oops_layer_norm_rows_backward_workspace_bytes bytes (256-byte aligned; NULL when both gradients are NULL).
+ * Replaces the reference's backward with its affine reduction kernel
+ * (oops/normalization/layer_norm/triton/kernel.py:100-163 and :236-268). */
+size_t oops_layer_norm_rows_backward_workspace_bytes(const oops_row_norm_geometry* geo);
+int oops_layer_norm_rows_backward_affine(const oops_row_norm_geometry* geo, const void* x, const float* weight,
+                                         const float* mean, const float* rstd, const void* grad_y, void* grad_x,
+                                         float* grad_weight, float* grad_bias, void* workspace, size_t ws_bytes,
+                                         void* stream);
 
 /* ---- triangle multiplicative update (oops/pair/triangle_multiplication) ----
  *

@@ -19,7 +19,7 @@ BIAS_NONE, BIAS_FULL, BIAS_SHARED = 0, 1, 2
 NOALLOC_SCRATCH_BYTES = 32 << 20
 PHASE_DELTA, PHASE_DQ, PHASE_DKV, PHASE_DBIAS = 1, 2, 4, 8
 TABLE_WIDTH = 40
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # geometry table columns (enum oops_table_column)
 (
@@ -48,6 +48,8 @@ EXPORTED_SYMBOLS = (
     "oops_layer_norm_rows_forward",
     "oops_layer_norm_rows_parts",
     "oops_layer_norm_rows_backward",
+    "oops_layer_norm_rows_backward_workspace_bytes",
+    "oops_layer_norm_rows_backward_affine",
     "oops_trimul_factors_forward",
     "oops_trimul_mask_parts",
     "oops_trimul_bias_parts",
@@ -191,6 +193,10 @@ def load() -> ctypes.CDLL:
         lib.oops_layer_norm_rows_parts.restype = sz
         lib.oops_layer_norm_rows_backward.argtypes = [rg, vp, vp, vp, vp, vp, vp, vp, vp, vp]
         lib.oops_layer_norm_rows_backward.restype = i32
+        lib.oops_layer_norm_rows_backward_workspace_bytes.argtypes = [rg]
+        lib.oops_layer_norm_rows_backward_workspace_bytes.restype = sz
+        lib.oops_layer_norm_rows_backward_affine.argtypes = [rg, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
+        lib.oops_layer_norm_rows_backward_affine.restype = i32
         tg = ctypes.POINTER(TrimulGeometry)
         lib.oops_trimul_factors_forward.argtypes = [tg, vp, vp, vp, vp, vp, vp]
         lib.oops_trimul_factors_forward.restype = i32

@@ -378,7 +378,7 @@ int run_forward(const oops_attn_geometry* geo, const oops::Plan& plan, const voi
 
 extern "C" {
 
-int oops_abi_version(void) { return 5; }
+int oops_abi_version(void) { return 6; }
 
 const char* oops_last_error(void) { return g_last_error.c_str(); }
 
@@ -521,6 +521,57 @@ int oops_layer_norm_rows_backward(const oops_row_norm_geometry* geo, const void*
                                                                   grad_weight_parts, grad_bias_parts,
                                                                   static_cast<hipStream_t>(stream)),
                             "row LayerNorm backward");
+}
+
+namespace {
+// the two float32 partial arrays [parts][width] the backward kernel writes,
+// as the segments of the fixed-order sums into the final gradients
+int ln_affine_segments(const oops_row_norm_geometry& g, float* parts, float* grad_weight, float* grad_bias,
+                       oops_sum_segment (&seg)[2]) {
+  const int64_t P = oops::layer_norm_rows_parts(g), W = g.width;
+  int n = 0;
+  if (grad_weight) seg[n++] = oops_sum_segment{parts, grad_weight, P, W, W, OOPS_F32, 0};
+  if (grad_bias) seg[n++] = oops_sum_segment{parts + P * W, grad_bias, P, W, W, OOPS_F32, 0};
+  return n;
+}
+size_t ln_parts_bytes(const oops_row_norm_geometry& g) {
+  return align256((size_t)2 * (size_t)oops::layer_norm_rows_parts(g) * (size_t)g.width * sizeof(float));
+}
+}  // namespace
+
+size_t oops_layer_norm_rows_backward_workspace_bytes(const oops_row_norm_geometry* geo) {
+  if (check_row_norm(geo)) return 0;
+  oops_sum_segment seg[2];
+  float one = 0.f;
+  const int n = ln_affine_segments(*geo, nullptr, &one, &one, seg);
+  return ln_parts_bytes(*geo) + oops::sum_partials_workspace_bytes(seg, n);
+}
+
+int oops_layer_norm_rows_backward_affine(const oops_row_norm_geometry* geo, const void* x, const float* weight,
+                                         const float* mean, const float* rstd, const void* grad_y, void* grad_x,
+                                         float* grad_weight, float* grad_bias, void* workspace, size_t ws_bytes,
+                                         void* stream) {
+  g_last_error.clear();
+  if (int rc = check_row_norm(geo)) return rc;
+  if (!x || !mean || !rstd || !grad_y || !grad_x)
+    return fail(OOPS_EINVAL, "x, mean, rstd, grad_y and grad_x must be non-NULL");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (!grad_weight && !grad_bias)
+    return gate_launch_result(oops::launch_layer_norm_rows_backward(*geo, x, weight, mean, rstd, grad_y, grad_x,
+                                                                    nullptr, nullptr, st),
+                              "row LayerNorm backward");
+  if (int rc = check_workspace(workspace, ws_bytes, oops_layer_norm_rows_backward_workspace_bytes(geo))) return rc;
+  float* parts = static_cast<float*>(workspace);
+  const int64_t pw = oops::layer_norm_rows_parts(*geo) * geo->width;
+  hipError_t e = oops::launch_layer_norm_rows_backward(*geo, x, weight, mean, rstd, grad_y, grad_x,
+                                                       grad_weight ? parts : nullptr, grad_bias ? parts + pw : nullptr,
+                                                       st);
+  if (e == hipSuccess && geo->rows > 0) {
+    oops_sum_segment seg[2];
+    const int n = ln_affine_segments(*geo, parts, grad_weight, grad_bias, seg);
+    e = oops::launch_sum_partials(seg, n, static_cast<char*>(workspace) + ln_parts_bytes(*geo), st);
+  }
+  return gate_launch_result(e, "row LayerNorm backward");
 }
 
 int oops_trimul_factors_forward(const oops_trimul_geometry* geo, const void* normalized, const void* weight,

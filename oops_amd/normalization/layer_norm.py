@@ -5,14 +5,17 @@ Drop-in for the reference's operator
 nested input whose normalized (final) axis is static and physically last,
 float16 / bfloat16 / float32 activations, widths 1-8192, optional affine parameters in the
 activation dtype (or float32 over half activations).  Forward and backward run
-in ``row_norm_*_kernel`` behind ``oops_layer_norm_rows_forward/backward``
-(float32 statistics, biased variance); the affine gradients are float32
-per-wave partials summed once and returned in the parameters' dtype.
+in ``row_norm_*_kernel`` behind ``oops_layer_norm_rows_forward`` and
+``oops_layer_norm_rows_backward_affine`` (float32 statistics, biased
+variance); the affine gradients are float32 per-wave partials that the library
+sums in a fixed order, returned in the parameters' dtype.
 """
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
+import functools
 import math
 from typing import Iterable, Optional, Tuple, Union
 
@@ -117,23 +120,65 @@ def _ptr(t: Optional[Tensor]) -> Optional[int]:
     return None if t is None or t.numel() == 0 else t.data_ptr()
 
 
-@torch.library.custom_op("oops_amd::layer_norm_forward", mutates_args=(), device_types="cuda")
-def layer_norm_forward(
-    x: Tensor, weight: Optional[Tensor], bias: Optional[Tensor], eps: float
-) -> Tuple[Tensor, Tensor, Tensor]:
-    """Rows ``x`` (rows, width) with unit column stride; float32 affine.  Returns (y, mean, rstd)."""
+@functools.lru_cache(maxsize=64)
+def _backward_workspace_bytes(lib, dtype, rows: int, width: int, x_row: int) -> int:
+    return lib.oops_layer_norm_rows_backward_workspace_bytes(ctypes.byref(_geometry(dtype, rows, width, x_row, 0.0)))
 
+
+def _on_device(device):
+    """The device context of a launch (a no-op when that device is already current)."""
+
+    return contextlib.nullcontext() if device.index == torch.cuda.current_device() else torch.cuda.device(device)
+
+
+def _forward_impl(x: Tensor, weight: Optional[Tensor], bias: Optional[Tensor], eps: float) -> Tuple[Tensor, Tensor, Tensor]:
     lib = _lib.load()
     rows, width = x.shape
     y = torch.empty(rows, width, dtype=x.dtype, device=x.device)
     mean = torch.empty(rows, dtype=torch.float32, device=x.device)
     rstd = torch.empty_like(mean)
     geo = _geometry(x.dtype, rows, width, x.stride(0) if rows > 1 else width, eps)
-    with torch.cuda.device(x.device):
+    with _on_device(x.device):
         rc = lib.oops_layer_norm_rows_forward(ctypes.byref(geo), _ptr(x), _ptr(weight), _ptr(bias), _ptr(y),
                                               _ptr(mean), _ptr(rstd), torch.cuda.current_stream().cuda_stream)
     _lib.check(rc, "layer_norm forward")
     return y, mean, rstd
+
+
+def _backward_impl(dy: Tensor, x: Tensor, weight: Optional[Tensor], mean: Tensor, rstd: Tensor, eps: float,
+                   need_affine: bool) -> Tuple[Tensor, Tensor, Tensor]:  # fmt: skip
+    lib = _lib.load()
+    rows, width = x.shape
+    if dy.is_neg():
+        dy = dy.resolve_neg()
+    if dy.dtype != x.dtype:
+        dy = dy.to(x.dtype)
+    if dy.dim() != 2 or not dy.is_contiguous():
+        dy = dy.reshape(rows, width).contiguous()
+    geo = _geometry(x.dtype, rows, width, x.stride(0) if rows > 1 else width, eps)
+    # grad_x is written with x's row stride
+    dx = torch.empty_strided(x.shape, x.stride(), dtype=x.dtype, device=x.device)
+    n = width if need_affine else 0
+    dw = torch.empty(n, dtype=torch.float32, device=x.device)
+    db = torch.empty(n, dtype=torch.float32, device=x.device)
+    ws_bytes = _backward_workspace_bytes(lib, x.dtype, rows, width, geo.x_row) if need_affine else 0
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+    with _on_device(x.device):
+        # the affine gradients are summed in the library, in a fixed order
+        rc = lib.oops_layer_norm_rows_backward_affine(ctypes.byref(geo), _ptr(x), _ptr(weight), _ptr(mean),
+                                                      _ptr(rstd), _ptr(dy), _ptr(dx), _ptr(dw), _ptr(db), _ptr(ws),
+                                                      ws_bytes, torch.cuda.current_stream().cuda_stream)  # fmt: skip
+    _lib.check(rc, "layer_norm backward")
+    return dx, dw, db
+
+
+@torch.library.custom_op("oops_amd::layer_norm_forward", mutates_args=(), device_types="cuda")
+def layer_norm_forward(
+    x: Tensor, weight: Optional[Tensor], bias: Optional[Tensor], eps: float
+) -> Tuple[Tensor, Tensor, Tensor]:
+    """Rows ``x`` (rows, width) with unit column stride; float32 affine.  Returns (y, mean, rstd)."""
+
+    return _forward_impl(x, weight, bias, eps)
 
 
 @layer_norm_forward.register_fake
@@ -148,30 +193,7 @@ def layer_norm_backward(
 ) -> Tuple[Tensor, Tensor, Tensor]:
     """(dx, dweight, dbias); the affine gradients are float32 (empty when not needed)."""
 
-    lib = _lib.load()
-    rows, width = x.shape
-    if dy.is_neg():
-        dy = dy.resolve_neg()
-    if dy.dtype != x.dtype:
-        dy = dy.to(x.dtype)
-    if dy.dim() != 2 or not dy.is_contiguous():
-        dy = dy.reshape(rows, width).contiguous()
-    geo = _geometry(x.dtype, rows, width, x.stride(0) if rows > 1 else width, eps)
-    # grad_x is written with x's row stride
-    dx = torch.empty_strided(x.shape, x.stride(), dtype=x.dtype, device=x.device)
-    acc = None
-    if need_affine:
-        acc = torch.empty(2, lib.oops_layer_norm_rows_parts(ctypes.byref(geo)), width, dtype=torch.float32,
-                          device=x.device)  # fmt: skip
-    with torch.cuda.device(x.device):
-        rc = lib.oops_layer_norm_rows_backward(ctypes.byref(geo), _ptr(x), _ptr(weight), _ptr(mean), _ptr(rstd),
-                                               _ptr(dy), _ptr(dx), None if acc is None else acc[0].data_ptr(),
-                                               None if acc is None else acc[1].data_ptr(),
-                                               torch.cuda.current_stream().cuda_stream)  # fmt: skip
-    _lib.check(rc, "layer_norm backward")
-    if acc is None:
-        return dx, x.new_empty(0, dtype=torch.float32), x.new_empty(0, dtype=torch.float32)
-    return dx, acc[0].sum(0), acc[1].sum(0)
+    return _backward_impl(dy, x, weight, mean, rstd, eps, need_affine)
 
 
 @layer_norm_backward.register_fake
@@ -192,18 +214,43 @@ def _setup_context(ctx, inputs, output):
     ctx.set_materialize_grads(False)  # no zero-filled gradients for mean and rstd
 
 
-def _backward(ctx, dy, _dmean, _drstd):
-    if dy is None:
-        return None, None, None, None
+def _grads(ctx, dy, backward):
     x, weight, mean, rstd = ctx.saved_tensors
     need = ctx.needs_input_grad
     need_affine = bool(need[1] or need[2])
-    dx, dw, db = layer_norm_backward(dy, x, weight, mean, rstd, ctx.eps, need_affine)
+    dx, dw, db = backward(dy, x, weight, mean, rstd, ctx.eps, need_affine)
     return (dx if need[0] else None, dw if ctx.has[0] and need[1] else None,
             db if ctx.has[1] and need[2] else None, None)  # fmt: skip
 
 
+def _backward(ctx, dy, _dmean, _drstd):
+    if dy is None:
+        return None, None, None, None
+    return _grads(ctx, dy, layer_norm_backward)
+
+
 layer_norm_forward.register_autograd(_backward, setup_context=_setup_context)
+
+
+class _EagerLayerNorm(torch.autograd.Function):
+    """The same kernels as the custom ops, for eager calls: autograd calls the
+    backward directly instead of through the operator dispatcher (about 25 us
+    of host time per op).  Traced code (torch.compile) takes the custom ops."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, eps):
+        y, mean, rstd = _forward_impl(x, weight, bias, eps)
+        ctx.save_for_backward(x, weight, mean, rstd)
+        ctx.eps = eps
+        ctx.has = (weight is not None, bias is not None)
+        ctx.set_materialize_grads(False)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        if dy is None:
+            return None, None, None, None
+        return _grads(ctx, dy, _backward_impl)
 
 
 def _apply(x: Tensor, weight: Optional[Tensor], bias: Optional[Tensor], eps: float) -> Tensor:
@@ -213,5 +260,8 @@ def _apply(x: Tensor, weight: Optional[Tensor], bias: Optional[Tensor], eps: flo
     if x2.stride(1) != 1 or (rows > 1 and x2.stride(0) < width):
         x2 = x2.contiguous()
     f32 = lambda t: None if t is None else t.resolve_neg().float().contiguous()  # noqa: E731
-    y, _, _ = layer_norm_forward(x2, f32(weight), f32(bias), eps)
+    if torch.compiler.is_compiling():
+        y, _, _ = layer_norm_forward(x2, f32(weight), f32(bias), eps)
+    else:
+        y = _EagerLayerNorm.apply(x2, f32(weight), f32(bias), eps)
     return y.view(x.shape)

@@ -183,6 +183,15 @@ def test_row_norm_and_trimul_validation(lib):
     assert lib.oops_layer_norm_rows_forward(ctypes.byref(rg), fake, None, None, fake, fake, fake, None) != 0
     rg.width, rg.y_row, rg.x_row = 9000, 9000, 9000
     assert lib.oops_layer_norm_rows_parts(ctypes.byref(rg)) == 0
+    assert lib.oops_layer_norm_rows_backward_workspace_bytes(ctypes.byref(rg)) == 0
+    rg.width, rg.y_row, rg.x_row, rg.rows = 128, 128, 128, 1 << 18
+    parts = lib.oops_layer_norm_rows_parts(ctypes.byref(rg))
+    need = lib.oops_layer_norm_rows_backward_workspace_bytes(ctypes.byref(rg))
+    assert need >= 2 * parts * 128 * 4 and need % 256 == 0
+    # the summed backward needs the workspace when an affine gradient is asked for
+    rc = lib.oops_layer_norm_rows_backward_affine(ctypes.byref(rg), fake, None, fake, fake, fake, fake, fake, None,
+                                                  None, 0, None)  # fmt: skip
+    assert rc == 3 and b"workspace" in lib.oops_last_error()
 
     tg = _lib.TrimulGeometry()
     tg.dtype, tg.channels, tg.hidden, tg.has_mask = 7, 16, 16, 0  # no such dtype

@@ -149,3 +149,52 @@ def test_layer_norm_module():
     m2 = LayerNorm((5, 96)).to(DEV)
     x2 = torch.randn(2, 5, 96, device=DEV)
     torch.testing.assert_close(m2(x2), torch.nn.functional.layer_norm(x2, (5, 96), m2.weight, m2.bias))
+
+
+def test_layer_norm_backward_affine_abi():
+    """oops_layer_norm_rows_backward_affine: the backward with the affine gradients summed in the library.
+    dx equals the partial-writing entry point's bit for bit; the sums equal a float64 sum of its partials,
+    and repeated calls are bit-identical (fixed summation order, two launches of chunk sums here)."""
+
+    import ctypes
+    import importlib
+
+    from oops_amd import _lib
+
+    ln = importlib.import_module("oops_amd.normalization.layer_norm")
+    lib = _lib.load()
+    rows, width = 1 << 17, 128
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(rows, width, generator=g).to(torch.bfloat16).to(DEV)
+    w = torch.randn(width, generator=g).to(DEV)
+    dy = torch.randn(rows, width, generator=g).to(torch.bfloat16).to(DEV)
+    _, mean, rstd = ln.layer_norm_forward(x, w, None, 1e-5)
+    geo = ln._geometry(x.dtype, rows, width, width, 1e-5)
+    parts = lib.oops_layer_norm_rows_parts(ctypes.byref(geo))
+    assert parts > 256, "the chunked (two-launch) sum is the case under test"
+    stream = torch.cuda.current_stream().cuda_stream
+    acc = torch.empty(2, parts, width, device=DEV)
+    dx_ref = torch.empty_like(x)
+    rc = lib.oops_layer_norm_rows_backward(ctypes.byref(geo), x.data_ptr(), w.data_ptr(), mean.data_ptr(),
+                                           rstd.data_ptr(), dy.data_ptr(), dx_ref.data_ptr(), acc[0].data_ptr(),
+                                           acc[1].data_ptr(), stream)  # fmt: skip
+    assert rc == 0, lib.oops_last_error()
+    need = lib.oops_layer_norm_rows_backward_workspace_bytes(ctypes.byref(geo))
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    outs = []
+    for _ in range(2):
+        dx = torch.full_like(x, float("nan"))
+        dw, db = torch.full((width,), float("nan"), device=DEV), torch.full((width,), float("nan"), device=DEV)
+        rc = lib.oops_layer_norm_rows_backward_affine(ctypes.byref(geo), x.data_ptr(), w.data_ptr(), mean.data_ptr(),
+                                                      rstd.data_ptr(), dy.data_ptr(), dx.data_ptr(), dw.data_ptr(),
+                                                      db.data_ptr(), ws.data_ptr(), need, stream)  # fmt: skip
+        assert rc == 0, lib.oops_last_error()
+        outs.append((dx, dw, db))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], dx_ref)
+    want = acc.double().sum(1)
+    for got, ref, name in ((outs[0][1], want[0], "dweight"), (outs[0][2], want[1], "dbias")):
+        err = (got.double() - ref).abs().max().item()
+        assert err <= 1e-5 * max(1.0, ref.abs().max().item()), f"{name}: {err:.3g}"
+    for a, b in zip(outs[0], outs[1]):
+        assert torch.equal(a, b)
