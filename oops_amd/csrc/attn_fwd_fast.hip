@@ -109,8 +109,9 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
   const bool has_mask = a.mask != nullptr && S.m_off >= 0;
   const uint8_t* mbase = has_mask ? a.mask + S.m_off + g * S.m_sg : nullptr;
 
-  // ---- per 64-key tile keep bitmaps (bit i: key 64t+i in range and kept)
-  for (int t = wave; t < ntiles; t += 4) {
+  // ---- per 64-key tile keep bitmaps (bit i: key 64t+i in range and kept);
+  // without mixed tiles (no mask, Lk a multiple of 64) every tile is whole
+  if constexpr (MASKED_TILES) for (int t = wave; t < ntiles; t += 4) {
     const int key = t * 64 + lane;
     bool keep = key < Lk;
     if (keep && has_mask) keep = mbase[key] != 0;
@@ -146,6 +147,8 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
   // chunk (l % CPR) ^ swz(row).  The step adds k0 * stride via soffset.
   const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kbase, (uint32_t)(((int64_t)(Lk - 1) * k_si + D) * 2));
   const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vbase, (uint32_t)(((int64_t)(Lk - 1) * v_si + D) * 2));
+  // empty ranges: the loads of an absent tile (t >= ntiles) read zeros and make no memory request
+  const __amdgpu_buffer_rsrc_t k_none = make_rsrc(kbase, 0u), v_none = make_rsrc(vbase, 0u);
   int d_row[IPW];
   uint32_t k_off[IPW], v_off[IPW];
 #pragma unroll
@@ -160,7 +163,7 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
   // bias fragments: from the fragment-major copy of a shared bias (one
   // contiguous 1 KB load per fragment), else from the bias rows themselves
   const bool use_bf = HAS_BIAS && a.bias_frag != nullptr && S.bias_mode == OOPS_BIAS_SHARED;
-  __amdgpu_buffer_rsrc_t b_rsrc;
+  __amdgpu_buffer_rsrc_t b_rsrc, b_none;
   uint32_t b_off[2][2], b_step;
   if (use_bf) {
     const int qt = qb * 4 + wave;
@@ -169,6 +172,7 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
     b_rsrc = make_rsrc(a.bias_frag + s_idx * a.bf_sample_stride +
                            (((int64_t)h * a.bf_nqt + (in ? qt : 0)) * a.bf_nkt) * 1024,
                        in ? (uint32_t)(a.bf_nkt * 2048) : 0u);
+    b_none = make_rsrc(a.bias_frag, 0u);
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
@@ -177,6 +181,7 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
   } else {
     const T* bbase = HAS_BIAS ? a.bias + S.b_off + g * S.b_sg + h * S.b_sh : a.q;
     b_rsrc = make_rsrc(bbase, HAS_BIAS ? (uint32_t)(((int64_t)(Lq - 1) * b_si + Lk) * 2) : 0u);
+    b_none = make_rsrc(bbase, 0u);
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
@@ -190,8 +195,19 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
   // no memory traffic, and no branch, so the compiler can count outstanding
   // loads exactly and never has to wait for all of them.
   auto load_kv = [&](int t, auto bc) {
-    const uint64_t bits = t < ntiles ? keep_lds[t < ntiles ? t : 0] : 0;
     const uint32_t ks = (uint32_t)(t * 64 * k_si * 2), vs = (uint32_t)(t * 64 * v_si * 2);
+    if constexpr (!MASKED_TILES) {
+      // whole tiles: the per-lane offsets are fixed, an absent tile takes the empty ranges
+      const bool live = t < ntiles;
+#pragma unroll
+      for (int i = 0; i < IPW; ++i) {
+        const int r0 = 16 * wave + i * RPI;
+        dma16(live ? k_rsrc : k_none, kbuf(bc) + r0 * DP, k_off[i], ks);
+        dma16(live ? v_rsrc : v_none, vbuf(bc) + r0 * DP, v_off[i], vs);
+      }
+      return;
+    }
+    const uint64_t bits = t < ntiles ? keep_lds[t < ntiles ? t : 0] : 0;
     const bool full = bits == ~uint64_t(0);
 #pragma unroll
     for (int i = 0; i < IPW; ++i) {
@@ -207,6 +223,16 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
   // covers the vector offset, which keeps the last row's tail in bounds)
   auto load_bias = [&](int t, uint4 (&bf)[2][2]) {
     const uint32_t s = (uint32_t)t * b_step;
+    if (!MASKED_TILES && use_bf) {
+      // whole tiles of the fragment-major copy: the tile offset is a scalar
+      // offset (every tile lies inside the range), an absent tile reads the empty range
+      const __amdgpu_buffer_rsrc_t r = t < ntiles ? b_rsrc : b_none;
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) bf[t2][c] = buffer_load16_s(r, b_off[t2][c], s);
+      return;
+    }
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
@@ -231,8 +257,9 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
     }
   };
 
-  __syncthreads();  // keep bitmaps visible
+  if constexpr (MASKED_TILES) __syncthreads();  // keep bitmaps visible
   auto next_tile = [&](int t) {
+    if constexpr (!MASKED_TILES) return t + 1 < ntiles ? t + 1 : ntiles;
     if (t >= ntiles) return ntiles;
     ++t;
     while (t < ntiles && keep_lds[t] == 0) ++t;
@@ -241,6 +268,7 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
 
   const float c1 = a.scale * kLog2e;
   float m_run = kNegInf;  // reference max (log2 units), raised lazily
+  float neg_m = 0.0f;     // -m_run (0 while no key has been seen)
   float l_run = 0.0f;     // this lane's partial row sum
   f32x16 oacc[NDT];
 #pragma unroll
@@ -278,14 +306,13 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
       const float m_new = grow ? mx : m_run;
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       m_run = m_new;
+      neg_m = m_run == kNegInf ? 0.0f : -m_run;
       l_run *= alpha;
 #pragma unroll
       for (int t = 0; t < NDT; ++t) oacc[t] *= alpha;
     }
-    const float neg_m = m_run == kNegInf ? 0.0f : -m_run;
-    // row sum in four independent chains, added to l_run at the end
-    // (each chain's first v_dot2 adds to a literal zero: no register to clear)
-    float ls[4];
+    // the row sum: one v_dot2 chain into l_run (the exponentials between its
+    // links hide their latency; no chain registers to clear or add up)
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
@@ -296,7 +323,7 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
           P2 pr;
           pr[0] = (T)__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t2][8 * m + e], c1, neg_m));
           pr[1] = (T)__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t2][8 * m + e + 1], c1, neg_m));
-          ls[e >> 1] = Pair<T>::dot(pr, ones, t2 == 0 && m == 0 ? 0.0f : ls[e >> 1]);
+          l_run = Pair<T>::dot(pr, ones, l_run);
           pf[e] = pr[0];
           pf[e + 1] = pr[1];
         }
@@ -306,7 +333,6 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
           oacc[t] = E::mma(vf, pf, oacc[t]);
         }
       }
-    l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
   };
 
   // ---- pipeline.  Step i computes tile t0 from ring buffer i % kRing.  It
@@ -337,7 +363,7 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
   // the ring position is a compile-time constant in each of four unrolled steps
   auto step = [&](auto bc, auto bc_load) {
     const int t3 = next_tile(t2);
-    const uint64_t bits = keep_lds[t0];
+    const uint64_t bits = MASKED_TILES ? keep_lds[t0] : ~uint64_t(0);
     load_kv(t3, bc_load);
     scores(bc, bias_a, sacc);
     if constexpr (HAS_BIAS) load_bias(t1, bias_a);
