@@ -364,7 +364,8 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS> ? 4 : O
   const uint8_t* mbase = has_mask ? a.mask + S.m_off + g * S.m_sg : nullptr;
   const bool write_dbias = FULL_DBIAS && a.dbias != nullptr && S.bias_mode == OOPS_BIAS_FULL;
 
-  for (int t = wave; t < ntiles; t += 4) {
+  // keep bitmaps; without mixed tiles (no mask, Lk a multiple of 64) every tile is whole
+  if constexpr (MASKED_TILES) for (int t = wave; t < ntiles; t += 4) {
     const int key = t * 64 + lane;
     bool keep = key < Lk;
     if (keep && has_mask) keep = mbase[key] != 0;
@@ -433,9 +434,16 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS> ? 4 : O
         const T* oe = reinterpret_cast<const T*>(&ou);
         const T* le = reinterpret_cast<const T*>(&lu);
         const T* de = reinterpret_cast<const T*>(&du[i]);
+        // O dO + O_lo dO, two products per v_dot2 on the packed 16-bit pairs
         float s = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s += (E::to_f(oe[e]) + E::to_f(le[e])) * E::to_f(de[e]);
+        for (int e = 0; e < 8; e += 2) {
+          typename Pair<T>::v2 op, lp, dp;
+          op[0] = oe[e], op[1] = oe[e + 1];
+          lp[0] = le[e], lp[1] = le[e + 1];
+          dp[0] = de[e], dp[1] = de[e + 1];
+          s = Pair<T>::dot(lp, dp, Pair<T>::dot(op, dp, s));
+        }
 #pragma unroll
         for (int m = 1; m < LPR; m <<= 1) s += __shfl_xor(s, m);
         part[i] = s;
@@ -485,6 +493,8 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS> ? 4 : O
   const T* vbase = a.v + S.v_off + g * S.v_sg + h * S.v_sh;
   const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kbase, (uint32_t)(((int64_t)(Lk - 1) * k_si + D) * 2));
   const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vbase, (uint32_t)(((int64_t)(Lk - 1) * v_si + D) * 2));
+  // empty ranges: the loads of an absent tile (t >= ntiles) read zeros and make no memory request
+  const __amdgpu_buffer_rsrc_t k_none = make_rsrc(kbase, 0u), v_none = make_rsrc(vbase, 0u);
   uint32_t kv_row[NCH], k_off[NCH], v_off[NCH];
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
@@ -498,7 +508,7 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS> ? 4 : O
   // bias fragments: from the fragment-major copy of a shared bias (one
   // contiguous 1 KB load per fragment), else from the bias rows themselves
   const bool use_bf = HAS_BIAS && a.bias_frag != nullptr && S.bias_mode == OOPS_BIAS_SHARED;
-  __amdgpu_buffer_rsrc_t b_rsrc;
+  __amdgpu_buffer_rsrc_t b_rsrc, b_none;
   uint32_t b_off[2][2], b_step;
   if (use_bf) {
     const int qt = qb * 4 + wave;
@@ -506,6 +516,7 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS> ? 4 : O
     b_rsrc = make_rsrc(a.bias_frag + s_idx * a.bf_sample_stride +
                            (((int64_t)h * a.bf_nqt + (in ? qt : 0)) * a.bf_nkt) * 1024,
                        in ? (uint32_t)(a.bf_nkt * 2048) : 0u);
+    b_none = make_rsrc(a.bias_frag, 0u);
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
@@ -514,6 +525,7 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS> ? 4 : O
   } else {
     const T* bbase = HAS_BIAS ? a.bias + S.b_off + g * S.b_sg + h * S.b_sh : a.q;
     b_rsrc = make_rsrc(bbase, HAS_BIAS ? (uint32_t)(((int64_t)(Lq - 1) * b_si + Lk) * 2) : 0u);
+    b_none = make_rsrc(bbase, 0u);
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
@@ -528,8 +540,18 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS> ? 4 : O
   // no memory traffic, and no branch, so the compiler can count outstanding
   // loads exactly and never has to wait for all of them.
   auto load_kv = [&](int t, uint4 (&ku)[NCH], uint4 (&vu)[NCH]) {
-    const uint64_t bits = t < ntiles ? keep_lds[t < ntiles ? t : 0] : 0;
     const uint32_t ks = (uint32_t)(t * 64 * k_si * 2), vs = (uint32_t)(t * 64 * v_si * 2);
+    if constexpr (!MASKED_TILES) {
+      // whole tiles: fixed per-lane offsets, an absent tile takes the empty ranges
+      const bool live = t < ntiles;
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        ku[i] = buffer_load16_s(live ? k_rsrc : k_none, k_off[i], ks);
+        vu[i] = buffer_load16_s(live ? v_rsrc : v_none, v_off[i], vs);
+      }
+      return;
+    }
+    const uint64_t bits = t < ntiles ? keep_lds[t < ntiles ? t : 0] : 0;
     const bool full = bits == ~uint64_t(0);
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
@@ -550,6 +572,16 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS> ? 4 : O
   };
   auto load_bias = [&](int t, uint4 (&bf)[2][2]) {
     const uint32_t s = (uint32_t)t * b_step;
+    if (!MASKED_TILES && use_bf) {
+      // whole tiles of the fragment-major copy: the tile offset is a scalar
+      // offset (every tile lies inside the range), an absent tile reads the empty range
+      const __amdgpu_buffer_rsrc_t r = t < ntiles ? b_rsrc : b_none;
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) bf[t2][c] = buffer_load16_s(r, b_off[t2][c], s);
+      return;
+    }
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
@@ -558,6 +590,7 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS> ? 4 : O
 
   __syncthreads();
   auto next_tile = [&](int t) {
+    if constexpr (!MASKED_TILES) return t + 1 < ntiles ? t + 1 : ntiles;
     if (t >= ntiles) return ntiles;
     ++t;
     while (t < ntiles && keep_lds[t] == 0) ++t;
@@ -647,7 +680,7 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS> ? 4 : O
   int buf = 0;
   while (t0 < ntiles) {
     const int t3 = next_tile(t2);
-    const uint64_t bits = uniform64(keep_lds[t0]);
+    const uint64_t bits = MASKED_TILES ? uniform64(keep_lds[t0]) : ~uint64_t(0);
     const int b1 = buf == 2 ? 0 : buf + 1;
     const int b2 = b1 == 2 ? 0 : b1 + 1;
     if (t2 < ntiles) store_kv(b2, ku, vu);

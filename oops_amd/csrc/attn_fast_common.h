@@ -83,12 +83,19 @@ __device__ __forceinline__ void trade16(const uint32_t (&p)[8], uint4& lo, uint4
 // 16 entries 16c .. 16c+15 of the other operand's k axis, each times w.
 template <typename T>
 __device__ __forceinline__ void identity_frags(typename Elem<T>::Frag (&id)[2], float w, int lane) {
+  // element j of fragment c holds the weight when lq == 16 c + 8 g2 + j: the
+  // weight's 16 bits shifted into place within the dword that holds j
   const int lq = lane & 31, g2 = lane >> 5;
-  const T wt = (T)w;
+  const uint32_t wb = __builtin_bit_cast(uint16_t, (T)w);
 #pragma unroll
-  for (int c = 0; c < 2; ++c)
+  for (int c = 0; c < 2; ++c) {
+    const int j = lq - 16 * c - 8 * g2;  // in 0..7 for the one fragment that holds the weight
+    const uint32_t v = wb << ((j & 1) * 16);
+    uint32_t u[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) id[c][j] = (lq == 16 * c + g2 * 8 + j) ? wt : (T)0.0f;
+    for (int k = 0; k < 4; ++k) u[k] = (j >> 1) == k ? v : 0u;
+    id[c] = __builtin_bit_cast(typename Elem<T>::Frag, make_uint4(u[0], u[1], u[2], u[3]));
+  }
 }
 
 template <typename T>

@@ -133,13 +133,7 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
   }
   // identity A-fragments carrying the bias weight 1/scale: MFMA c adds bias keys 16c..16c+15
   Frag ident[2];
-  {
-    const T w = (T)(1.0f / a.scale);
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) ident[c][j] = (lq == 16 * c + g2 * 8 + j) ? w : (T)0.0f;
-  }
+  identity_frags<T>(ident, 1.0f / a.scale, lane);
 
   // ---- fixed per-lane offsets (bytes) of the direct-to-LDS tile loads:
   // wave w fills rows 16w .. 16w+15 of the K and V tiles; lane l writes slot
