@@ -310,16 +310,20 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
 // MASKED_TILES: the geometry may have 64-key tiles with masked or
 // out-of-range keys (else only the unmasked tile code is compiled);
 // FULL_DBIAS: some sample has a per-group bias whose dBias = dS is written
-// here.  Both only add code that costs registers when compiled in.
-// The lean instances (D <= 32, neither of the two) start dP from a register
-// tile of -delta instead of zero (one VALU add less per score) and are built
-// for four waves per SIMD, which the extra 16 registers still fit.
-template <int DP, bool MASKED_TILES, bool FULL_DBIAS>
-constexpr bool kLeanDq = DP == 32 && !MASKED_TILES && !FULL_DBIAS;
-template <typename T, int DP, bool HAS_BIAS, bool MASKED_TILES, bool FULL_DBIAS>
-__global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS> ? 4 : OOPS_DQ_OCC)) void attn_dq_fast_kernel(
+// here.  Both only add code that costs registers when compiled in.  FOLD
+// (bf16, bias, at most kFoldTiles key tiles): the key masks are folded into
+// the bias fragments (fold_bias) instead of selected per score.
+// The lean instances (D <= 32, no per-score mask code, no full dBias) start
+// dP from a register tile of -delta instead of zero (one VALU add less per
+// score) and are built for four waves per SIMD, which the extra 16 registers
+// still fit.
+template <int DP, bool MASKED_TILES, bool FULL_DBIAS, bool FOLD>
+constexpr bool kLeanDq = DP == 32 && (!MASKED_TILES || FOLD) && !FULL_DBIAS;
+template <typename T, int DP, bool HAS_BIAS, bool MASKED_TILES, bool FULL_DBIAS, bool FOLD>
+__global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS, FOLD> ? 4 : OOPS_DQ_OCC)) void attn_dq_fast_kernel(
     BwdArgsT<T, T> a) {
-  constexpr bool LEAN = kLeanDq<DP, MASKED_TILES, FULL_DBIAS>;
+  constexpr bool LEAN = kLeanDq<DP, MASKED_TILES, FULL_DBIAS, FOLD>;
+  static_assert(!FOLD || (MASKED_TILES && HAS_BIAS && sizeof(T) == 2), "fold: masked bf16 tiles with a bias");
   using E = Elem<T>;
   using Frag = typename E::Frag;
   constexpr int LD = DP + 8;
@@ -332,6 +336,7 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS> ? 4 : O
   __shared__ __attribute__((aligned(16))) T v_lds[3 * TBUF];
   __shared__ uint64_t keep_lds[kMaxKeyTiles];
   __shared__ float dl_lds[4 * 32];
+  __shared__ __attribute__((aligned(16))) uint32_t fold_lds[FOLD ? kFoldTiles * 32 : 4];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -589,6 +594,8 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS> ? 4 : O
   };
 
   __syncthreads();
+  // (the fold table is read after the barrier that ends the prologue)
+  if constexpr (FOLD) build_fold_table(fold_lds, keep_lds, ntiles, tid, 256);
   auto next_tile = [&](int t) {
     if constexpr (!MASKED_TILES) return t + 1 < ntiles ? t + 1 : ntiles;
     if (t >= ntiles) return ntiles;
@@ -612,12 +619,15 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS> ? 4 : O
     const T* kt = &k_lds[buf * TBUF];
     const T* vt = &v_lds[buf * TBUF];
     const uint64_t lb = bits >> (g2 * 4);
+    const uint4* fm = reinterpret_cast<const uint4*>(&fold_lds[FOLD ? (t * 2 + g2) * 16 : 0]);
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
       f32x16 sacc;
       if constexpr (HAS_BIAS) {
-        sacc = E::mma(ident[0], __builtin_bit_cast(Frag, bf[t2][0]), f32x16{});
-        sacc = E::mma(ident[1], __builtin_bit_cast(Frag, bf[t2][1]), sacc);
+        const uint4 b0 = FOLD ? fold_bias(bf[t2][0], fm[t2 * 2]) : bf[t2][0];
+        const uint4 b1 = FOLD ? fold_bias(bf[t2][1], fm[t2 * 2 + 1]) : bf[t2][1];
+        sacc = E::mma(ident[0], __builtin_bit_cast(Frag, b0), f32x16{});
+        sacc = E::mma(ident[1], __builtin_bit_cast(Frag, b1), sacc);
       } else {
         sacc = f32x16{};
       }
@@ -685,9 +695,9 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS> ? 4 : O
     const int b2 = b1 == 2 ? 0 : b1 + 1;
     if (t2 < ntiles) store_kv(b2, ku, vu);
     load_kv(t3, ku, vu);
-    if (!MASKED_TILES || bits == ~uint64_t(0))
+    if (!MASKED_TILES || FOLD || bits == ~uint64_t(0))
       compute(std::false_type{}, buf, t0, bits, bias_a);
-    else if constexpr (MASKED_TILES)
+    else if constexpr (MASKED_TILES && !FOLD)
       compute(std::true_type{}, buf, t0, bits, bias_a);
     if constexpr (HAS_BIAS)
       load_bias(t1, bias_a);  // one register set: the next tile's bias
@@ -987,11 +997,11 @@ __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(Bw
   }
 }
 
-#define OOPS_DQ_FAST_INST(T, DP, B)                                                         \
-  template __global__ void attn_dq_fast_kernel<T, DP, B, false, false>(BwdArgsT<T, T>); \
-  template __global__ void attn_dq_fast_kernel<T, DP, B, true, false>(BwdArgsT<T, T>);  \
-  template __global__ void attn_dq_fast_kernel<T, DP, B, false, true>(BwdArgsT<T, T>);  \
-  template __global__ void attn_dq_fast_kernel<T, DP, B, true, true>(BwdArgsT<T, T>);
+#define OOPS_DQ_FAST_INST(T, DP, B)                                                                \
+  template __global__ void attn_dq_fast_kernel<T, DP, B, false, false, false>(BwdArgsT<T, T>); \
+  template __global__ void attn_dq_fast_kernel<T, DP, B, true, false, false>(BwdArgsT<T, T>);  \
+  template __global__ void attn_dq_fast_kernel<T, DP, B, false, true, false>(BwdArgsT<T, T>);  \
+  template __global__ void attn_dq_fast_kernel<T, DP, B, true, true, false>(BwdArgsT<T, T>);
 #define OOPS_BWD_FAST_INST(T, DP)                                                \
   template __global__ void attn_dkv_fast_kernel<T, DP, true, 1>(BwdArgsT<T, T>);  \
   template __global__ void attn_dkv_fast_kernel<T, DP, true, 2>(BwdArgsT<T, T>);  \
@@ -1002,6 +1012,8 @@ __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(Bw
   template __global__ void attn_dbias_fast_kernel<T, DP, true>(BwdArgsT<T, T>);
 OOPS_BWD_FAST_INST(__bf16, 32)
 OOPS_BWD_FAST_INST(__bf16, 64)
+template __global__ void attn_dq_fast_kernel<__bf16, 32, true, true, false, true>(BwdArgsT<__bf16, __bf16>);
+template __global__ void attn_dq_fast_kernel<__bf16, 64, true, true, false, true>(BwdArgsT<__bf16, __bf16>);
 OOPS_BWD_FAST_INST(_Float16, 32)
 OOPS_BWD_FAST_INST(_Float16, 64)
 
@@ -1064,14 +1076,17 @@ hipError_t launch_dq_fast(const oops_attn_geometry& geo, const Plan& plan, const
     a.fused_max_lq = L.qc != nullptr && plan.fused_split ? kFusedMaxLen : 0;
     const dim3 grid((unsigned)xcd_grid(plan.fwd_tiles, xcd_chunk(plan.fwd_uniform)));
     const bool full = a.dbias != nullptr && plan.any_full;
-    auto go = [&](auto has_bias, auto masked, auto full_db) {
+    auto go = [&](auto has_bias, auto masked, auto full_db, auto fold) {
       hipLaunchKernelGGL((attn_dq_fast_kernel<T, DP, decltype(has_bias)::value, decltype(masked)::value,
-                                              decltype(full_db)::value>),
+                                              decltype(full_db)::value, decltype(fold)::value>),
                          grid, dim3(256), 0, stream, a);
     };
     auto by_full = [&](auto has_bias, auto masked) {
-      if (full) go(has_bias, masked, std::true_type{});
-      else go(has_bias, masked, std::false_type{});
+      if constexpr (decltype(has_bias)::value && decltype(masked)::value && std::is_same_v<T, __bf16>) {
+        if (!full && fold_masks_ok(plan)) return go(has_bias, masked, std::false_type{}, std::true_type{});
+      }
+      if (full) go(has_bias, masked, std::true_type{}, std::false_type{});
+      else go(has_bias, masked, std::false_type{}, std::false_type{});
     };
     auto by_mask = [&](auto has_bias) {
       if (plan.masked_tiles) by_full(has_bias, std::true_type{});

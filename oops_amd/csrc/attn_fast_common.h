@@ -98,6 +98,33 @@ __device__ __forceinline__ void identity_frags(typename Elem<T>::Frag (&id)[2], 
   }
 }
 
+// Key masks folded into the bias operand of the identity MFMA (bf16, row-
+// shared key masks, at most kFoldTiles 64-key tiles): a masked key's bias
+// element becomes -3.39e38, so its logit is -inf or below -1e38 and its P
+// underflows to exactly 0 with no per-score select.  Every tile a kernel
+// visits has a kept key (fully masked tiles are skipped), so each row's
+// maximum is a kept key's.  Masked keys' K and V rows are still read as
+// zeros, so their products stay finite.  The fold table holds, per tile and
+// lane half g2, 16 dwords of 16-bit keep masks: dword (2 t2 + c) * 4 + k
+// covers keys 32 t2 + 16 c + 8 g2 + 2 k and + 1, the elements of dword k of
+// the bias fragment of 32-key tile t2 and chunk c.
+constexpr int kFoldTiles = 16;                // Lk <= 1024
+constexpr uint32_t kFoldNeg = 0xFF7FFF7Fu;    // two bf16 -3.39e38
+__device__ __forceinline__ void build_fold_table(uint32_t* tab, const uint64_t* keep, int ntiles, int tid,
+                                                 int nthreads) {
+  for (int e = tid; e < ntiles * 32; e += nthreads) {
+    const int t = e >> 5, g2 = (e >> 4) & 1, i = e & 15;
+    const int key0 = 32 * (i >> 3) + 16 * ((i >> 2) & 1) + 8 * g2 + 2 * (i & 3);
+    const uint64_t b = keep[t];
+    tab[e] = (((b >> key0) & 1) ? 0x0000FFFFu : 0u) | (((b >> (key0 + 1)) & 1) ? 0xFFFF0000u : 0u);
+  }
+}
+// bias fragment b with its masked keys' elements replaced (m: keep masks)
+__device__ __forceinline__ uint4 fold_bias(uint4 b, uint4 m) {
+  return make_uint4((b.x & m.x) | (~m.x & kFoldNeg), (b.y & m.y) | (~m.y & kFoldNeg),
+                    (b.z & m.z) | (~m.z & kFoldNeg), (b.w & m.w) | (~m.w & kFoldNeg));
+}
+
 template <typename T>
 __device__ __forceinline__ typename Elem<T>::Frag lds_frag(const T* p) {
   return __builtin_bit_cast(typename Elem<T>::Frag, *reinterpret_cast<const uint4*>(p));

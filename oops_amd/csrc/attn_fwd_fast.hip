@@ -45,8 +45,10 @@ constexpr int kRing = 4;  // K/V tile buffers in LDS
 
 // MASKED_TILES: the geometry may have 64-key tiles with masked or
 // out-of-range keys; without it the per-score mask code is not compiled
-// (it costs registers even when never executed).
-template <typename T, int DP, bool HAS_BIAS, bool MASKED_TILES>
+// (it costs registers even when never executed).  FOLD (bf16, bias, at most
+// kFoldTiles key tiles): the masks are folded into the bias fragments
+// instead of selected per score.
+template <typename T, int DP, bool HAS_BIAS, bool MASKED_TILES, bool FOLD>
 __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArgsT<T, T> a) {
   using E = Elem<T>;
   using Frag = typename E::Frag;
@@ -69,6 +71,8 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
   auto kbuf = [&](auto bc) -> T* { return k_lds + decltype(bc)::value * KT; };
   auto vbuf = [&](auto bc) -> T* { return v_lds + decltype(bc)::value * KT; };
   __shared__ uint64_t keep_lds[kMaxKeyTiles];
+  __shared__ __attribute__((aligned(16))) uint32_t fold_lds[FOLD ? kFoldTiles * 32 : 4];
+  static_assert(!FOLD || (MASKED_TILES && HAS_BIAS && sizeof(T) == 2), "fold: masked bf16 tiles with a bias");
 
   const int tid = threadIdx.x;
   const int wave = (tid >> 6) & 3;  // (& 3: lets the compiler bound LDS addresses)
@@ -233,12 +237,15 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
       for (int c = 0; c < 2; ++c) bf[t2][c] = buffer_load16_s(b_rsrc, t < ntiles ? b_off[t2][c] + s : kOut, 0);
   };
   // S^T of a tile (bias by identity MFMA, then Q K^T) from LDS buffer buf
-  auto scores = [&](auto bc, const uint4 (&bf)[2][2], f32x16 (&sacc)[2]) {
+  auto scores = [&](auto bc, int t, const uint4 (&bf)[2][2], f32x16 (&sacc)[2]) {
+    const uint4* fm = reinterpret_cast<const uint4*>(&fold_lds[FOLD ? (t * 2 + g2) * 16 : 0]);
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
       if constexpr (HAS_BIAS) {
-        sacc[t2] = E::mma(ident[0], __builtin_bit_cast(Frag, bf[t2][0]), f32x16{});
-        sacc[t2] = E::mma(ident[1], __builtin_bit_cast(Frag, bf[t2][1]), sacc[t2]);
+        const uint4 b0 = FOLD ? fold_bias(bf[t2][0], fm[t2 * 2]) : bf[t2][0];
+        const uint4 b1 = FOLD ? fold_bias(bf[t2][1], fm[t2 * 2 + 1]) : bf[t2][1];
+        sacc[t2] = E::mma(ident[0], __builtin_bit_cast(Frag, b0), f32x16{});
+        sacc[t2] = E::mma(ident[1], __builtin_bit_cast(Frag, b1), sacc[t2]);
       } else {
         sacc[t2] = f32x16{};
       }
@@ -252,6 +259,8 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
   };
 
   if constexpr (MASKED_TILES) __syncthreads();  // keep bitmaps visible
+  // (the fold table is read after the barrier that ends the prologue)
+  if constexpr (FOLD) build_fold_table(fold_lds, keep_lds, ntiles, tid, 256);
   auto next_tile = [&](int t) {
     if constexpr (!MASKED_TILES) return t + 1 < ntiles ? t + 1 : ntiles;
     if (t >= ntiles) return ntiles;
@@ -273,7 +282,7 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
 
   // softmax of one tile's scores + O^T += V^T P^T from LDS buffer buf
   auto attend = [&](auto bc, uint64_t bits, f32x16 (&sacc)[2]) {
-    if (MASKED_TILES && bits != ~uint64_t(0)) {
+    if (MASKED_TILES && !FOLD && bits != ~uint64_t(0)) {
       // mixed tile: masked / out-of-range keys get -inf
       const uint64_t lb = bits >> (g2 * 4);
 #pragma unroll
@@ -359,7 +368,7 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
     const int t3 = next_tile(t2);
     const uint64_t bits = MASKED_TILES ? keep_lds[t0] : ~uint64_t(0);
     load_kv(t3, bc_load);
-    scores(bc, bias_a, sacc);
+    scores(bc, t0, bias_a, sacc);
     if constexpr (HAS_BIAS) load_bias(t1, bias_a);
     attend(bc, bits, sacc);
     vmem_wait<2 * NDMA + (HAS_BIAS ? 12 : 0)>();
@@ -404,14 +413,18 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
 }
 
 #define OOPS_FWD_FAST_INST(T, DP)                                                       \
-  template __global__ void attn_fwd_fast_kernel<T, DP, true, false>(FwdArgsT<T, T>);  \
-  template __global__ void attn_fwd_fast_kernel<T, DP, true, true>(FwdArgsT<T, T>);   \
-  template __global__ void attn_fwd_fast_kernel<T, DP, false, false>(FwdArgsT<T, T>); \
-  template __global__ void attn_fwd_fast_kernel<T, DP, false, true>(FwdArgsT<T, T>);
+  template __global__ void attn_fwd_fast_kernel<T, DP, true, false, false>(FwdArgsT<T, T>);  \
+  template __global__ void attn_fwd_fast_kernel<T, DP, true, true, false>(FwdArgsT<T, T>);   \
+  template __global__ void attn_fwd_fast_kernel<T, DP, false, false, false>(FwdArgsT<T, T>); \
+  template __global__ void attn_fwd_fast_kernel<T, DP, false, true, false>(FwdArgsT<T, T>);
 OOPS_FWD_FAST_INST(__bf16, 32)
+template __global__ void attn_fwd_fast_kernel<__bf16, 32, true, true, true>(FwdArgsT<__bf16, __bf16>);
+template __global__ void attn_fwd_fast_kernel<__bf16, 64, true, true, true>(FwdArgsT<__bf16, __bf16>);
 OOPS_FWD_FAST_INST(__bf16, 64)
 OOPS_FWD_FAST_INST(_Float16, 32)
 OOPS_FWD_FAST_INST(_Float16, 64)
+
+bool fold_masks_ok(const Plan& plan) { return plan.max_len_k <= 64 * kFoldTiles; }
 
 bool fast_path_ok(const oops_attn_geometry& geo, const Plan& plan) {
   if (geo.force_generic == 1) return false;
@@ -508,13 +521,17 @@ bool launch_forward_fast(const oops_attn_geometry& geo, const Plan& plan, const 
     a.bf_nqt = plan.bf_nqt;
     a.bf_nkt = plan.bf_nkt;
     const dim3 grid((unsigned)xcd_grid(plan.fwd_tiles, xcd_chunk(plan.fwd_uniform)));
-    auto go = [&](auto has_bias, auto masked) {
-      hipLaunchKernelGGL((attn_fwd_fast_kernel<T, DP, decltype(has_bias)::value, decltype(masked)::value>), grid,
-                         dim3(256), 0, stream, a);
+    auto go = [&](auto has_bias, auto masked, auto fold) {
+      hipLaunchKernelGGL((attn_fwd_fast_kernel<T, DP, decltype(has_bias)::value, decltype(masked)::value,
+                                               decltype(fold)::value>),
+                         grid, dim3(256), 0, stream, a);
     };
     auto by_mask = [&](auto has_bias) {
-      if (plan.masked_tiles) go(has_bias, std::true_type{});
-      else go(has_bias, std::false_type{});
+      if constexpr (decltype(has_bias)::value && std::is_same_v<T, __bf16>) {
+        if (plan.masked_tiles && fold_masks_ok(plan)) return go(has_bias, std::true_type{}, std::true_type{});
+      }
+      if (plan.masked_tiles) go(has_bias, std::true_type{}, std::false_type{});
+      else go(has_bias, std::false_type{}, std::false_type{});
     };
     if (a.bias != nullptr) by_mask(std::true_type{});
     else by_mask(std::false_type{});

@@ -170,6 +170,8 @@ struct Plan {
 
 // True when the 16-bit fast kernels serve this geometry (forward and backward).
 bool fast_path_ok(const oops_attn_geometry& geo, const Plan& plan);
+// key masks may be folded into the bias fragments (every sample's keys fit the fold table)
+bool fold_masks_ok(const Plan& plan);
 
 // Writes the fragment-major copy of every shared bias of the table into bf
 // (plan.bf_bytes bytes); see attn_bias_frag_kernel.
