@@ -49,10 +49,15 @@ using namespace fast;
 namespace {
 
 constexpr int kFusedWaves = 8;
-constexpr int kRowWaves = 4;       // waves per group: two groups in flight
-constexpr int kFusedMaxSteps = 6;  // query tiles per wave and group: Lq <= 4 * 6 * 32
-constexpr int kFusedMaxQT = kRowWaves * kFusedMaxSteps;  // query tiles of the largest bias region
-static_assert(kFusedMaxQT * 32 == kFusedMaxLen, "the plan's length limit is the kernel's");
+// Two geometries of the workgroup: RW = 4 waves per group and two groups (two
+// rows) in flight, up to 6 query tiles per wave (Lq <= 768), with a 3-stage
+// ring; or RW = 8, all eight waves on one row, up to 4 query tiles per wave
+// (Lq <= 1024), with a 2-stage ring so that the 64 KB bias region still fits.
+constexpr int kFusedMaxSteps = 6;
+static_assert(4 * kFusedMaxSteps * 32 == kFusedMaxLen, "the plan's length limit is the kernel's");
+static_assert(8 * 4 * 32 == kFusedLongMaxLen, "the plan's long-sample limit is the kernel's");
+template <int RW>
+constexpr int kStages = RW == 4 ? 3 : 2;
 constexpr int kQT = 32 * 32;       // elements of one 32 x 32 tile
 
 // LDS byte address of p (a __shared__ object), as a wave-uniform value: the
@@ -105,32 +110,36 @@ struct RingStage {
   float ld[64];  // -LSE / c of the 32 queries, then -delta
 };
 
-template <typename T, bool MASKED, int NS>
+template <typename T, bool MASKED, int NS, int RW>
 __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a) {
   using E = Elem<T>;
   using Frag = typename E::Frag;
   static_assert(sizeof(T) == 2, "16-bit operands");
-  static_assert(NS >= 1 && NS <= kFusedMaxSteps, "query tiles per wave and group");
+  static_assert(RW == 4 || RW == 8, "waves per group");
+  static_assert(NS >= 1 && NS <= (RW == 4 ? kFusedMaxSteps : 4), "query tiles per wave and group");
+  constexpr int kRowWaves = RW;
+  constexpr int kGroups = kFusedWaves / RW;  // groups (rows) in flight
+  constexpr int NST = kStages<RW>;           // ring stages
 
-  // per-wave ring of three stages (two in flight while one is read); at a
+  // per-wave ring of NST stages (NST - 1 in flight while one is read); at a
   // pair's end a wave's just-read stage holds its dK/dV partials
-  __shared__ __attribute__((aligned(16))) RingStage ring_lds[3][kFusedWaves];
-  // K / V blocks of the pair's two groups: [group of the pair][K, V][32 keys][32]
-  __shared__ __attribute__((aligned(16))) T kv_lds[2 * 2 * 32 * 32];
+  __shared__ __attribute__((aligned(16))) RingStage ring_lds[NST][kFusedWaves];
+  // K / V blocks of the groups in flight: [group][K, V][32 keys][32]
+  __shared__ __attribute__((aligned(16))) T kv_lds[kGroups * 2 * 32 * 32];
   // the workgroup's bias region, identity-MFMA fragments of its 32 keys for
   // every query tile: [query tile][chunk c][64 lanes][8], loaded once per part
   __shared__ __attribute__((aligned(16))) T bias_lds[NS * kRowWaves * 2 * 64 * 8];
-  // keep bytes of the 32 keys of the pair's groups, per lane (lanes 32..63
-  // repeat 0..31): [group of the pair][64]
-  __shared__ uint32_t keep_lds[2][64];
+  // keep bytes of the 32 keys of the groups in flight, per lane (lanes 32..63
+  // repeat 0..31): [group][64]
+  __shared__ uint32_t keep_lds[kGroups][64];
 
   const int tid = threadIdx.x;
   // (readfirstlane: the wave index, and everything derived from it, is
   // wave-uniform and lives in scalar registers, e.g. the LDS base of the
   // direct-to-LDS loads, which must be a scalar)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int rs = wave >> 2;  // group of the pair this wave works on
-  const int wq = wave & 3;   // its quarter of the query tiles
+  const int rs = wave / RW;  // group (of the rows in flight) this wave works on
+  const int wq = wave % RW;  // its share of the query tiles
   const int lane = tid & 63;
   const int lq = lane & 31;
   const int g2 = lane >> 5;
@@ -150,8 +159,8 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   const int H = a.num_heads;
   const int s_idx = find_sample(tile, tab, a.num_samples, a.uniform_tiles, [&](const Sample& s) {
     // (a split batch: only the samples this kernel serves)
-    return a.fused_max_lq == 0 || s.Lq <= a.fused_max_lq ? (int64_t)H * cdiv(s.Lk, 32) * parts_for(s.G, a.part_groups, a.parts)
-                                                          : (int64_t)0;
+    const bool mine = (a.fused_max_lq == 0 || s.Lq <= a.fused_max_lq) && s.Lq > a.fused_min_lq;
+    return mine ? (int64_t)H * cdiv(s.Lk, 32) * parts_for(s.G, a.part_groups, a.parts) : (int64_t)0;
   });
   if (s_idx < 0) return;
   const Sample& S = tab[__builtin_amdgcn_readfirstlane(s_idx)];
@@ -217,8 +226,9 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
     const int q = (kRowWaves * i + wq) * 32 + ld_q;
     ld_off[i] = (uint32_t)((q + g2 * Lq) * 4) | ((uint32_t)(q >= Lq) << 31);
   }
-  // K/V block DMA of a group: the group's four waves load tensor wq / 2
-  // (K, V), rows 16 (wq % 2) .. + 15
+  // K/V block DMA of a group: wave wq loads tensor (wq / 2) % 2 (K, V),
+  // rows 16 (wq % 2) .. + 15 (with eight waves per group, waves 4..7 load the
+  // same bytes as waves 0..3)
   const int kv_t = (wq >> 1) & 1;
   const int kv_row = 16 * (wq & 1) + (lane >> 2);
   const int kv_col = (lane & 3) * 8;
@@ -327,19 +337,22 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
     for (int c = 0; c < 4; ++c)
       rw[64 * c + (lane ^ (4 * c))] = make_float4(acc[4 * c], acc[4 * c + 1], acc[4 * c + 2], acc[4 * c + 3]);
     __syncthreads();
-    const float4* src = red + kRowWaves * rs * kStageF4 + red_src;
-    float4 o = src[0];
+    // readers: each group's first four waves (256 threads, one per key and four dims)
+    if (RW == 4 || wq < 4) {
+      const float4* src = red + kRowWaves * rs * kStageF4 + red_src;
+      float4 o = src[0];
 #pragma unroll
-    for (int w = 1; w < kRowWaves; ++w) {
-      const float4 x = src[w * kStageF4];
-      o.x += x.x;
-      o.y += x.y;
-      o.z += x.z;
-      o.w += x.w;
-    }
-    if (dst != nullptr && red_live && live) {
-      const float f = ok ? sc : 0.0f;
-      *reinterpret_cast<uint2*>(dst + off) = make_uint2(pack2<T>(o.x * f, o.y * f), pack2<T>(o.z * f, o.w * f));
+      for (int w = 1; w < kRowWaves; ++w) {
+        const float4 x = src[w * kStageF4];
+        o.x += x.x;
+        o.y += x.y;
+        o.z += x.z;
+        o.w += x.w;
+      }
+      if (dst != nullptr && red_live && live) {
+        const float f = ok ? sc : 0.0f;
+        *reinterpret_cast<uint2*>(dst + off) = make_uint2(pack2<T>(o.x * f, o.y * f), pack2<T>(o.z * f, o.w * f));
+      }
     }
     __syncthreads();
   };
@@ -353,22 +366,24 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
 
-  // ---- prologue: K/V and keep bytes of the first pair, the first two
+  // ---- prologue: K/V and keep bytes of the first rows, the first NST - 1
   // stages, the bias region
   dma_kv(g_begin + rs);
   if constexpr (MASKED) dma_keep(g_begin + rs);
   // (gd: the resources of the group whose stage was issued last)
   GroupDesc gd = group_desc(g_begin + rs);
   dma_stage(gd, I0{}, 0);
-  if constexpr (NS == 1) {
-    gd = group_desc(g_begin + 2 + rs);
-    dma_stage(gd, I0{}, 1);
-  } else {
-    dma_stage(gd, I1{}, 1);
+  if constexpr (NST == 3) {
+    if constexpr (NS == 1) {
+      gd = group_desc(g_begin + kGroups + rs);
+      dma_stage(gd, I0{}, 1);
+    } else {
+      dma_stage(gd, I1{}, 1);
+    }
   }
-  // the bias region: wave w loads query tiles 4 i + w % 4 (both chunks; the
-  // two groups' waves write the same bytes); query tiles past Lq, which
-  // ghost steps read, are zeros
+  // the bias region: wave w loads query tiles RW i + w % RW (both chunks;
+  // with two groups, the groups' waves write the same bytes); query tiles
+  // past Lq, which ghost steps read, are zeros
 #pragma unroll
   for (int i = 0; i < NS; ++i) {
     const int qt = kRowWaves * i + wq;
@@ -381,16 +396,16 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   wait_vm<0>();
   __syncthreads();
 
-  // Loads per step, in issue order: [at a pair's first step: the next
-  // pair's K/V block and keep bytes (1 + MASKED)], the pack (1), the Q/dO
-  // tiles (4), all for the stage two ahead.  A step first waits for its own
-  // stage, issued two steps earlier: everything issued after it (the
-  // previous step's loads) may still be in flight.
+  // Loads per step, in issue order: [at a row's first step: the next rows'
+  // K/V block and keep bytes (1 + MASKED)], the pack (1), the Q/dO tiles
+  // (4), all for the stage NST - 1 ahead.  A step first waits for its own
+  // stage, issued NST - 1 steps earlier: everything issued after it (with
+  // three stages, the previous step's loads) may still be in flight.
   constexpr int kPerStep = 5;
   constexpr int kGroupLoads = MASKED ? 2 : 1;
-  int slot = 0;  // ring slot of the stage being computed (the step index mod 3 when 3 divides NS)
-  constexpr bool kFixedSlots = NS % 3 == 0;
-  for (int gp = g_begin; gp < g_end; gp += 2) {
+  int slot = 0;  // ring slot of the stage being computed (the step index mod NST when NST divides NS)
+  constexpr bool kFixedSlots = NS % NST == 0;
+  for (int gp = g_begin; gp < g_end; gp += kGroups) {
     const int g = gp + rs;  // this wave's group (past g_end: a dead group, all zeros, nothing stored)
     const bool g_live = g < g_end;
     // this group's K / V fragments (B operand: lane = key, 8 consecutive d),
@@ -421,20 +436,22 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
     auto step = [&](auto ic) {
       constexpr int i = decltype(ic)::value;
       __builtin_amdgcn_sched_barrier(0);
-      // the previous step was a pair's first (it issued the pair loads too)
-      if constexpr (i == 1 || NS == 1) wait_vm<kPerStep + kGroupLoads>();
+      // (three stages: the previous step was a row's first when i == 1, and issued the rows' loads too;
+      // two stages: the step's own stage was the last load issued)
+      if constexpr (NST == 2) wait_vm<0>();
+      else if constexpr (i == 1 || NS == 1) wait_vm<kPerStep + kGroupLoads>();
       else wait_vm<kPerStep>();
-      const int cs = kFixedSlots ? i % 3 : slot;
+      const int cs = kFixedSlots ? i % NST : slot;
       const RingStage& cur = ring_lds[cs][wave];
       if constexpr (i == 0) {
-        dma_kv(gp + 2 + rs);
-        if constexpr (MASKED) dma_keep(gp + 2 + rs);
+        dma_kv(gp + kGroups + rs);
+        if constexpr (MASKED) dma_keep(gp + kGroups + rs);
       }
       {
-        constexpr int ahead = i + 2;
-        const int as = kFixedSlots ? ahead % 3 : (slot == 0 ? 2 : slot - 1);
+        constexpr int ahead = i + NST - 1;
+        const int as = kFixedSlots ? ahead % NST : (NST == 3 ? (slot == 0 ? 2 : slot - 1) : 1 - slot);
         // the first stage of a group: that group's resources
-        if constexpr (ahead % NS == 0) gd = group_desc(gp + 2 * (ahead / NS) + rs);
+        if constexpr (ahead % NS == 0) gd = group_desc(gp + kGroups * (ahead / NS) + rs);
         dma_stage(gd, std::integral_constant<int, ahead % NS>{}, as);
       }
 
@@ -475,7 +492,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
         dk = E::mma(lds_read_tr_frag_sw<T>(qt_ + at, trl), sf, dk);
       }
       }
-      if constexpr (!kFixedSlots) slot = slot == 2 ? 0 : slot + 1;
+      if constexpr (!kFixedSlots) slot = slot == NST - 1 ? 0 : slot + 1;
     };
     step(I0{});
     if constexpr (NS > 1) step(I1{});
@@ -490,29 +507,37 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
     // step); each group's dK and dV partials are summed and stored through
     // the ring stage the last step read
     wait_vm<NS * kPerStep>();
-    const int red_slot = kFixedSlots ? (NS - 1) % 3 : (slot == 0 ? 2 : slot - 1);
+    const int red_slot = kFixedSlots ? (NS - 1) % NST : (NST == 3 ? (slot == 0 ? 2 : slot - 1) : 1 - slot);
     reduce_store(red_slot, dk, a.dk, red_k + (int64_t)g * k_sg, a.scale, g_live, red_ok);
     reduce_store(red_slot, dv, a.dv, red_v + (int64_t)g * v_sg, 1.0f, g_live, red_ok);
     dk = f32x16{};
     dv = f32x16{};
   }
 
-  // ---- the part's dBias slab.  Waves w and w + 4 hold the same query tiles
-  // (their groups' halves of the part's sum): the second group's regions go
-  // through LDS (the ring, idle once its loads have drained) to the first's
-  // waves, which add them and store; region[i] holds queries
-  // (4 i + wq) * 32 + kappa(g2, j) of this lane's key
-  wait_vm<0>();
-  __syncthreads();
-  float* const xr = reinterpret_cast<float*>(&ring_lds[0][0]) + (wq * NS * 16) * 64 + lane;
-  static_assert(kRowWaves * NS * 16 * 64 * 4 <= sizeof(RingStage) * 3 * kFusedWaves, "regions fit the ring");
-  if (rs == 1) {
+  // ---- the part's dBias slab; region[i] holds queries (RW i + wq) * 32 +
+  // kappa(g2, j) of this lane's key.  With two groups, waves w and w + 4 hold
+  // the same query tiles (their groups' halves of the part's sum): the second
+  // group's regions go through LDS (the ring, idle once its loads have
+  // drained) to the first's waves, which add them and store
+  if constexpr (kGroups == 2) {
+    wait_vm<0>();
+    __syncthreads();
+    float* const xr = reinterpret_cast<float*>(&ring_lds[0][0]) + (wq * NS * 16) * 64 + lane;
+    static_assert(kRowWaves * NS * 16 * 64 * 4 <= sizeof(RingStage) * NST * kFusedWaves, "regions fit the ring");
+    if (rs == 1) {
 #pragma unroll
-    for (int i = 0; i < NS; ++i)
+      for (int i = 0; i < NS; ++i)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) xr[(i * 16 + j) * 64] = region[i][j];
+        for (int j = 0; j < 16; ++j) xr[(i * 16 + j) * 64] = region[i][j];
+    }
+    __syncthreads();
+    if (rs == 0) {
+#pragma unroll
+      for (int i = 0; i < NS; ++i)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) region[i][j] += xr[(i * 16 + j) * 64];
+    }
   }
-  __syncthreads();
   if (rs == 0 && key < Lk) {
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
@@ -520,7 +545,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const int q = q0 + kappa(g2, j);
-        if (q < Lq) db_col[(int64_t)q * db_si] = region[i][j] + xr[(i * 16 + j) * 64];
+        if (q < Lq) db_col[(int64_t)q * db_si] = region[i][j];
       }
     }
   }
@@ -530,7 +555,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
 
 bool dkvb_fused_ok(const oops_attn_geometry& geo, const Plan& plan) {
   return geo.force_generic == 0 && fast_path_ok(geo, plan) && plan.dp == kCompactRow && plan.all_shared &&
-         plan.bias_frag && plan.fused_max_len_q > 0 && plan.fused_max_len_q <= kFusedMaxLen && plan.fused_tiles > 0;
+         plan.bias_frag && plan.fused_max_len_q <= kFusedMaxLen && (plan.fused_tiles > 0 || plan.fused_long_tiles > 0);
 }
 
 hipError_t launch_dkvb_fused(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L,
@@ -541,23 +566,36 @@ hipError_t launch_dkvb_fused(const oops_attn_geometry& geo, const Plan& plan, co
     fill_bwd_args(a, geo, plan, L);
     a.parts = plan.fused_parts;
     a.part_groups = plan.fused_part_groups;
-    a.uniform_tiles = plan.fused_uniform;
-    a.total_tiles = plan.fused_tiles;
-    const dim3 grid((unsigned)xcd_grid(plan.fused_tiles, xcd_chunk(plan.fused_uniform)));
-    // query tiles per wave and group: that of the longest sample
-    a.fused_max_lq = plan.fused_split ? kFusedMaxLen : 0;
-    const int ns = (int)((plan.fused_max_len_q + 32 * kRowWaves - 1) / (32 * kRowWaves));
-    auto run = [&](auto masked, auto nsc) {
-      hipLaunchKernelGGL((attn_dkvb_fast_kernel<T, decltype(masked)::value, decltype(nsc)::value>), grid, dim3(512),
-                         0, stream, a);
+    auto run = [&](auto masked, auto nsc, auto rwc, int64_t tiles, int64_t uniform) {
+      a.uniform_tiles = uniform;
+      a.total_tiles = tiles;
+      const dim3 grid((unsigned)xcd_grid(tiles, xcd_chunk(uniform)));
+      hipLaunchKernelGGL(
+          (attn_dkvb_fast_kernel<T, decltype(masked)::value, decltype(nsc)::value, decltype(rwc)::value>), grid,
+          dim3(512), 0, stream, a);
     };
+    using RW4 = std::integral_constant<int, 4>;
     auto by_ns = [&](auto masked) {
-      if (ns == 1) run(masked, std::integral_constant<int, 1>{});
-      else if (ns == 2) run(masked, std::integral_constant<int, 2>{});
-      else if (ns == 3) run(masked, std::integral_constant<int, 3>{});
-      else if (ns == 4) run(masked, std::integral_constant<int, 4>{});
-      else if (ns == 5) run(masked, std::integral_constant<int, 5>{});
-      else run(masked, std::integral_constant<int, 6>{});
+      // four waves per row: query tiles per wave and group, that of the longest sample it serves
+      if (plan.fused_tiles > 0) {
+        a.fused_max_lq = plan.fused_split || plan.fused_long_tiles > 0 ? kFusedMaxLen : 0;
+        a.fused_min_lq = 0;
+        const int ns = (int)((plan.fused_max_len_q + 32 * 4 - 1) / (32 * 4));
+        const int64_t t = plan.fused_tiles, u = plan.fused_uniform;
+        if (ns == 1) run(masked, std::integral_constant<int, 1>{}, RW4{}, t, u);
+        else if (ns == 2) run(masked, std::integral_constant<int, 2>{}, RW4{}, t, u);
+        else if (ns == 3) run(masked, std::integral_constant<int, 3>{}, RW4{}, t, u);
+        else if (ns == 4) run(masked, std::integral_constant<int, 4>{}, RW4{}, t, u);
+        else if (ns == 5) run(masked, std::integral_constant<int, 5>{}, RW4{}, t, u);
+        else run(masked, std::integral_constant<int, 6>{}, RW4{}, t, u);
+      }
+      // eight waves per row, four query tiles per wave: the samples with kFusedMaxLen < Lq <= kFusedLongMaxLen
+      if (plan.fused_long_tiles > 0) {
+        a.fused_max_lq = kFusedLongMaxLen;
+        a.fused_min_lq = kFusedMaxLen;
+        run(masked, std::integral_constant<int, 4>{}, std::integral_constant<int, 8>{}, plan.fused_long_tiles,
+            plan.fused_long_uniform);
+      }
     };
     if (geo.has_mask) by_ns(std::true_type{});
     else by_ns(std::false_type{});

@@ -68,6 +68,7 @@ struct BwdArgsT {
   // separate dK/dV and dBias kernels (the longer ones); each kernel skips the other's samples, and the dBias
   // reduction takes a longer sample's parts from parts_rest / part_groups_rest
   int fused_max_lq;
+  int fused_min_lq;  // the fused kernel's eight-wave launch: only samples with Lq > fused_min_lq
   int parts_rest;
   int64_t part_groups_rest;
   int head_group;
@@ -130,7 +131,8 @@ inline bool dispatch_config(int dtype, int bias_dtype, int dp, F&& f) {
 }
 
 // longest sample (Lq) the fused dK/dV + dBias kernel serves: 8 waves x 3 query tiles of 32
-constexpr int kFusedMaxLen = 768;
+constexpr int kFusedMaxLen = 768;       // fused dK/dV + dBias, four waves per row
+constexpr int kFusedLongMaxLen = 1024;  // fused dK/dV + dBias, eight waves per row (longer samples)
 
 // Host-side launch plan derived from the geometry table.
 struct Plan {
@@ -154,7 +156,9 @@ struct Plan {
   bool fused_ok = false;  // the fused dK/dV + dBias kernel serves this geometry (sizes its workspace)
   int fused_parts = 1;
   int64_t fused_part_groups = 1;
-  int64_t fused_max_len_q = 0;                   // longest sample the fused kernel serves
+  int64_t fused_max_len_q = 0;                   // longest sample the fused kernel's four-wave launch serves
+  int64_t fused_long_tiles = 0;                  // its eight-wave launch: samples with kFusedMaxLen < Lq <= kFusedLongMaxLen
+  int64_t fused_long_uniform = 0;
   bool fused_split = false;                      // some samples too long for it: separate kernels for those
   int64_t dkv_rest_tiles = 0, fast_sbias_rest_tiles = 0;  // the separate kernels' tiles of those samples
   bool any_pair_mask = false;                    // a mask that depends on the query
@@ -234,6 +238,7 @@ inline void fill_bwd_args(BwdArgsT<T, BT>& a, const oops_attn_geometry& geo, con
   a.parts = plan.parts;
   a.part_groups = 0;
   a.fused_max_lq = 0;
+  a.fused_min_lq = 0;
   a.parts_rest = 1;
   a.part_groups_rest = 0;
   a.head_group = head_group_of(geo);

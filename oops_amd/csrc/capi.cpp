@@ -181,20 +181,34 @@ int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
     plan.sred_uniform = u_red && c_red > 0 ? c_red : 0;
     // fused dK/dV + dBias kernel: one workgroup per (head, 32-key block, part),
     // about kTargetFusedBlocks workgroups (whole rounds of one per CU)
-    // (samples longer than kFusedMaxLen take the separate dK/dV and dBias kernels: a split batch)
+    // (samples longer than kFusedMaxLen take a second launch with eight waves per row when every one of
+    // them fits it, else the separate dK/dV and dBias kernels: a split batch)
     plan.all_shared = geo->has_bias != 0;
     int64_t fused_units = 0;
+    bool long_ok = true;
     for (int s = 0; s < geo->num_samples; ++s) {
       const Sample& S = tab[s];
       if (S.bias_mode != OOPS_BIAS_SHARED || S.b_off < 0) plan.all_shared = false;
-      if (S.Lq <= oops::kFusedMaxLen) fused_units += H * cdiv(S.Lk, 32) * S.G;
+      if (S.Lq > oops::kFusedLongMaxLen) long_ok = false;
+    }
+    for (int s = 0; s < geo->num_samples; ++s) {
+      const Sample& S = tab[s];
+      if (S.Lq <= oops::kFusedMaxLen || long_ok) fused_units += H * cdiv(S.Lk, 32) * S.G;
     }
     if (plan.all_shared) {
       plan.fused_part_groups = std::max<int64_t>(cdiv(fused_units, kTargetFusedBlocks), kMinFusedPartGroups);
-      int64_t c_fu = -1;
-      bool u_fu = true, rest = false;
+      int64_t c_fu = -1, c_lo = -1;
+      bool u_fu = true, u_lo = true, rest = false;
       for (int s = 0; s < geo->num_samples; ++s) {
         const Sample& S = tab[s];
+        if (S.Lq > oops::kFusedMaxLen && long_ok) {
+          const int p = oops::parts_for(S.G, plan.fused_part_groups, kMaxParts);
+          const int64_t c = H * cdiv(S.Lk, 32) * p;
+          plan.fused_parts = std::max(plan.fused_parts, p);
+          plan.fused_long_tiles += c;
+          track(c, c_lo, u_lo);
+          continue;
+        }
         if (S.Lq > oops::kFusedMaxLen) {
           rest = true;
           plan.dkv_rest_tiles += S.G * H * cdiv(S.Lk, 128);
@@ -209,9 +223,12 @@ int make_plan(const oops_attn_geometry* geo, oops::Plan& plan) {
         plan.fused_max_len_q = std::max(plan.fused_max_len_q, S.Lq);
         track(c, c_fu, u_fu);
       }
-      plan.fused_uniform = u_fu && !rest && c_fu > 0 ? c_fu : 0;
+      // (uniform tile counts only when one launch serves every sample)
+      plan.fused_uniform = u_fu && !rest && plan.fused_long_tiles == 0 && c_fu > 0 ? c_fu : 0;
+      plan.fused_long_uniform = u_lo && plan.fused_tiles == 0 && c_lo > 0 ? c_lo : 0;
       // not served by the fused kernel (16-bit, head size <= 32 only)
-      if (plan.fused_tiles > kMaxGrid || geo->dtype == OOPS_F32 || plan.dp != 32) plan.fused_tiles = 0;
+      if (plan.fused_tiles > kMaxGrid || plan.fused_long_tiles > kMaxGrid || geo->dtype == OOPS_F32 || plan.dp != 32)
+        plan.fused_tiles = plan.fused_long_tiles = 0;
       plan.fused_split = rest && plan.fused_tiles > 0;
     }
     if (plan.sbias_tiles > kMaxGrid || plan.fast_sbias_tiles > kMaxGrid || plan.sred_tiles > kMaxGrid)
