@@ -63,12 +63,12 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
   const int Lq = (int)S.Lq, Lk = (int)S.Lk;
   const int nkb = (int)cdiv(Lk, 128);
   const int HG = a.head_group;
-  const int kb = (int)(tile % nkb);
-  int64_t rest = tile / nkb;
-  const int hh = (int)(rest % HG);
-  rest /= HG;
-  const int g0 = (int)(rest % GB) * R;
-  const int h = (int)(rest / GB) * HG + hh;
+  const int kb = (int)((uint32_t)tile % (uint32_t)nkb);
+  uint32_t rest = (uint32_t)tile / (uint32_t)nkb;
+  const int hh = (int)(rest % (uint32_t)HG);
+  rest /= (uint32_t)HG;
+  const int g0 = (int)(rest % (uint32_t)GB) * R;
+  const int h = (int)(rest / (uint32_t)GB) * HG + hh;
   const int D = a.head_size;
   const int q_si = (int)S.q_si, do_si = (int)S.do_si, b_si = (int)S.b_si;
   const int nsteps = (Lq + 63) >> 6;
@@ -356,12 +356,13 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS, FOLD> ?
   const int Lq = (int)S.Lq, Lk = (int)S.Lk;
   const int nqb = (int)cdiv(Lq, 128);
   const int HG = a.head_group;
-  const int qb = (int)(tile % nqb);
-  int64_t rest = tile / nqb;
-  const int hh = (int)(rest % HG);
-  rest /= HG;
-  const int g = (int)(rest % G);
-  const int h = (int)(rest / G) * HG + hh;
+  // (launch grids stay below 2^31 workgroups: 32-bit division)
+  const int qb = (int)((uint32_t)tile % (uint32_t)nqb);
+  uint32_t rest = (uint32_t)tile / (uint32_t)nqb;
+  const int hh = (int)(rest % (uint32_t)HG);
+  rest /= (uint32_t)HG;
+  const int g = (int)(rest % (uint32_t)G);
+  const int h = (int)(rest / (uint32_t)G) * HG + hh;
   const int D = a.head_size;
   const int ntiles = (Lk + 63) >> 6;
   const int k_si = (int)S.k_si, v_si = (int)S.v_si, b_si = (int)S.b_si;
@@ -768,12 +769,12 @@ __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(Bw
   const int nkb = (int)cdiv(Lk, 64);
   const int nqb = (int)cdiv(Lq, 128);
   // logical order (head, part, q block, key block): neighbours share the bias block rows
-  const int kb = (int)(tile % nkb);
-  int64_t rest = tile / nkb;
-  const int qb = (int)(rest % nqb);
-  rest /= nqb;
-  const int part = (int)(rest % P);
-  const int h = (int)(rest / P);
+  const int kb = (int)((uint32_t)tile % (uint32_t)nkb);
+  uint32_t rest = (uint32_t)tile / (uint32_t)nkb;
+  const int qb = (int)(rest % (uint32_t)nqb);
+  rest /= (uint32_t)nqb;
+  const int part = (int)(rest % (uint32_t)P);
+  const int h = (int)(rest / (uint32_t)P);
   const int64_t g_begin = G * part / P, g_end = G * (part + 1) / P;
   const int D = a.head_size;
   const int k0 = kb * 64;

@@ -175,10 +175,11 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   const int nkb = (int)cdiv(Lk, 32);
   // logical order (head, part, key block): the key blocks of one (head, part)
   // read the same Q / dO rows and run next to each other on one XCD
-  const int kb = (int)(tile % nkb);
-  int64_t rest = tile / nkb;
-  const int part = (int)(rest % P);
-  const int h = (int)(rest / P);
+  // (launch grids stay below 2^31 workgroups: 32-bit division)
+  const int kb = (int)((uint32_t)tile % (uint32_t)nkb);
+  const uint32_t rest = (uint32_t)tile / (uint32_t)nkb;
+  const int part = (int)(rest % (uint32_t)P);
+  const int h = (int)(rest / (uint32_t)P);
   const int g_begin = __builtin_amdgcn_readfirstlane((int)(G * part / P));
   const int g_end = __builtin_amdgcn_readfirstlane((int)(G * (part + 1) / P));
   const int D = a.head_size;

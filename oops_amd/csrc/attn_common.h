@@ -193,9 +193,11 @@ template <typename Count>
 __device__ __forceinline__ int find_sample(int64_t& tile, const Sample* table, int num_samples,
                                            int64_t uniform, Count count) {
   if (uniform > 0) {
-    const int s = (int)(tile / uniform);
-    tile -= (int64_t)s * uniform;
-    return s;
+    // (launch grids stay below 2^31 workgroups: 32-bit division)
+    const uint32_t t = (uint32_t)tile, u = (uint32_t)uniform;
+    const uint32_t s = t / u;
+    tile = (int64_t)(t - s * u);
+    return (int)s;
   }
   for (int s = 0; s < num_samples; ++s) {
     const int64_t c = count(table[s]);
@@ -233,10 +235,11 @@ __host__ __device__ __forceinline__ int64_t xcd_grid(int64_t tiles, int chunk) {
   const int64_t m = (int64_t)kNumXcds * (chunk > 0 ? chunk : 1);
   return (tiles + m - 1) / m * m;
 }
+// (chunk is 0 or kXcdChunk; grids stay below 2^31 workgroups)
 __device__ __forceinline__ int64_t xcd_tile(int64_t block, int64_t grid, int chunk) {
-  const int64_t x = block % kNumXcds, j = block / kNumXcds;
-  if (chunk == 0) return x * (grid / kNumXcds) + j;
-  return ((j / chunk) * kNumXcds + x) * chunk + j % chunk;
+  const uint32_t b = (uint32_t)block, x = b % kNumXcds, j = b / kNumXcds;
+  if (chunk == 0) return (int64_t)(x * ((uint32_t)grid / kNumXcds) + j);
+  return (int64_t)(((j / kXcdChunk) * kNumXcds + x) * kXcdChunk + j % kXcdChunk);
 }
 // Heads whose D-element rows together fill one 128-byte line.
 __host__ __forceinline__ int head_group(const oops_attn_geometry& geo) {

@@ -98,12 +98,13 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
   const int Lq = (int)S.Lq, Lk = (int)S.Lk;
   const int nqb = (int)cdiv(Lq, 128);
   const int HG = a.head_group;
-  const int qb = (int)(tile % nqb);
-  int64_t rest = tile / nqb;
-  const int hh = (int)(rest % HG);
-  rest /= HG;
-  const int g = (int)(rest % G);
-  const int h = (int)(rest / G) * HG + hh;
+  // (launch grids stay below 2^31 workgroups: 32-bit division)
+  const int qb = (int)((uint32_t)tile % (uint32_t)nqb);
+  uint32_t rest = (uint32_t)tile / (uint32_t)nqb;
+  const int hh = (int)(rest % (uint32_t)HG);
+  rest /= (uint32_t)HG;
+  const int g = (int)(rest % (uint32_t)G);
+  const int h = (int)(rest / (uint32_t)G) * HG + hh;
   const int D = a.head_size;
   const int ntiles = (Lk + 63) >> 6;
   const int k_si = (int)S.k_si, v_si = (int)S.v_si, b_si = (int)S.b_si;
