@@ -63,12 +63,12 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
   const int Lq = (int)S.Lq, Lk = (int)S.Lk;
   const int nkb = (int)cdiv(Lk, 128);
   const int HG = a.head_group;
-  const int kb = (int)((uint32_t)tile % (uint32_t)nkb);
+  const int kb = __builtin_amdgcn_readfirstlane((int)((uint32_t)tile % (uint32_t)nkb));
   uint32_t rest = (uint32_t)tile / (uint32_t)nkb;
-  const int hh = (int)(rest % (uint32_t)HG);
+  const int hh = __builtin_amdgcn_readfirstlane((int)(rest % (uint32_t)HG));
   rest /= (uint32_t)HG;
-  const int g0 = (int)(rest % (uint32_t)GB) * R;
-  const int h = (int)(rest / (uint32_t)GB) * HG + hh;
+  const int g0 = __builtin_amdgcn_readfirstlane((int)(rest % (uint32_t)GB) * R);
+  const int h = __builtin_amdgcn_readfirstlane((int)(rest / (uint32_t)GB) * HG + hh);
   const int D = a.head_size;
   const int q_si = (int)S.q_si, do_si = (int)S.do_si, b_si = (int)S.b_si;
   const int nsteps = (Lq + 63) >> 6;
@@ -339,7 +339,7 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS, FOLD> ?
   __shared__ __attribute__((aligned(16))) uint32_t fold_lds[FOLD ? kFoldTiles * 32 : 4];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   const int lane = tid & 63;
   const int lq = lane & 31;
   const int g2 = lane >> 5;
@@ -357,12 +357,12 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS, FOLD> ?
   const int nqb = (int)cdiv(Lq, 128);
   const int HG = a.head_group;
   // (launch grids stay below 2^31 workgroups: 32-bit division)
-  const int qb = (int)((uint32_t)tile % (uint32_t)nqb);
+  const int qb = __builtin_amdgcn_readfirstlane((int)((uint32_t)tile % (uint32_t)nqb));
   uint32_t rest = (uint32_t)tile / (uint32_t)nqb;
-  const int hh = (int)(rest % (uint32_t)HG);
+  const int hh = __builtin_amdgcn_readfirstlane((int)(rest % (uint32_t)HG));
   rest /= (uint32_t)HG;
-  const int g = (int)(rest % (uint32_t)G);
-  const int h = (int)(rest / (uint32_t)G) * HG + hh;
+  const int g = __builtin_amdgcn_readfirstlane((int)(rest % (uint32_t)G));
+  const int h = __builtin_amdgcn_readfirstlane((int)(rest / (uint32_t)G) * HG + hh);
   const int D = a.head_size;
   const int ntiles = (Lk + 63) >> 6;
   const int k_si = (int)S.k_si, v_si = (int)S.v_si, b_si = (int)S.b_si;
@@ -709,10 +709,16 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS, FOLD> ?
     t2 = t3;
   }
 
-  if (qv && a.dq != nullptr) {
-    T* row = a.dq + S.q_off + g * S.q_sg + h * S.q_sh + (int64_t)q_lane * S.q_si;
+  // the lane's query, recomputed from the lane id here (an opaque read, so
+  // that the compiler does not keep the epilogue's per-lane addresses live
+  // through the loop, where the lean instances have no registers to spare)
+  uint32_t ln;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+  const int q_end = qb * 128 + wave * 32 + (int)(ln & 31);
+  if (q_end < Lq && a.dq != nullptr) {
+    T* row = a.dq + S.q_off + g * S.q_sg + h * S.q_sh + (int64_t)q_end * S.q_si;
 #pragma unroll
-    for (int t = 0; t < NDT; ++t) store_tile<T>(row, t * 32, D, g2, acc[t], a.scale);
+    for (int t = 0; t < NDT; ++t) store_tile<T>(row, t * 32, D, (int)(ln >> 5), acc[t], a.scale);
   }
 }
 
@@ -769,12 +775,12 @@ __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(Bw
   const int nkb = (int)cdiv(Lk, 64);
   const int nqb = (int)cdiv(Lq, 128);
   // logical order (head, part, q block, key block): neighbours share the bias block rows
-  const int kb = (int)((uint32_t)tile % (uint32_t)nkb);
+  const int kb = __builtin_amdgcn_readfirstlane((int)((uint32_t)tile % (uint32_t)nkb));
   uint32_t rest = (uint32_t)tile / (uint32_t)nkb;
-  const int qb = (int)(rest % (uint32_t)nqb);
+  const int qb = __builtin_amdgcn_readfirstlane((int)(rest % (uint32_t)nqb));
   rest /= (uint32_t)nqb;
-  const int part = (int)(rest % (uint32_t)P);
-  const int h = (int)(rest / (uint32_t)P);
+  const int part = __builtin_amdgcn_readfirstlane((int)(rest % (uint32_t)P));
+  const int h = __builtin_amdgcn_readfirstlane((int)(rest / (uint32_t)P));
   const int64_t g_begin = G * part / P, g_end = G * (part + 1) / P;
   const int D = a.head_size;
   const int k0 = kb * 64;

@@ -75,7 +75,8 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
   static_assert(!FOLD || (MASKED_TILES && HAS_BIAS && sizeof(T) == 2), "fold: masked bf16 tiles with a bias");
 
   const int tid = threadIdx.x;
-  const int wave = (tid >> 6) & 3;  // (& 3: lets the compiler bound LDS addresses)
+  // wave-uniform (scalar); & 3 lets the compiler bound LDS addresses
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6) & 3;
   const int lane = tid & 63;
   const int lq = lane & 31;
   const int g2 = lane >> 5;
@@ -99,12 +100,12 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
   const int nqb = (int)cdiv(Lq, 128);
   const int HG = a.head_group;
   // (launch grids stay below 2^31 workgroups: 32-bit division)
-  const int qb = (int)((uint32_t)tile % (uint32_t)nqb);
+  const int qb = __builtin_amdgcn_readfirstlane((int)((uint32_t)tile % (uint32_t)nqb));
   uint32_t rest = (uint32_t)tile / (uint32_t)nqb;
-  const int hh = (int)(rest % (uint32_t)HG);
+  const int hh = __builtin_amdgcn_readfirstlane((int)(rest % (uint32_t)HG));
   rest /= (uint32_t)HG;
-  const int g = (int)(rest % (uint32_t)G);
-  const int h = (int)(rest / (uint32_t)G) * HG + hh;
+  const int g = __builtin_amdgcn_readfirstlane((int)(rest % (uint32_t)G));
+  const int h = __builtin_amdgcn_readfirstlane((int)(rest / (uint32_t)G) * HG + hh);
   const int D = a.head_size;
   const int ntiles = (Lk + 63) >> 6;
   const int k_si = (int)S.k_si, v_si = (int)S.v_si, b_si = (int)S.b_si;
