@@ -9,17 +9,20 @@
 // dK/dV kernel and again in a dBias kernel.
 //
 // One workgroup = 8 wavefronts = 32 keys of one (sample, head) and one range
-// ("part") of the groups.  It walks the groups of its part; for each group g
-// every wave walks its eighth of the queries: wave w takes the 32-query tiles
-// w, w + 8, w + 16 (at most three, so Lq <= 768).  Every lane owns one key
-// (the MFMA column).  Per step a wave computes, for one query tile,
+// ("part") of the groups.  The waves form groups of RW: with RW = 4 two
+// groups work on two rows (groups g, g + 1) at a time, wave w of a group
+// taking the 32-query tiles w, w + 4, w + 8, ... (at most six, Lq <= 768);
+// with RW = 8 all eight waves work on one row, wave w taking the tiles w,
+// w + 8, w + 16, w + 24 (Lq <= 1024).  Every lane owns one key (the MFMA
+// column).  Per step a wave computes, for one query tile,
 //   S  = Q K^T (+ bias by an identity MFMA, - LSE as the accumulator input),
 //   dP = dO V^T - delta,   P = exp2(S * scale * log2 e),   dS = P * dP,
 //   dV^T += dO^T P,  dK^T += Q^T dS,  region[step] += dS.
 // The dBias region of a wave (32 keys x its query tiles) stays in registers
-// for the whole part.  At the end of each group the eight waves' dK/dV
-// partials are summed in a fixed order through LDS and stored; at the end of
-// the part the region goes to the part's dBias slab, and
+// for the whole part.  At the end of each row its group's partials of dK and
+// dV are summed in a fixed order through LDS and stored, whole 64-byte key
+// rows at a time; at the end of the part the regions go to the part's dBias
+// slab (with two groups, the second group's through LDS to the first's), and
 // attn_dbias_reduce_kernel sums the slabs.  No atomics: results are
 // bit-identical from run to run.
 //
@@ -27,14 +30,15 @@
 // memory to LDS (buffer_load ... lds, issued through inline assembly and
 // ordered by explicit vmcnt waits).  Q and dO come from the head-major
 // compact copies the dQ kernel writes (2 KB contiguous per tile), -LSE/c and
-// -delta from the pack it writes beside them.  Each wave has its own 3-stage
-// LDS ring (Q and dO tiles with XOR-swizzled rows, -LSE/c and -delta), filled
-// two steps ahead, so the steps need no workgroup barrier; each group's K/V
-// block and keep bytes go into 2-buffer slots shared by the waves, one group
-// ahead; the bias of the workgroup's 32 keys and all query tiles (identity-
-// MFMA fragments, from the fragment-major copy made by attn_bias_frag_kernel)
-// is loaded into LDS once per part.  Two barriers per tensor at each group's
-// end, around the dK/dV sum, which reuses the ring stage just read.
+// -delta from the pack it writes beside them.  Each wave has its own LDS
+// ring (3 stages with RW = 4, 2 with RW = 8) of Q and dO tiles with
+// XOR-swizzled rows, -LSE/c and -delta, filled one or two steps ahead, so
+// the steps need no workgroup barrier; each group's K/V block and keep bytes
+// go into one slot per group, loaded during the previous row; the bias of
+// the workgroup's 32 keys and all query tiles (identity-MFMA fragments, from
+// the fragment-major copy made by attn_bias_frag_kernel) is loaded into LDS
+// once per part.  Two barriers per tensor at each row's end, around the
+// dK/dV sum, which reuses the ring stage just read.
 //
 // Semantics: the reference's _backward_key_value and _backward_shared_bias
 // (oops/attention/triangle/triton/kernel.py:569-873, generic.py:484-534) with

@@ -258,7 +258,7 @@ hipError_t launch_dkv_fast(const oops_attn_geometry& geo, const Plan& plan, cons
 // later kernels (no separate delta pass)
 hipError_t launch_dq_fast(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L, bool delta_in_dq,
                           hipStream_t stream);
-// Fused dK, dV and row-shared dBias (head size <= 32, Lq <= 768, every sample a shared bias); it
+// Fused dK, dV and row-shared dBias (head size <= 32, Lq <= 1024, every sample a shared bias); it
 // reads L.ld_pack, L.qc and L.dc, which the fast dQ kernel writes.
 bool dkvb_fused_ok(const oops_attn_geometry& geo, const Plan& plan);
 hipError_t launch_dkvb_fused(const oops_attn_geometry& geo, const Plan& plan, const BwdLaunch& L,
