@@ -119,9 +119,11 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   using E = Elem<T>;
   using Frag = typename E::Frag;
   static_assert(sizeof(T) == 2, "16-bit operands");
-  static_assert(RW == 4 || RW == 8, "waves per group");
-  static_assert(NS >= 1 && NS <= (RW == 4 ? kFusedMaxSteps : 4), "query tiles per wave and group");
+  static_assert(RW == 2 || RW == 4 || RW == 8, "waves per group");
+  static_assert(NS >= 1 && NS <= (RW == 8 ? 4 : kFusedMaxSteps), "query tiles per wave and group");
   constexpr int kRowWaves = RW;
+  constexpr int kKvLoads = RW == 2 ? 2 : 1;  // K/V block loads per wave and row
+  constexpr int kItems = RW == 2 ? 2 : 1;    // (key, four dims) items each reader thread sums and stores
   constexpr int kGroups = kFusedWaves / RW;  // groups (rows) in flight
   constexpr int NST = kStages<RW>;           // ring stages
 
@@ -152,8 +154,6 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   // stage 0 (stage s adds s * kStageStride), its K/V rows, its keep bytes
   constexpr uint32_t kStageStride = kFusedWaves * sizeof(RingStage);
   const uint32_t ring_m0 = lds_addr(&ring_lds[0][wave]);
-  const uint32_t kv_m0 =
-      lds_addr(kv_lds) + (uint32_t)(((rs * 2 + ((wq >> 1) & 1)) * 32 * 32 + 16 * (wq & 1) * 32) * sizeof(T));
   const uint32_t keep_m0 = lds_addr(keep_lds) + (uint32_t)(rs * 64 * 4);
   const uint32_t bias_m0 = lds_addr(bias_lds);
 
@@ -204,45 +204,47 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   const uint8_t* const m_h = has_mask ? uptr(a.mask + S.m_off) : nullptr;
   const int64_t m_sg = has_mask ? u64(S.m_sg) : 0;
 
-  // ---- per-lane DMA offsets (bytes) of the Q / dO tile rows of step i
-  // (query tile 4 i + wq) within the (g, h) block of the compact copies,
-  // which are the same for Q and dO: load r (0, 1) of a tile covers rows
-  // 16 r .. 16 r + 15; lane l writes slot l = row 16 r + l / 4, physical
-  // chunk l % 4, which holds logical chunk (l % 4) ^ swz(row).  Rows past Lq
-  // (and chunks past D) get an offset past the block's range: they read 0.
-  uint32_t tile_off[NS][2];
+  // ---- per-lane DMA offsets (bytes) of the Q / dO tile rows of step 0
+  // (query tile wq) within the (g, h) block of the compact copies, which are
+  // the same for Q and dO; step i (query tile RW i + wq) adds i kStepQD.
+  // Load r (0, 1) of a tile covers rows 16 r .. 16 r + 15; lane l writes
+  // slot l = row 16 r + l / 4, physical chunk l % 4, which holds logical
+  // chunk (l % 4) ^ swz(row).  Rows past Lq fall past the block's range and
+  // chunks past D get an offset past every range: they read 0.
+  constexpr uint32_t kStepQD = (uint32_t)(kRowWaves * 32 * kCompactRow * 2);
+  uint32_t tile_off0[2];
 #pragma unroll
-  for (int i = 0; i < NS; ++i)
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int row = 16 * r + (lane >> 2);
-      const int col = ((lane & 3) ^ swz<32>(row)) * 8;
-      const int q = (kRowWaves * i + wq) * 32 + row;
-      tile_off[i][r] = col < D && q < Lq ? (uint32_t)((q * kCompactRow + col) * 2) : kOut;
-    }
-  // pack offsets of step i: lane l reads query (4 i + wq) * 32 + ld_q,
+  for (int r = 0; r < 2; ++r) {
+    const int row = 16 * r + (lane >> 2);
+    const int col = ((lane & 3) ^ swz<32>(row)) * 8;
+    tile_off0[r] = col < D ? (uint32_t)(((wq * 32 + row) * kCompactRow + col) * 2) : kOut;
+  }
+  // pack offsets of step i: lane l reads query (RW i + wq) * 32 + ld_q,
   // lanes 32..63 from the -delta half, so that ring position l holds the
   // query the accumulator layout puts there (ld_q inverts perm32); a query
   // past Lq gets 2^31 added (out of range: it reads 0)
-  const int ld_q = kappa(lq >> 4, lq & 15);
-  uint32_t ld_off[NS];
+  const int ld_q0 = wq * 32 + kappa(lq >> 4, lq & 15);
+  // K/V block DMA of a group: its four loads (K rows 0..15, K rows 16..31, V
+  // rows 0..15, V rows 16..31) spread over the group's waves, load u = (kKvLoads
+  // wq + j) % 4 (with eight waves per group, waves 4..7 load the same bytes as
+  // waves 0..3)
+  uint32_t kv_m0[kKvLoads], kv_lane_off[kKvLoads], kv_bytes[kKvLoads];
+  int64_t kv_sg[kKvLoads];
+  const T* kv_h[kKvLoads];
 #pragma unroll
-  for (int i = 0; i < NS; ++i) {
-    const int q = (kRowWaves * i + wq) * 32 + ld_q;
-    ld_off[i] = (uint32_t)((q + g2 * Lq) * 4) | ((uint32_t)(q >= Lq) << 31);
+  for (int j = 0; j < kKvLoads; ++j) {
+    const int u = (kKvLoads * wq + j) & 3;
+    const int t = u >> 1;
+    const int row = 16 * (u & 1) + (lane >> 2);
+    const int col = (lane & 3) * 8;
+    kv_m0[j] = lds_addr(kv_lds) + (uint32_t)(((rs * 2 + t) * 32 * 32 + 16 * (u & 1) * 32) * sizeof(T));
+    const int64_t si = u64(t ? S.v_si : S.k_si);
+    kv_sg[j] = u64(t ? S.v_sg : S.k_sg);
+    kv_h[j] = uptr(t ? a.v + S.v_off + h * S.v_sh : a.k + S.k_off + h * S.k_sh);
+    kv_bytes[j] = (uint32_t)(((int64_t)(Lk - 1) * si + D) * 2);
+    const int key_ = kb * 32 + row;
+    kv_lane_off[j] = key_ < Lk && col < D ? (uint32_t)((key_ * si + col) * 2) : kOut;
   }
-  // K/V block DMA of a group: wave wq loads tensor (wq / 2) % 2 (K, V),
-  // rows 16 (wq % 2) .. + 15 (with eight waves per group, waves 4..7 load the
-  // same bytes as waves 0..3)
-  const int kv_t = (wq >> 1) & 1;
-  const int kv_row = 16 * (wq & 1) + (lane >> 2);
-  const int kv_col = (lane & 3) * 8;
-  const int64_t kv_si = u64(kv_t ? S.v_si : S.k_si);
-  const int64_t kv_sg = u64(kv_t ? S.v_sg : S.k_sg);
-  const T* const kv_h = uptr(kv_t ? a.v + S.v_off + h * S.v_sh : a.k + S.k_off + h * S.k_sh);
-  const uint32_t kv_bytes = (uint32_t)(((int64_t)(Lk - 1) * kv_si + D) * 2);
-  const int kv_key = kb * 32 + kv_row;
-  const uint32_t kv_lane_off = kv_key < Lk && kv_col < D ? (uint32_t)((kv_key * kv_si + kv_col) * 2) : kOut;
   // bias fragments (A operand, lane = query): the fragment-major copy of the
   // shared bias; the 1 KB block of (query tile, chunk c) sits at a uniform offset
   const bool bf_in = kb < a.bf_nkt;
@@ -282,19 +284,24 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   auto dma_stage = [&](const GroupDesc& gd, auto ic, int st) {
     constexpr int i = decltype(ic)::value;
     const uint32_t m0 = ring_m0 + (uint32_t)st * kStageStride;
-    dma4_m0(gd.pk, m0 + offsetof(RingStage, ld), ld_off[i]);
+    const int q = ld_q0 + kRowWaves * 32 * i;
+    dma4_m0(gd.pk, m0 + offsetof(RingStage, ld), (uint32_t)((q + g2 * Lq) * 4) | ((uint32_t)(q >= Lq) << 31));
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      dma16_m0(gd.q, m0 + offsetof(RingStage, q) + 16 * r * 32 * 2, tile_off[i][r]);
-      dma16_m0(gd.d, m0 + offsetof(RingStage, d) + 16 * r * 32 * 2, tile_off[i][r]);
+      const uint32_t off = tile_off0[r] + (uint32_t)i * kStepQD;
+      dma16_m0(gd.q, m0 + offsetof(RingStage, q) + 16 * r * 32 * 2, off);
+      dma16_m0(gd.d, m0 + offsetof(RingStage, d) + 16 * r * 32 * 2, off);
     }
   };
-  // K/V block of this wave's group g into its slot of kv_lds (one DMA load)
+  // K/V block of this wave's group g into its slot of kv_lds (kKvLoads DMA loads)
   auto dma_kv = [&](int g) {
     const bool live = g < g_end;
     const int64_t gg = live ? g : g_begin;
-    const u32x4 r = rsrc_words(kv_h + gg * kv_sg, live ? kv_bytes : 0u);
-    dma16_m0(r, kv_m0, kv_lane_off);
+#pragma unroll
+    for (int j = 0; j < kKvLoads; ++j) {
+      const u32x4 r = rsrc_words(kv_h[j] + gg * kv_sg[j], live ? kv_bytes[j] : 0u);
+      dma16_m0(r, kv_m0[j], kv_lane_off[j]);
+    }
   };
   // keep bytes of group g's keys into keep_lds[rs] (one load)
   auto dma_keep = [&](int g) {
@@ -308,20 +315,29 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
     return g < g_end && kb * 32 + k < Lk && (!has_mask || keep_lds[rs][k] != 0);
   };
 
-  // Pair end: each group's four waves' dK (then dV) partials are summed
-  // through LDS and stored.  The reader threads of a group are its own four
-  // waves; thread t of them owns dims 4 red_q .. 4 red_q + 3 of key red_key
-  // (red_q = 2 c + g2 for chunk c and lane half g2 of the accumulator
-  // layout), so eight consecutive lanes write one whole 64-byte key row:
-  // scattered 4-byte stores into rows 196 KB apart (the ending-node layout)
-  // cost the kernel a third of its time.
-  const int red_t = tid & 255;
-  const int red_key = red_t >> 3, red_q = red_t & 7;
-  const int red_c = red_q >> 1, red_g = red_q & 1;
-  const int red_gkey = kb * 32 + red_key;
-  const bool red_live = red_gkey < Lk && 4 * red_q < D;
-  const int64_t red_k = S.k_off + h * S.k_sh + (int64_t)red_gkey * S.k_si + 4 * red_q;
-  const int64_t red_v = S.v_off + h * S.v_sh + (int64_t)red_gkey * S.v_si + 4 * red_q;
+  // Row end: each group's waves' dK (then dV) partials are summed through
+  // LDS and stored.  The reader threads of a group are its own waves (with
+  // eight waves per group, the first four); item t of them owns dims 4 red_q
+  // .. 4 red_q + 3 of key red_key (red_q = 2 c + g2 for chunk c and lane half
+  // g2 of the accumulator layout), so eight consecutive lanes write one whole
+  // 64-byte key row: scattered 4-byte stores into rows 196 KB apart (the
+  // ending-node layout) cost the kernel a third of its time.  256 items per
+  // group: one per thread, two with two waves per group.
+  int red_key[kItems], red_src[kItems];
+  bool red_live[kItems];
+  int64_t red_k[kItems], red_v[kItems];
+#pragma unroll
+  for (int it = 0; it < kItems; ++it) {
+    const int red_t = tid % (kRowWaves * 64) + it * kRowWaves * 64;
+    red_key[it] = (red_t >> 3) & 31;
+    const int red_q = red_t & 7, red_c = red_q >> 1, red_g = red_q & 1;
+    const int red_gkey = kb * 32 + red_key[it];
+    red_live[it] = red_gkey < Lk && 4 * red_q < D;
+    red_k[it] = S.k_off + h * S.k_sh + (int64_t)red_gkey * S.k_si + 4 * red_q;
+    red_v[it] = S.v_off + h * S.v_sh + (int64_t)red_gkey * S.v_si + 4 * red_q;
+    // (see the layout of the partials below)
+    red_src[it] = 64 * red_c + ((red_key[it] + 32 * red_g) ^ (4 * red_c));
+  }
   const int64_t k_sg = S.k_sg, v_sg = S.v_sg;
   constexpr int kStageF4 = (int)(sizeof(RingStage) / 16);
   static_assert(sizeof(RingStage) % 16 == 0 && 16 * 64 <= 4 * kStageF4, "a wave's partials fit its ring stage");
@@ -333,30 +349,33 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   // the writes of a wave are a permutation of consecutive 16-byte slots, and
   // the reads of eight consecutive lanes (one key, four c, two g2) fall into
   // four bank groups, two lanes each.
-  const int red_src = 64 * red_c + ((red_key + 32 * red_g) ^ (4 * red_c));
   // (a masked key's rows are written as zeros; a dead group writes nothing)
-  auto reduce_store = [&](int slot, const f32x16& acc, T* dst, int64_t off, float sc, bool live, bool ok) {
+  auto reduce_store = [&](int slot, const f32x16& acc, T* dst, const int64_t (&off)[kItems], int64_t goff, float sc,
+                          bool live, const bool (&ok)[kItems]) {
     float4* const red = reinterpret_cast<float4*>(&ring_lds[slot][0]);
     float4* const rw = red + wave * kStageF4;
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       rw[64 * c + (lane ^ (4 * c))] = make_float4(acc[4 * c], acc[4 * c + 1], acc[4 * c + 2], acc[4 * c + 3]);
     __syncthreads();
-    // readers: each group's first four waves (256 threads, one per key and four dims)
-    if (RW == 4 || wq < 4) {
-      const float4* src = red + kRowWaves * rs * kStageF4 + red_src;
-      float4 o = src[0];
+    if (RW != 8 || wq < 4) {
 #pragma unroll
-      for (int w = 1; w < kRowWaves; ++w) {
-        const float4 x = src[w * kStageF4];
-        o.x += x.x;
-        o.y += x.y;
-        o.z += x.z;
-        o.w += x.w;
-      }
-      if (dst != nullptr && red_live && live) {
-        const float f = ok ? sc : 0.0f;
-        *reinterpret_cast<uint2*>(dst + off) = make_uint2(pack2<T>(o.x * f, o.y * f), pack2<T>(o.z * f, o.w * f));
+      for (int it = 0; it < kItems; ++it) {
+        const float4* src = red + kRowWaves * rs * kStageF4 + red_src[it];
+        float4 o = src[0];
+#pragma unroll
+        for (int w = 1; w < kRowWaves; ++w) {
+          const float4 x = src[w * kStageF4];
+          o.x += x.x;
+          o.y += x.y;
+          o.z += x.z;
+          o.w += x.w;
+        }
+        if (dst != nullptr && red_live[it] && live) {
+          const float f = ok[it] ? sc : 0.0f;
+          *reinterpret_cast<uint2*>(dst + off[it] + goff) =
+              make_uint2(pack2<T>(o.x * f, o.y * f), pack2<T>(o.z * f, o.w * f));
+        }
       }
     }
     __syncthreads();
@@ -407,7 +426,7 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
   // stage, issued NST - 1 steps earlier: everything issued after it (with
   // three stages, the previous step's loads) may still be in flight.
   constexpr int kPerStep = 5;
-  constexpr int kGroupLoads = MASKED ? 2 : 1;
+  constexpr int kGroupLoads = kKvLoads + (MASKED ? 1 : 0);
   int slot = 0;  // ring slot of the stage being computed (the step index mod NST when NST divides NS)
   constexpr bool kFixedSlots = NS % NST == 0;
   for (int gp = g_begin; gp < g_end; gp += kGroups) {
@@ -418,7 +437,9 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
     Frag kf[2], vf[2];
     const bool kvalid = MASKED ? kv_keep(g, lq) : true;
     const bool wave_masked = MASKED && __any(!kvalid);
-    const bool red_ok = MASKED ? kv_keep(g, red_key) : true;
+    bool red_ok[kItems];
+#pragma unroll
+    for (int it = 0; it < kItems; ++it) red_ok[it] = MASKED ? kv_keep(g, red_key[it]) : true;
     {
       const T* kb_ = kv_lds + (rs * 2) * 32 * 32 + lq * 32;
 #pragma unroll
@@ -513,34 +534,38 @@ __global__ __launch_bounds__(512, 1) void attn_dkvb_fast_kernel(BwdArgsT<T, T> a
     // the ring stage the last step read
     wait_vm<NS * kPerStep>();
     const int red_slot = kFixedSlots ? (NS - 1) % NST : (NST == 3 ? (slot == 0 ? 2 : slot - 1) : 1 - slot);
-    reduce_store(red_slot, dk, a.dk, red_k + (int64_t)g * k_sg, a.scale, g_live, red_ok);
-    reduce_store(red_slot, dv, a.dv, red_v + (int64_t)g * v_sg, 1.0f, g_live, red_ok);
+    reduce_store(red_slot, dk, a.dk, red_k, (int64_t)g * k_sg, a.scale, g_live, red_ok);
+    reduce_store(red_slot, dv, a.dv, red_v, (int64_t)g * v_sg, 1.0f, g_live, red_ok);
     dk = f32x16{};
     dv = f32x16{};
   }
 
   // ---- the part's dBias slab; region[i] holds queries (RW i + wq) * 32 +
-  // kappa(g2, j) of this lane's key.  With two groups, waves w and w + 4 hold
-  // the same query tiles (their groups' halves of the part's sum): the second
-  // group's regions go through LDS (the ring, idle once its loads have
-  // drained) to the first's waves, which add them and store
-  if constexpr (kGroups == 2) {
+  // kappa(g2, j) of this lane's key.  With several groups, wave wq of every
+  // group holds the same query tiles (its group's share of the part's sum):
+  // the other groups' regions go through LDS (the ring, idle once its loads
+  // have drained) to the first group's waves, one group at a time in a fixed
+  // order, which add them and store
+  if constexpr (kGroups > 1) {
     wait_vm<0>();
-    __syncthreads();
     float* const xr = reinterpret_cast<float*>(&ring_lds[0][0]) + (wq * NS * 16) * 64 + lane;
     static_assert(kRowWaves * NS * 16 * 64 * 4 <= sizeof(RingStage) * NST * kFusedWaves, "regions fit the ring");
-    if (rs == 1) {
+#pragma unroll 1
+    for (int r = 1; r < kGroups; ++r) {
+      __syncthreads();
+      if (rs == r) {
 #pragma unroll
-      for (int i = 0; i < NS; ++i)
+        for (int i = 0; i < NS; ++i)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) xr[(i * 16 + j) * 64] = region[i][j];
-    }
-    __syncthreads();
-    if (rs == 0) {
+          for (int j = 0; j < 16; ++j) xr[(i * 16 + j) * 64] = region[i][j];
+      }
+      __syncthreads();
+      if (rs == 0) {
 #pragma unroll
-      for (int i = 0; i < NS; ++i)
+        for (int i = 0; i < NS; ++i)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) region[i][j] += xr[(i * 16 + j) * 64];
+          for (int j = 0; j < 16; ++j) region[i][j] += xr[(i * 16 + j) * 64];
+      }
     }
   }
   if (rs == 0 && key < Lk) {
@@ -579,15 +604,25 @@ hipError_t launch_dkvb_fused(const oops_attn_geometry& geo, const Plan& plan, co
           (attn_dkvb_fast_kernel<T, decltype(masked)::value, decltype(nsc)::value, decltype(rwc)::value>), grid,
           dim3(512), 0, stream, a);
     };
+    using RW2 = std::integral_constant<int, 2>;
     using RW4 = std::integral_constant<int, 4>;
     auto by_ns = [&](auto masked) {
-      // four waves per row: query tiles per wave and group, that of the longest sample it serves
+      // the samples up to kFusedMaxLen: query tiles per wave and group, that of the longest sample it
+      // serves; two waves per row (four rows in flight, a quarter of the per-row dK/dV sums per step)
+      // from 129 to 384 queries, four waves per row otherwise
       if (plan.fused_tiles > 0) {
         a.fused_max_lq = plan.fused_split || plan.fused_long_tiles > 0 ? kFusedMaxLen : 0;
         a.fused_min_lq = 0;
-        const int ns = (int)((plan.fused_max_len_q + 32 * 4 - 1) / (32 * 4));
         const int64_t t = plan.fused_tiles, u = plan.fused_uniform;
-        if (ns == 1) run(masked, std::integral_constant<int, 1>{}, RW4{}, t, u);
+        const int64_t lq = plan.fused_max_len_q;
+        const int ns2 = (int)((lq + 32 * 2 - 1) / (32 * 2));
+        const int ns = (int)((lq + 32 * 4 - 1) / (32 * 4));
+        if (lq > 128 && lq <= 384) {
+          if (ns2 == 3) run(masked, std::integral_constant<int, 3>{}, RW2{}, t, u);
+          else if (ns2 == 4) run(masked, std::integral_constant<int, 4>{}, RW2{}, t, u);
+          else if (ns2 == 5) run(masked, std::integral_constant<int, 5>{}, RW2{}, t, u);
+          else run(masked, std::integral_constant<int, 6>{}, RW2{}, t, u);
+        } else if (ns == 1) run(masked, std::integral_constant<int, 1>{}, RW4{}, t, u);
         else if (ns == 2) run(masked, std::integral_constant<int, 2>{}, RW4{}, t, u);
         else if (ns == 3) run(masked, std::integral_constant<int, 3>{}, RW4{}, t, u);
         else if (ns == 4) run(masked, std::integral_constant<int, 4>{}, RW4{}, t, u);

@@ -291,12 +291,12 @@ def test_config_c3_ending_node():
     "cols,rows,masked,layout",
     [(96, 5, True, "swapped"), (200, 3, True, "dense"), (40, 4, False, "swapped"), (768, 2, False, "swapped"),
      (33, 6, True, "dense"), (384, 64, True, "dense"), (1024, 3, True, "dense"), (800, 2, False, "swapped"),
-     (1000, 5, True, "swapped")],
+     (1000, 5, True, "swapped"), (300, 7, True, "swapped"), (160, 9, False, "dense"), (384, 5, False, "swapped")],
 )  # fmt: skip
 def test_fused_dkv_dbias(cols, rows, masked, layout):
-    """The fused dK/dV + shared-dBias kernel (16-bit, head size <= 32, row-shared bias; four waves per row
-    up to Lq = 768, eight waves per row up to 1024): oracle parity, agreement with the separate dK/dV and
-    dBias kernels, and bit-identical repeats."""
+    """The fused dK/dV + shared-dBias kernel (16-bit, head size <= 32, row-shared bias; two waves per row
+    from 129 to 384 queries, four up to 768, eight up to 1024; rows not a multiple of the rows in flight):
+    oracle parity, agreement with the separate dK/dV and dBias kernels, and bit-identical repeats."""
 
     case = make_case(torch.bfloat16, prefix=(1,), rows=rows, cols=cols, heads=4, head=32, masked=masked,
                      layout=layout, seed=cols + rows)  # fmt: skip
