@@ -251,6 +251,7 @@ __global__ __launch_bounds__(256, OOPS_DKV_OCC) void attn_dkv_fast_kernel(BwdArg
         const uint32_t off = use_bf ? (uint32_t)((((2 * step + qr) * a.bf_nkt * 2 + c) * 64 + lane) * 16)
                                     : (q < Lq ? (uint32_t)((q * b_si + kw + 16 * c + g2 * 8) * 2) : kOut);
         bias[qr][c] = buffer_load16_s(b_rsrc, off, 0);
+        if (!use_bf) bias[qr][c] = finite16<T>(bias[qr][c]);  // (the copy holds finite values already)
       }
     }
   };
@@ -592,6 +593,13 @@ __global__ __launch_bounds__(256, (kLeanDq<DP, MASKED_TILES, FULL_DBIAS, FOLD> ?
     for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
       for (int c = 0; c < 2; ++c) bf[t2][c] = buffer_load16_s(b_rsrc, t < ntiles ? b_off[t2][c] + s : kOut, 0);
+    // bias rows read directly (not the fragment-major copy, which holds finite values already)
+    if (!use_bf) {
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) bf[t2][c] = finite16<T>(bf[t2][c]);
+    }
   };
 
   __syncthreads();
@@ -808,7 +816,7 @@ __global__ __launch_bounds__(256, OOPS_DBIAS_OCC) void attn_dbias_fast_kernel(Bw
           if (key + 8 <= Lk) u = *reinterpret_cast<const uint4*>(brow + key);
           else u = load16(brow, key, Lk, false);
         }
-        bacc[t2] = E::mma(ident[c], __builtin_bit_cast(Frag, u), bacc[t2]);
+        bacc[t2] = E::mma(ident[c], __builtin_bit_cast(Frag, finite16<T>(u)), bacc[t2]);
       }
     }
   }

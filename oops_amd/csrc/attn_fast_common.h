@@ -1,5 +1,6 @@
 // Helpers shared by the 16-bit fast-path kernels (forward and backward).
 #pragma once
+#include <type_traits>
 
 #include "attn_kernels.h"
 
@@ -96,6 +97,26 @@ __device__ __forceinline__ void identity_frags(typename Elem<T>::Frag (&id)[2], 
     for (int k = 0; k < 4; ++k) u[k] = (j >> 1) == k ? v : 0u;
     id[c] = __builtin_bit_cast(typename Elem<T>::Frag, make_uint4(u[0], u[1], u[2], u[3]));
   }
+}
+
+// The identity MFMA that adds the bias multiplies every bias element of a
+// 16-key chunk by the zeros of the other keys' columns, so a non-finite bias
+// element (an additive -inf mask) would make the whole chunk NaN.  Bias
+// elements whose exponent is all ones (+-inf, NaN) are therefore read as the
+// largest finite value of their sign: -max times the weight 1/scale still
+// gives a logit of -inf or below -1e38, so such a key's P is exactly 0, as
+// with -inf.  (A NaN or +inf bias element, which makes the whole row NaN in
+// float arithmetic, reads as +-max.)
+template <typename T>
+__device__ __forceinline__ uint32_t finite2(uint32_t d) {
+  constexpr uint32_t kExp = sizeof(T) == 2 && std::is_same_v<T, __bf16> ? 0x7F80u : 0x7C00u;
+  constexpr uint32_t kMax = std::is_same_v<T, __bf16> ? 0x7F7Fu : 0x7BFFu;
+  const uint32_t sp = ((d & kExp) == kExp ? 0x0000FFFFu : 0u) | (((d >> 16) & kExp) == kExp ? 0xFFFF0000u : 0u);
+  return (d & ~sp) | (((d & 0x80008000u) | (kMax * 0x00010001u)) & sp);
+}
+template <typename T>
+__device__ __forceinline__ uint4 finite16(uint4 u) {
+  return make_uint4(finite2<T>(u.x), finite2<T>(u.y), finite2<T>(u.z), finite2<T>(u.w));
 }
 
 // Key masks folded into the bias operand of the identity MFMA (bf16, row-

@@ -244,8 +244,11 @@ __global__ __launch_bounds__(256, OOPS_FWD_OCC) void attn_fwd_fast_kernel(FwdArg
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
       if constexpr (HAS_BIAS) {
-        const uint4 b0 = FOLD ? fold_bias(bf[t2][0], fm[t2 * 2]) : bf[t2][0];
-        const uint4 b1 = FOLD ? fold_bias(bf[t2][1], fm[t2 * 2 + 1]) : bf[t2][1];
+        // (bias rows read directly are made finite here; the fragment-major copy holds finite values)
+        const uint4 r0 = use_bf ? bf[t2][0] : finite16<T>(bf[t2][0]);
+        const uint4 r1 = use_bf ? bf[t2][1] : finite16<T>(bf[t2][1]);
+        const uint4 b0 = FOLD ? fold_bias(r0, fm[t2 * 2]) : r0;
+        const uint4 b1 = FOLD ? fold_bias(r1, fm[t2 * 2 + 1]) : r1;
         sacc[t2] = E::mma(ident[0], __builtin_bit_cast(Frag, b0), f32x16{});
         sacc[t2] = E::mma(ident[1], __builtin_bit_cast(Frag, b1), sacc[t2]);
       } else {
@@ -473,6 +476,7 @@ __global__ __launch_bounds__(256) void attn_bias_frag_kernel(const T* __restrict
       for (int j = 0; j < 8; ++j) e[j] = k + j < S.Lk ? row[k + j] : (T)0.0f;
       v = __builtin_bit_cast(uint4, e);
     }
+    v = fast::finite16<T>(v);  // (non-finite elements read as +-max: see finite2)
   }
   const int64_t dst = (int64_t)s * sample_stride + ((((int64_t)h * nqt + qt) * nkt + kt) * 2 + c) * 512 + lane * 8;
   *reinterpret_cast<uint4*>(bf + dst) = v;

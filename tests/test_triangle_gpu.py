@@ -180,6 +180,68 @@ def test_fully_masked_nonfinite():
         torch.testing.assert_close(grad, torch.zeros_like(leaf))
 
 
+@pytest.mark.parametrize("cols,rows", [(200, 3), (900, 2)])
+def test_masked_keys_nonfinite_fast_path(cols, rows):
+    """bf16 fast path with a shared bias and mixed 64-key tiles (the key mask folded into the bias fragments,
+    the fused dK/dV + dBias kernel with two or eight waves per row): inf in the K rows and NaN in the V rows
+    of masked keys, and NaN in the bias column of a key masked in every row, change no output and no
+    gradient against the same call with finite values there."""
+
+    q, k, v, mask, bias, dout = make_case(torch.bfloat16, prefix=(1,), rows=rows, cols=cols, heads=4, head=32,
+                                          seed=cols)  # fmt: skip
+    kc = cols // 3
+    mask[..., kc] = False  # masked in every row: its bias column may hold anything
+    q, k, v, bias, dout, mask = (t.to(DEV) for t in (q, k, v, bias, dout, mask))
+
+    def run(k_, v_, b_):
+        leaves = [t.detach().clone().requires_grad_(True) for t in (q, k_, v_, b_)]
+        out = triangle_attention(leaves[0], leaves[1], leaves[2], mask, leaves[3])
+        return (out, *torch.autograd.grad(out, leaves, dout))
+
+    clean = run(k, v, bias)
+    off = ~mask  # (1, rows, cols): masked (row, key) pairs
+    kp, vp, bp = k.clone(), v.clone(), bias.clone()
+    kp[off] = float("inf")
+    vp[off] = float("nan")
+    bp[..., kc] = float("nan")
+    poisoned = run(kp, vp, bp)
+    for name, a_, b_ in zip(("out", "dq", "dk", "dv", "dbias"), clean, poisoned):
+        if name == "dbias":
+            a_, b_ = a_[..., torch.arange(cols) != kc], b_[..., torch.arange(cols) != kc]
+        elif name in ("dk", "dv"):
+            a_, b_ = a_[mask], b_[mask]
+        assert torch.isfinite(b_).all(), name
+        assert torch.equal(a_, b_), name
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("bias_kind", ["shared", "full"])
+def test_additive_neg_inf_bias(dtype, bias_kind):
+    """-inf in the bias works as an additive key mask on the 16-bit fast paths: the bias passes through an
+    identity MFMA there, so a non-finite element must not turn the 16 keys it is summed with into NaN.
+    Every output and gradient is finite and matches the call that masks the same key through ``mask``."""
+
+    cols, kc = 200, 7
+    q, k, v, _, bias, dout = make_case(dtype, prefix=(1,), rows=3, cols=cols, heads=4, head=32, masked=False,
+                                       bias_kind=bias_kind, seed=3)  # fmt: skip
+    q, k, v, bias, dout = (t.to(DEV) for t in (q, k, v, bias, dout))
+    b_inf, b_zero = bias.clone(), bias.clone()
+    b_inf[..., kc] = float("-inf")
+    b_zero[..., kc] = 0
+    mask = torch.ones(1, 3, cols, dtype=torch.bool, device=DEV)
+    mask[..., kc] = False
+
+    def run(b_, m_):
+        leaves = [t.detach().clone().requires_grad_(True) for t in (q, k, v, b_)]
+        out = triangle_attention(leaves[0], leaves[1], leaves[2], m_, leaves[3])
+        return (out, *torch.autograd.grad(out, leaves, dout))
+
+    additive, masked = run(b_inf, None), run(b_zero, mask)
+    for name, a_, b_ in zip(("out", "dq", "dk", "dv", "dbias"), additive, masked):
+        assert torch.isfinite(a_).all(), name
+        torch.testing.assert_close(a_.float(), b_.float(), atol=2e-2, rtol=2e-2, msg=name)
+
+
 def test_rows_fully_masked_partially():
     q, k, v, mask, bias, dout = make_case(torch.bfloat16, rows=6, cols=40, head=32, seed=9)
     mask[:, 2] = False
