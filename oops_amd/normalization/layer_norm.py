@@ -109,7 +109,10 @@ def _nested(input, normalized_shape, weight, bias, eps):
     return input.packed_like(layer_norm(input.concat, normalized_shape, weight, bias, eps))
 
 
+@functools.lru_cache(maxsize=256)
 def _geometry(dtype, rows: int, width: int, x_row: int, eps: float) -> _lib.RowNormGeometry:
+    """The launch geometry (cached: the library only reads it)."""
+
     g = _lib.RowNormGeometry()
     g.dtype = _DTYPE_CODE[dtype]
     g.width, g.rows, g.x_row, g.y_row, g.eps = width, rows, x_row, width, float(eps)
@@ -123,6 +126,12 @@ def _ptr(t: Optional[Tensor]) -> Optional[int]:
 @functools.lru_cache(maxsize=64)
 def _backward_workspace_bytes(lib, dtype, rows: int, width: int, x_row: int) -> int:
     return lib.oops_layer_norm_rows_backward_workspace_bytes(ctypes.byref(_geometry(dtype, rows, width, x_row, 0.0)))
+
+
+def _stream(device) -> int:
+    """The raw handle of the device's current stream."""
+
+    return torch._C._cuda_getCurrentRawStream(device.index)
 
 
 def _on_device(device):
@@ -140,7 +149,7 @@ def _forward_impl(x: Tensor, weight: Optional[Tensor], bias: Optional[Tensor], e
     geo = _geometry(x.dtype, rows, width, x.stride(0) if rows > 1 else width, eps)
     with _on_device(x.device):
         rc = lib.oops_layer_norm_rows_forward(ctypes.byref(geo), _ptr(x), _ptr(weight), _ptr(bias), _ptr(y),
-                                              _ptr(mean), _ptr(rstd), torch.cuda.current_stream().cuda_stream)
+                                              _ptr(mean), _ptr(rstd), _stream(x.device))
     _lib.check(rc, "layer_norm forward")
     return y, mean, rstd
 
@@ -167,7 +176,7 @@ def _backward_impl(dy: Tensor, x: Tensor, weight: Optional[Tensor], mean: Tensor
         # the affine gradients are summed in the library, in a fixed order
         rc = lib.oops_layer_norm_rows_backward_affine(ctypes.byref(geo), _ptr(x), _ptr(weight), _ptr(mean),
                                                       _ptr(rstd), _ptr(dy), _ptr(dx), _ptr(dw), _ptr(db), _ptr(ws),
-                                                      ws_bytes, torch.cuda.current_stream().cuda_stream)  # fmt: skip
+                                                      ws_bytes, _stream(x.device))  # fmt: skip
     _lib.check(rc, "layer_norm backward")
     return dx, dw, db
 
@@ -256,7 +265,11 @@ class _EagerLayerNorm(torch.autograd.Function):
 def _apply(x: Tensor, weight: Optional[Tensor], bias: Optional[Tensor], eps: float) -> Tensor:
     width = x.shape[-1]
     rows = x.numel() // width
-    x2 = x.resolve_neg().reshape(rows, width)
+    # (a 2-D input is used as it is: each reshape or view adds an autograd node, about 8 us of host
+    # time in the backward)
+    x2 = x.resolve_neg()
+    if x2.dim() != 2:
+        x2 = x2.reshape(rows, width)
     if x2.stride(1) != 1 or (rows > 1 and x2.stride(0) < width):
         x2 = x2.contiguous()
     f32 = lambda t: None if t is None else t.resolve_neg().float().contiguous()  # noqa: E731
@@ -264,4 +277,4 @@ def _apply(x: Tensor, weight: Optional[Tensor], bias: Optional[Tensor], eps: flo
         y, _, _ = layer_norm_forward(x2, f32(weight), f32(bias), eps)
     else:
         y = _EagerLayerNorm.apply(x2, f32(weight), f32(bias), eps)
-    return y.view(x.shape)
+    return y if x.dim() == 2 else y.view(x.shape)
