@@ -91,7 +91,7 @@ constexpr int kBM = 128;  // tokens per workgroup (32 per wave)
 constexpr int kBN = 128;  // gate channels per workgroup
 constexpr int kBK = 64;   // k per step
 #ifndef OOPS_GATE_WGS
-#define OOPS_GATE_WGS 512  // workgroups of the W-resident projection (two per CU)
+#define OOPS_GATE_WGS 256  // workgroups of the W-resident projection (one per CU)
 #endif
 
 // epilogue of one token tile: lane (lq, g2) of accumulator tile t owns channels n0 + 32 t + 16 g2 .. +15
@@ -293,7 +293,7 @@ __global__ __launch_bounds__(256) void gate_projection_kernel(GateArgs a) {
 }
 
 // gate_projection_w_kernel (C <= 256): the same tile and epilogue, with the workgroup's W block (128
-// channels x C) loaded into LDS once and kept across a run of tpw token tiles (about two workgroups per
+// channels x C) loaded into LDS once and kept across a run of tpw token tiles (about one workgroup per
 // CU for the whole launch, so no workgroup start-up, W reload or k-step barrier per tile).  While a
 // tile's MFMAs consume k-panel p of its `single` fragments, panel p of the next tile loads into the same
 // registers; the tile's attention runs load before its MFMAs.  Every load is unconditional (past the
