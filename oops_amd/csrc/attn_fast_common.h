@@ -109,8 +109,9 @@ __device__ __forceinline__ void identity_frags(typename Elem<T>::Frag (&id)[2], 
 // float arithmetic, reads as +-max.)
 template <typename T>
 __device__ __forceinline__ uint32_t finite2(uint32_t d) {
-  constexpr uint32_t kExp = sizeof(T) == 2 && std::is_same_v<T, __bf16> ? 0x7F80u : 0x7C00u;
-  constexpr uint32_t kMax = std::is_same_v<T, __bf16> ? 0x7F7Fu : 0x7BFFu;
+  static_assert(std::is_same_v<T, __bf16> || std::is_same_v<T, _Float16>, "16-bit elements");
+  constexpr uint32_t kExp = std::is_same_v<T, __bf16> ? 0x7F80u : 0x7C00u;  // exponent field
+  constexpr uint32_t kMax = std::is_same_v<T, __bf16> ? 0x7F7Fu : 0x7BFFu;  // largest finite magnitude
   const uint32_t sp = ((d & kExp) == kExp ? 0x0000FFFFu : 0u) | (((d >> 16) & kExp) == kExp ? 0xFFFF0000u : 0u);
   return (d & ~sp) | (((d & 0x80008000u) | (kMax * 0x00010001u)) & sp);
 }
