@@ -282,8 +282,9 @@ def _median_ms(fn, iters=10, warmup=3, reps=3):
     return statistics.median(runs)
 
 
-def other_configs(device):
-    """fwd+bwd ms and TFLOP/s of BASELINE configs 2, 4 and 5 (parity cases, reported beside the headline)."""
+def other_configs(device, which=("c2", "c4", "c5")):
+    """fwd+bwd ms and TFLOP/s of BASELINE configs 2, 4 and 5 (parity cases, reported beside the headline);
+    ``which`` selects a subset (one config per profiler run keeps their kernel statistics apart)."""
 
     import torch
 
@@ -300,6 +301,21 @@ def other_configs(device):
         return run
 
     # C2: starting node, N=384, key padding of the last 10-30% (seed 1)
+    if "c2" in which:
+        res.update(_config2(device, grad_step))
+    if "c4" in which:
+        res.update(_config4(device, grad_step))
+    if "c5" in which:
+        res.update(_config5(device, grad_step))
+    return res
+
+
+def _config2(device, grad_step):
+    import torch
+
+    from oops_amd import triangle_attention
+
+    res = {}
     g = torch.Generator().manual_seed(1)
     n = 384
     q, k, v, do = (torch.randn(1, n, n, H, C, generator=g).to(torch.bfloat16).to(device) for _ in range(4))
@@ -311,7 +327,15 @@ def other_configs(device):
     leaves = [t.requires_grad_(True) for t in (q, k, v, bias)]
     ms = _median_ms(grad_step(lambda: triangle_attention(q, k, v, mask, bias), leaves, do))
     res["c2_starting_n384_keypad"] = {"ms": round(ms, 4), "tflops": round(14 * H * C * n**3 / ms / 1e9, 2)}
+    return res
 
+
+def _config4(device, grad_step):
+    import torch
+
+    from oops_amd import pair_bias_attention
+
+    res = {}
     # C4: MSA rows S=512, N=384, H=8 head-major, key mask ~15%, shared bias (seed 3)
     g = torch.Generator().manual_seed(3)
     s_, n, h = 512, 384, 8
@@ -325,7 +349,15 @@ def other_configs(device):
     leaves = [t.requires_grad_(True) for t in (q, k, v, bias)]
     ms = _median_ms(grad_step(lambda: pair_bias_attention(q, k, v, mask, bias), leaves, do))
     res["c4_msa_rows_s512_n384_h8"] = {"ms": round(ms, 4), "tflops": round(14 * s_ * h * C * n**2 / ms / 1e9, 2)}
+    return res
 
+
+def _config5(device, grad_step):
+    import torch
+
+    from oops_amd import triangle_attention
+
+    res = {}
     # C5: ragged complexes N_i in {256, 512, 768, 1024}, both orientations, key masks hiding 0-20% (seed 4)
     tests_dir = os.path.join(ROOT, "tests")
     if tests_dir not in sys.path:
@@ -691,7 +723,7 @@ def main():
     )
     ap.add_argument(
         "--only",
-        choices=("nested_msa", "layer_norm", "trimul_f32"),
+        choices=("nested_msa", "layer_norm", "trimul_f32", "c2", "c4", "c5"),
         help="only measure one of the rows beside attention (3 repetitions) and print its JSON",
     )
     ap.add_argument(
@@ -730,7 +762,8 @@ def main():
     torch.cuda.set_device(dev)
     if args.only:
         fn = {"nested_msa": nested_msa, "layer_norm": layer_norm_stage,
-              "trimul_f32": lambda d: trimul_stage(d, dtype="f32")}[args.only]
+              "trimul_f32": lambda d: trimul_stage(d, dtype="f32"),
+              **{c: (lambda d, c=c: other_configs(d, (c,))) for c in ("c2", "c4", "c5")}}[args.only]
         for _ in range(3):
             res = fn(dev)
         print(json.dumps(res))
