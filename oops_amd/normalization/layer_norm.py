@@ -158,25 +158,31 @@ def _backward_impl(dy: Tensor, x: Tensor, weight: Optional[Tensor], mean: Tensor
                    need_affine: bool) -> Tuple[Tensor, Tensor, Tensor]:  # fmt: skip
     lib = _lib.load()
     rows, width = x.shape
+    dev = x.device
     if dy.is_neg():
         dy = dy.resolve_neg()
     if dy.dtype != x.dtype:
         dy = dy.to(x.dtype)
     if dy.dim() != 2 or not dy.is_contiguous():
         dy = dy.reshape(rows, width).contiguous()
-    geo = _geometry(x.dtype, rows, width, x.stride(0) if rows > 1 else width, eps)
+    x_row = x.stride(0) if rows > 1 else width
+    geo = _geometry(x.dtype, rows, width, x_row, eps)
     # grad_x is written with x's row stride
-    dx = torch.empty_strided(x.shape, x.stride(), dtype=x.dtype, device=x.device)
+    dx = torch.empty_strided(x.shape, x.stride(), dtype=x.dtype, device=dev)
     n = width if need_affine else 0
-    dw = torch.empty(n, dtype=torch.float32, device=x.device)
-    db = torch.empty(n, dtype=torch.float32, device=x.device)
-    ws_bytes = _backward_workspace_bytes(lib, x.dtype, rows, width, geo.x_row) if need_affine else 0
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
-    with _on_device(x.device):
-        # the affine gradients are summed in the library, in a fixed order
-        rc = lib.oops_layer_norm_rows_backward_affine(ctypes.byref(geo), _ptr(x), _ptr(weight), _ptr(mean),
-                                                      _ptr(rstd), _ptr(dy), _ptr(dx), _ptr(dw), _ptr(db), _ptr(ws),
-                                                      ws_bytes, _stream(x.device))  # fmt: skip
+    dw = torch.empty(n, dtype=torch.float32, device=dev)
+    db = torch.empty(n, dtype=torch.float32, device=dev)
+    ws_bytes = _backward_workspace_bytes(lib, x.dtype, rows, width, x_row) if need_affine else 0
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    # (x, mean, rstd, dy and dx are never empty here)
+    args = (ctypes.byref(geo), x.data_ptr(), _ptr(weight), mean.data_ptr(), rstd.data_ptr(), dy.data_ptr(),
+            dx.data_ptr(), _ptr(dw), _ptr(db), _ptr(ws), ws_bytes, _stream(dev))  # fmt: skip
+    # the affine gradients are summed in the library, in a fixed order
+    if dev.index == torch.cuda.current_device():
+        rc = lib.oops_layer_norm_rows_backward_affine(*args)
+    else:
+        with torch.cuda.device(dev):
+            rc = lib.oops_layer_norm_rows_backward_affine(*args)
     _lib.check(rc, "layer_norm backward")
     return dx, dw, db
 
