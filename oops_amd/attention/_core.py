@@ -20,11 +20,13 @@ This plays the role of the reference's ``triton_triangle_attention`` /
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from collections import OrderedDict
 from typing import List, Optional, Sequence, Tuple
 
 import torch
+from torch.utils._python_dispatch import _get_current_dispatch_mode
 from torch import Tensor
 
 from .. import _lib
@@ -144,7 +146,7 @@ def _make_table(key: tuple) -> tuple:
     dev = torch.empty(host.shape, dtype=torch.int64, device=device)
     dev.copy_(host, non_blocking=True)
     # (host, device copy, streams the device copy is recorded on)
-    return host, dev, {torch.cuda.current_stream(device).cuda_stream}
+    return host, dev, {_stream(device)}
 
 
 _TABLES = _TableCache(512, _make_table)
@@ -160,12 +162,12 @@ def device_table(table: Sequence[int], device: torch.device) -> tuple[Tensor, Te
     launch on another stream may still read it.
     """
 
-    key = (device.index, tuple(int(x) for x in table))
+    key = (device.index, tuple(map(int, table)))
     host, dev, streams = _TABLES.get(key, torch.cuda.is_current_stream_capturing())
-    stream = torch.cuda.current_stream(device)
-    if stream.cuda_stream not in streams:
-        dev.record_stream(stream)
-        streams.add(stream.cuda_stream)
+    raw = _stream(device)
+    if raw not in streams:
+        dev.record_stream(torch.cuda.current_stream(device))
+        streams.add(raw)
     return host, dev
 
 
@@ -277,10 +279,40 @@ def _ptr(t: Optional[Tensor]) -> Optional[int]:
 
 
 def _stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The raw handle of the device's current stream."""
+
+    return torch._C._cuda_getCurrentRawStream(device.index)
+
+
+def _on_device(device: torch.device):
+    """The device context of a launch (a no-op when that device is already current)."""
+
+    return contextlib.nullcontext() if device.index == torch.cuda.current_device() else torch.cuda.device(device)
 
 
 # ----------------------------------------------------------------- ops
+
+
+def _forward_impl(q: Tensor, k: Tensor, v: Tensor, mask: Optional[Tensor], bias: Optional[Tensor], table: List[int],
+                  num_heads: int, scale: float, lse_numel: int, save_residual: bool) -> Tuple[Tensor, Tensor, Tensor]:
+    """The forward launch: (out, out_lo, lse)."""
+
+    lib = _lib.load()
+    out = torch.empty_strided(q.size(), q.stride(), dtype=q.dtype, device=q.device)
+    out_lo = _residual_like(out, save_residual)
+    lse = torch.empty(lse_numel, dtype=torch.float32, device=q.device)
+    vec = _vec_ok(table, (q, k, v, out), bias)
+    geo, keep = _geometry(q, bias, mask, table, num_heads, scale, vec)
+    ws_bytes = lib.oops_attn_forward_workspace_bytes(ctypes.byref(geo))
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+    with _on_device(q.device):
+        rc = lib.oops_attn_forward(
+            ctypes.byref(geo), _ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(bias), _ptr(out), _ptr(out_lo),
+            _ptr(lse), _ptr(workspace), ws_bytes, _stream(q.device),
+        )
+    _lib.check(rc, "attention forward")
+    del keep
+    return out, out_lo, lse
 
 
 @torch.library.custom_op("oops_amd::attention_forward", mutates_args=(), device_types="cuda")
@@ -296,22 +328,7 @@ def attention_forward(
     lse_numel: int,
     save_residual: bool,
 ) -> Tuple[Tensor, Tensor, Tensor]:
-    lib = _lib.load()
-    out = torch.empty_strided(q.size(), q.stride(), dtype=q.dtype, device=q.device)
-    out_lo = _residual_like(out, save_residual)
-    lse = torch.empty(lse_numel, dtype=torch.float32, device=q.device)
-    vec = _vec_ok(table, (q, k, v, out), bias)
-    geo, keep = _geometry(q, bias, mask, table, num_heads, scale, vec)
-    ws_bytes = lib.oops_attn_forward_workspace_bytes(ctypes.byref(geo))
-    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
-    with torch.cuda.device(q.device):
-        rc = lib.oops_attn_forward(
-            ctypes.byref(geo), _ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(bias), _ptr(out), _ptr(out_lo),
-            _ptr(lse), _ptr(workspace), ws_bytes, _stream(q.device),
-        )
-    _lib.check(rc, "attention forward")
-    del keep
-    return out, out_lo, lse
+    return _forward_impl(q, k, v, mask, bias, table, num_heads, scale, lse_numel, save_residual)
 
 
 def _residual_like(out: Tensor, save: bool) -> Tensor:
@@ -328,23 +345,11 @@ def _(q, k, v, mask, bias, table, num_heads, scale, lse_numel, save_residual):
     return out, _residual_like(out, save_residual), q.new_empty(lse_numel, dtype=torch.float32)
 
 
-@torch.library.custom_op("oops_amd::attention_backward", mutates_args=(), device_types="cuda")
-def attention_backward(
-    dout: Tensor,
-    q: Tensor,
-    k: Tensor,
-    v: Tensor,
-    mask: Optional[Tensor],
-    bias: Optional[Tensor],
-    out: Tensor,
-    out_lo: Tensor,
-    lse: Tensor,
-    table: List[int],
-    num_heads: int,
-    scale: float,
-    dbias_numel: int,
-    needs: List[bool],
-) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+def _backward_impl(dout: Tensor, q: Tensor, k: Tensor, v: Tensor, mask: Optional[Tensor], bias: Optional[Tensor],
+                   out: Tensor, out_lo: Tensor, lse: Tensor, table: List[int], num_heads: int, scale: float,
+                   dbias_numel: int, needs: List[bool]) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """The backward launch: (dq, dk, dv, float32 dbias)."""
+
     lib = _lib.load()
     dout = dout.resolve_neg().resolve_conj()
     if dout.dtype != out.dtype:
@@ -376,7 +381,7 @@ def attention_backward(
     if ws_bytes == 0:
         _lib.check(1, "attention backward workspace sizing")
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         rc = lib.oops_attn_backward(
             ctypes.byref(geo), _ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(bias), _ptr(out), _ptr(out_lo),
             _ptr(lse), _ptr(dout), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dbias), _ptr(workspace), ws_bytes,
@@ -385,6 +390,26 @@ def attention_backward(
     _lib.check(rc, "attention backward")
     del keep
     return dq, dk, dv, dbias
+
+
+@torch.library.custom_op("oops_amd::attention_backward", mutates_args=(), device_types="cuda")
+def attention_backward(
+    dout: Tensor,
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    mask: Optional[Tensor],
+    bias: Optional[Tensor],
+    out: Tensor,
+    out_lo: Tensor,
+    lse: Tensor,
+    table: List[int],
+    num_heads: int,
+    scale: float,
+    dbias_numel: int,
+    needs: List[bool],
+) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    return _backward_impl(dout, q, k, v, mask, bias, out, out_lo, lse, table, num_heads, scale, dbias_numel, needs)
 
 
 @attention_backward.register_fake
@@ -397,27 +422,37 @@ def _(dout, q, k, v, mask, bias, out, out_lo, lse, table, num_heads, scale, dbia
     return like(q, need_q), like(k, need_k), like(v, need_v), dbias
 
 
-def _setup_context(ctx, inputs, output):
-    q, k, v, mask, bias, table, num_heads, scale, lse_numel, save_residual = inputs
-    out, out_lo, lse = output
+def _save(ctx, q, k, v, mask, bias, table, num_heads, scale, out, out_lo, lse):
     ctx.save_for_backward(q, k, v, mask, bias, out, out_lo, lse)
     ctx.table = table
     ctx.num_heads = num_heads
     ctx.scale = scale
     ctx.bias_shape = None if bias is None else bias.shape
     ctx.bias_dtype = None if bias is None else bias.dtype
-    ctx.mark_non_differentiable(out_lo, lse)
     ctx.set_materialize_grads(False)  # no zero-filled gradients for the residual and LSE outputs
 
 
+def _setup_context(ctx, inputs, output):
+    q, k, v, mask, bias, table, num_heads, scale, lse_numel, save_residual = inputs
+    out, out_lo, lse = output
+    _save(ctx, q, k, v, mask, bias, table, num_heads, scale, out, out_lo, lse)
+    ctx.mark_non_differentiable(out_lo, lse)
+
+
 def _backward(ctx, dout, dout_lo, dlse):
+    return _grads(ctx, dout, attention_backward)
+
+
+def _grads(ctx, dout, backward):
+    """Gradients of (q, k, v, mask, bias, table, num_heads, scale, lse_numel, save_residual)."""
+
     q, k, v, mask, bias, out, out_lo, lse = ctx.saved_tensors
     need_q, need_k, need_v, _, need_b = ctx.needs_input_grad[:5]
     need_b = bool(need_b and bias is not None)
     if dout is None or not (need_q or need_k or need_v or need_b):
         return (None,) * 10
     dbias_numel = 0 if bias is None else bias.numel()
-    dq, dk, dv, dbias = attention_backward(
+    dq, dk, dv, dbias = backward(
         dout, q, k, v, mask, bias, out, out_lo, lse, ctx.table, ctx.num_heads, ctx.scale, dbias_numel,
         [bool(need_q), bool(need_k), bool(need_v), need_b],
     )
@@ -439,6 +474,23 @@ def _backward(ctx, dout, dout_lo, dlse):
 
 
 attention_forward.register_autograd(_backward, setup_context=_setup_context)
+
+
+class _EagerAttention(torch.autograd.Function):
+    """The same implementations as the custom ops, for eager calls: autograd
+    calls the backward directly instead of through the operator dispatcher
+    (about 100 us less host time per forward and backward on a slow host).
+    Traced code (torch.compile) takes the custom ops."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, mask, bias, table, num_heads, scale, lse_numel):
+        out, out_lo, lse = _forward_impl(q, k, v, mask, bias, table, num_heads, scale, lse_numel, True)
+        _save(ctx, q, k, v, mask, bias, table, num_heads, scale, out, out_lo, lse)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        return _grads(ctx, dout, _backward_impl)[:9]
 
 
 # ----------------------------------------------------------------- table rows
@@ -493,5 +545,11 @@ def attend(q, k, v, mask, bias, table, num_heads, scale, lse_numel) -> Tensor:
     save = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (q, k, v, bias)
     )
-    out, _, _ = attention_forward(q, k, v, mask, bias, table, num_heads, scale, lse_numel, save)
+    if torch.compiler.is_compiling() or type(q) is not Tensor or _get_current_dispatch_mode() is not None:
+        # traced, fake or subclass tensors: the custom op (with its fake kernel)
+        out, _, _ = attention_forward(q, k, v, mask, bias, table, num_heads, scale, lse_numel, save)
+    elif save:
+        out = _EagerAttention.apply(q, k, v, mask, bias, table, num_heads, scale, lse_numel)
+    else:
+        out, _, _ = _forward_impl(q, k, v, mask, bias, table, num_heads, scale, lse_numel, False)
     return out

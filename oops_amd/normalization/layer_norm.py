@@ -21,6 +21,7 @@ from typing import Iterable, Optional, Tuple, Union
 
 import torch
 from torch import Tensor
+from torch.utils._python_dispatch import _get_current_dispatch_mode
 
 from .. import _lib
 from .._errors import unsupported
@@ -279,7 +280,8 @@ def _apply(x: Tensor, weight: Optional[Tensor], bias: Optional[Tensor], eps: flo
     if x2.stride(1) != 1 or (rows > 1 and x2.stride(0) < width):
         x2 = x2.contiguous()
     f32 = lambda t: None if t is None else t.resolve_neg().float().contiguous()  # noqa: E731
-    if torch.compiler.is_compiling():
+    if torch.compiler.is_compiling() or type(x2) is not Tensor or _get_current_dispatch_mode() is not None:
+        # traced, fake or subclass tensors: the custom op (with its fake kernel)
         y, _, _ = layer_norm_forward(x2, f32(weight), f32(bias), eps)
     else:
         y = _EagerLayerNorm.apply(x2, f32(weight), f32(bias), eps)

@@ -205,3 +205,17 @@ def test_table_cache_pins_entries_used_under_capture():
     for i in range(600, 700):
         cache.get((0, (i, 9)), capturing=False)
     assert cache.get((0, (7, 7)), capturing=False) is early
+
+
+def test_layer_norm_fake_shapes():
+    """Fake tensors outside torch.compile take the custom op's fake kernel (eager calls of real tensors
+    go through an autograd.Function instead)."""
+
+    from oops_amd import layer_norm
+
+    with FakeTensorMode():
+        x = torch.empty(6, 10, 128, device="cuda", dtype=torch.bfloat16)
+        w = torch.empty(128, device="cuda")
+        y = layer_norm(x, 128, w, w)
+        assert is_fake(y)
+        assert y.shape == x.shape and y.dtype == x.dtype
