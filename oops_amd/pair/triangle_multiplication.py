@@ -28,6 +28,7 @@ from typing import List, Literal, Optional, Sequence, Tuple
 
 import torch
 from torch import Tensor
+from torch.utils._python_dispatch import _get_current_dispatch_mode
 from torch.nn import functional as F
 
 from .. import _lib
@@ -337,20 +338,8 @@ def _small_views(small: Tensor, spans: List[int]) -> List[Optional[Tensor]]:
     return [None if spans[2 * i] < 0 else small[spans[2 * i] : spans[2 * i + 1]] for i in range(len(_SMALL))]
 
 
-@torch.library.custom_op("oops_amd::trimul_forward", mutates_args=(), device_types="cuda")
-def trimul_forward(
-    pair: Tensor,
-    mask: Optional[Tensor],
-    w_cat: Tensor,
-    wo: Tensor,
-    wog: Tensor,
-    small: Tensor,
-    spans: List[int],
-    blocks: List[int],
-    direction: str,
-    eps_in: float,
-    eps_out: float,
-) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+def _forward_impl(pair: Tensor, mask: Optional[Tensor], w_cat: Tensor, wo: Tensor, wog: Tensor, small: Tensor,
+                  spans: List[int], blocks: List[int], direction: str, eps_in: float, eps_out: float):
     """Forward on prepared operands: pair (G, P, C); float32 mask (G, P); w_cat [4H][c_row]; wo [C][h_row];
     wog [C][c_row]; the float32 biases and LayerNorm affines in ``small`` (``spans``).  Returns (out, xn,
     mean_in, rstd_in, factors, combined, nrm, mean_out, rstd_out); all but ``out`` are kept for the backward."""
@@ -391,6 +380,23 @@ def trimul_forward(
     return out, xn, mean_in, rstd_in, factors, combined, nrm, mean_out, rstd_out
 
 
+@torch.library.custom_op("oops_amd::trimul_forward", mutates_args=(), device_types="cuda")
+def trimul_forward(
+    pair: Tensor,
+    mask: Optional[Tensor],
+    w_cat: Tensor,
+    wo: Tensor,
+    wog: Tensor,
+    small: Tensor,
+    spans: List[int],
+    blocks: List[int],
+    direction: str,
+    eps_in: float,
+    eps_out: float,
+) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    return _forward_impl(pair, mask, w_cat, wo, wog, small, spans, blocks, direction, eps_in, eps_out)
+
+
 @trimul_forward.register_fake
 def _(pair, mask, w_cat, wo, wog, small, spans, blocks, direction, eps_in, eps_out):
     G, P, C = pair.shape
@@ -402,30 +408,10 @@ def _(pair, mask, w_cat, wo, wog, small, spans, blocks, direction, eps_in, eps_o
             pair.new_empty(R, wo.shape[1]), pair.new_empty(R, **f32), pair.new_empty(R, **f32))  # fmt: skip
 
 
-@torch.library.custom_op("oops_amd::trimul_backward", mutates_args=(), device_types="cuda")
-def trimul_backward(
-    dout: Tensor,
-    pair: Tensor,
-    mask: Optional[Tensor],
-    w_cat: Tensor,
-    wo: Tensor,
-    wog: Tensor,
-    small: Tensor,
-    spans: List[int],
-    xn: Tensor,
-    mean_in: Tensor,
-    rstd_in: Tensor,
-    factors: Tensor,
-    combined: Tensor,
-    nrm: Tensor,
-    mean_out: Tensor,
-    rstd_out: Tensor,
-    blocks: List[int],
-    direction: str,
-    eps_in: float,
-    eps_out: float,
-    need_mask: bool,
-) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+def _backward_impl(dout: Tensor, pair: Tensor, mask: Optional[Tensor], w_cat: Tensor, wo: Tensor, wog: Tensor,
+                   small: Tensor, spans: List[int], xn: Tensor, mean_in: Tensor, rstd_in: Tensor, factors: Tensor,
+                   combined: Tensor, nrm: Tensor, mean_out: Tensor, rstd_out: Tensor, blocks: List[int],
+                   direction: str, eps_in: float, eps_out: float, need_mask: bool):  # fmt: skip
     """Gradients of the prepared operands: (pair, mask, w_cat, wo, wog, small); the mask gradient is empty
     when not needed."""
 
@@ -525,6 +511,34 @@ def trimul_backward(
     return d_pair, d_mask, d_wcat, d_wo, d_wog, d_small
 
 
+@torch.library.custom_op("oops_amd::trimul_backward", mutates_args=(), device_types="cuda")
+def trimul_backward(
+    dout: Tensor,
+    pair: Tensor,
+    mask: Optional[Tensor],
+    w_cat: Tensor,
+    wo: Tensor,
+    wog: Tensor,
+    small: Tensor,
+    spans: List[int],
+    xn: Tensor,
+    mean_in: Tensor,
+    rstd_in: Tensor,
+    factors: Tensor,
+    combined: Tensor,
+    nrm: Tensor,
+    mean_out: Tensor,
+    rstd_out: Tensor,
+    blocks: List[int],
+    direction: str,
+    eps_in: float,
+    eps_out: float,
+    need_mask: bool,
+) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    return _backward_impl(dout, pair, mask, w_cat, wo, wog, small, spans, xn, mean_in, rstd_in, factors, combined,
+                          nrm, mean_out, rstd_out, blocks, direction, eps_in, eps_out, need_mask)  # fmt: skip
+
+
 @trimul_backward.register_fake
 def _(dout, pair, mask, w_cat, wo, wog, small, spans, xn, mean_in, rstd_in, factors, combined, nrm, mean_out,
       rstd_out, blocks, direction, eps_in, eps_out, need_mask):  # fmt: skip
@@ -535,32 +549,58 @@ def _(dout, pair, mask, w_cat, wo, wog, small, spans, xn, mean_in, rstd_in, fact
             torch.empty_like(small))  # fmt: skip
 
 
-def _setup_context(ctx, inputs, output):
+def _save(ctx, inputs, output):
     pair, mask, w_cat, wo, wog, small, spans, blocks, direction, eps_in, eps_out = inputs
     _out, xn, mean_in, rstd_in, factors, combined, nrm, mean_out, rstd_out = output
     ctx.save_for_backward(pair, mask, w_cat, wo, wog, small, xn, mean_in, rstd_in, factors, combined, nrm,
                           mean_out, rstd_out)  # fmt: skip
     ctx.args = (spans, blocks, direction, eps_in, eps_out)
     ctx.has_mask = mask is not None
-    for t in output[1:]:
-        ctx.mark_non_differentiable(t)
     ctx.set_materialize_grads(False)  # no zero-filled gradients for the saved intermediates
 
 
-def _backward(ctx, dout, *_unused):
+def _setup_context(ctx, inputs, output):
+    _save(ctx, inputs, output)
+    for t in output[1:]:
+        ctx.mark_non_differentiable(t)
+
+
+def _grads(ctx, dout, backward):
+    """Gradients of trimul_forward's 11 inputs."""
+
     if dout is None:
         return (None,) * 11
     pair, mask, w_cat, wo, wog, small, *rest = ctx.saved_tensors
     spans, blocks, direction, eps_in, eps_out = ctx.args
     need = ctx.needs_input_grad
-    d_pair, d_mask, d_wcat, d_wo, d_wog, d_small = trimul_backward(
+    d_pair, d_mask, d_wcat, d_wo, d_wog, d_small = backward(
         dout, pair, mask, w_cat, wo, wog, small, spans, *rest, blocks, direction, eps_in, eps_out, bool(need[1])
     )
     d_mask = d_mask if ctx.has_mask and need[1] else None
     return d_pair, d_mask, d_wcat, d_wo, d_wog, d_small, None, None, None, None, None
 
 
+def _backward(ctx, dout, *_unused):
+    return _grads(ctx, dout, trimul_backward)
+
+
 trimul_forward.register_autograd(_backward, setup_context=_setup_context)
+
+
+class _EagerTrimul(torch.autograd.Function):
+    """The same implementations as the custom ops, for eager calls: autograd
+    calls the backward directly instead of through the operator dispatcher.
+    Traced code (torch.compile), fake and subclass tensors take the custom ops."""
+
+    @staticmethod
+    def forward(ctx, *inputs):
+        output = _forward_impl(*inputs)
+        _save(ctx, inputs, output)
+        return output[0]
+
+    @staticmethod
+    def backward(ctx, dout):
+        return _grads(ctx, dout, _backward_impl)
 
 
 def _prepare(grouped: Tensor, mask: Optional[Tensor], weights, biases):
@@ -602,7 +642,13 @@ def _run(grouped: Tensor, mask: Optional[Tensor], blocks, direction, weights, bi
     _admit(grouped, weights, biases)
     flat = [v for block in blocks for v in block]
     operands = _prepare(grouped, mask, weights, biases)
-    return trimul_forward(*operands, flat, direction, float(eps_in), float(eps_out))[0]
+    args = (*operands, flat, direction, float(eps_in), float(eps_out))
+    if torch.compiler.is_compiling() or type(grouped) is not Tensor or _get_current_dispatch_mode() is not None:
+        # traced, fake or subclass tensors: the custom op (with its fake kernel)
+        return trimul_forward(*args)[0]
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in operands[:6]):
+        return _EagerTrimul.apply(*args)
+    return _forward_impl(*args)[0]
 
 
 # ----------------------------------------------------------------- nested

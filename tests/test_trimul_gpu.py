@@ -133,15 +133,15 @@ def test_trimul_float_mask_gradient_and_broadcast(dtype):
 
 
 def test_trimul_float32_runs_the_fused_kernels(monkeypatch):
-    """float32 pairs go through the same fused custom op as 16-bit ones (the float32 MFMA kernels of
+    """float32 pairs go through the same fused implementation as 16-bit ones (the float32 MFMA kernels of
     csrc/trimul_f32.hip), not a composition of library ops."""
 
     import importlib
 
     mod = importlib.import_module("oops_amd.pair.triangle_multiplication")
     calls = []
-    orig = mod.trimul_forward
-    monkeypatch.setattr(mod, "trimul_forward", lambda *a: calls.append(a[0].dtype) or orig(*a))
+    orig = mod._forward_impl
+    monkeypatch.setattr(mod, "_forward_impl", lambda *a: calls.append(a[0].dtype) or orig(*a))
     dtype = torch.float32
     g = torch.Generator().manual_seed(9)
     pair = torch.randn(2, 9, 9, 24, generator=g).to(DEV).requires_grad_(True)
