@@ -26,10 +26,10 @@ from collections import OrderedDict
 from typing import List, Optional, Sequence, Tuple
 
 import torch
-from torch.utils._python_dispatch import _get_current_dispatch_mode
 from torch import Tensor
 
 from .. import _lib
+from ._runtime import needs_custom_op
 
 _DTYPE_CODE = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
 SUPPORTED_DTYPES = tuple(_DTYPE_CODE)
@@ -545,8 +545,7 @@ def attend(q, k, v, mask, bias, table, num_heads, scale, lse_numel) -> Tensor:
     save = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (q, k, v, bias)
     )
-    if torch.compiler.is_compiling() or type(q) is not Tensor or _get_current_dispatch_mode() is not None:
-        # traced, fake or subclass tensors: the custom op (with its fake kernel)
+    if needs_custom_op(q):
         out, _, _ = attention_forward(q, k, v, mask, bias, table, num_heads, scale, lse_numel, save)
     elif save:
         out = _EagerAttention.apply(q, k, v, mask, bias, table, num_heads, scale, lse_numel)

@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import torch
 from torch.autograd import forward_ad
+from torch.utils._python_dispatch import _get_current_dispatch_mode
 
 from .._errors import unsupported
 
@@ -46,3 +47,11 @@ def require_same_device(operator: str, *tensors) -> None:
     devices = {t.device for t in tensors if isinstance(t, torch.Tensor)}
     if len(devices) > 1:
         raise ValueError(f"{operator} operands must share one device, got {sorted(map(str, devices))}")
+
+
+def needs_custom_op(tensor) -> bool:
+    """True where an operator must go through its ``torch.library`` custom op (fake kernel, traced
+    graph): under ``torch.compile``, for fake or subclass tensors and under a Python dispatch mode.
+    Elsewhere eager calls may skip the dispatcher."""
+
+    return torch.compiler.is_compiling() or type(tensor) is not torch.Tensor or _get_current_dispatch_mode() is not None

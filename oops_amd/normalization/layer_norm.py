@@ -21,11 +21,10 @@ from typing import Iterable, Optional, Tuple, Union
 
 import torch
 from torch import Tensor
-from torch.utils._python_dispatch import _get_current_dispatch_mode
 
 from .. import _lib
 from .._errors import unsupported
-from ..attention._runtime import is_nested, require_no_forward_mode, require_same_device
+from ..attention._runtime import is_nested, needs_custom_op, require_no_forward_mode, require_same_device
 
 _OPERATOR = "layer_norm"
 _HALF = (torch.float16, torch.bfloat16)
@@ -280,8 +279,7 @@ def _apply(x: Tensor, weight: Optional[Tensor], bias: Optional[Tensor], eps: flo
     if x2.stride(1) != 1 or (rows > 1 and x2.stride(0) < width):
         x2 = x2.contiguous()
     f32 = lambda t: None if t is None else t.resolve_neg().float().contiguous()  # noqa: E731
-    if torch.compiler.is_compiling() or type(x2) is not Tensor or _get_current_dispatch_mode() is not None:
-        # traced, fake or subclass tensors: the custom op (with its fake kernel)
+    if needs_custom_op(x2):
         y, _, _ = layer_norm_forward(x2, f32(weight), f32(bias), eps)
     else:
         y = _EagerLayerNorm.apply(x2, f32(weight), f32(bias), eps)

@@ -28,13 +28,12 @@ from typing import List, Literal, Optional, Sequence, Tuple
 
 import torch
 from torch import Tensor
-from torch.utils._python_dispatch import _get_current_dispatch_mode
 from torch.nn import functional as F
 
 from .. import _lib
 from .._errors import unsupported
 from .._partials import PartialSums
-from ..attention._runtime import is_nested, require_no_forward_mode, require_same_device
+from ..attention._runtime import is_nested, needs_custom_op, require_no_forward_mode, require_same_device
 
 _OPERATOR = "triangle_multiplication"
 _KERNEL_DTYPES = (torch.bfloat16, torch.float16)
@@ -643,8 +642,7 @@ def _run(grouped: Tensor, mask: Optional[Tensor], blocks, direction, weights, bi
     flat = [v for block in blocks for v in block]
     operands = _prepare(grouped, mask, weights, biases)
     args = (*operands, flat, direction, float(eps_in), float(eps_out))
-    if torch.compiler.is_compiling() or type(grouped) is not Tensor or _get_current_dispatch_mode() is not None:
-        # traced, fake or subclass tensors: the custom op (with its fake kernel)
+    if needs_custom_op(grouped):
         return trimul_forward(*args)[0]
     if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in operands[:6]):
         return _EagerTrimul.apply(*args)

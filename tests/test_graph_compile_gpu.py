@@ -102,3 +102,4 @@ def test_pair_bias_compile_matches_eager():
         results.append((out.detach(), *torch.autograd.grad(out, leaves, dout)))
     for got, ref in zip(*results):
         torch.testing.assert_close(got, ref, atol=0, rtol=0)
+
