@@ -34,7 +34,10 @@ constexpr int kMaxParts = 64;
 // a dBias part shorter than this spends more on its set-up and partial-sum store than on groups
 constexpr int64_t kMinPartGroups = OOPS_MIN_PART_GROUPS;
 constexpr size_t kMaxBiasFragBytes = size_t(1) << 30;
-constexpr int64_t kTargetFusedBlocks = 768;  // three rounds of one workgroup per CU on 256 CUs
+#ifndef OOPS_FUSED_BLOCKS
+#define OOPS_FUSED_BLOCKS 768
+#endif
+constexpr int64_t kTargetFusedBlocks = OOPS_FUSED_BLOCKS;  // three rounds of one workgroup per CU on 256 CUs
 constexpr int64_t kMinFusedPartGroups = 16;
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
