@@ -29,7 +29,7 @@ import torch
 from torch import Tensor
 
 from .. import _lib
-from ._runtime import needs_custom_op
+from ._runtime import needs_custom_op, without_second_derivative
 
 _DTYPE_CODE = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
 SUPPORTED_DTYPES = tuple(_DTYPE_CODE)
@@ -490,7 +490,7 @@ class _EagerAttention(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout):
-        return _grads(ctx, dout, _backward_impl)[:9]
+        return without_second_derivative(_grads(ctx, dout, _backward_impl)[:9], ctx, dout)
 
 
 # ----------------------------------------------------------------- table rows

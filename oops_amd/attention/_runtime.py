@@ -8,6 +8,7 @@ Restates the contract pieces of the reference's runtime helpers
 from __future__ import annotations
 
 import torch
+from torch._C import _functions as _autograd_nodes
 from torch.autograd import forward_ad
 from torch.utils._python_dispatch import _get_current_dispatch_mode
 
@@ -55,3 +56,23 @@ def needs_custom_op(tensor) -> bool:
     Elsewhere eager calls may skip the dispatcher."""
 
     return torch.compiler.is_compiling() or type(tensor) is not torch.Tensor or _get_current_dispatch_mode() is not None
+
+
+def without_second_derivative(grads, ctx, grad_output):
+    """Gradients that a kernel computed have no derivatives of their own.  When a backward runs under
+    ``create_graph=True`` and ``grad_output`` or any tensor ``ctx`` saved is differentiable, the non-None ``grads`` come back as outputs of an autograd node that raises if it
+    is differentiated, so a second derivative fails loudly instead of silently missing these terms.
+    (The custom-op path raises the same way: its backward operator has no autograd formula.)"""
+
+    if not torch.is_grad_enabled():  # (an ordinary backward: the saved tensors are not unpacked)
+        return grads
+    inputs = (grad_output, *ctx.saved_tensors)
+    if not any(isinstance(t, torch.Tensor) and t.requires_grad for t in inputs):
+        return grads
+    present = [g for g in grads if g is not None]
+    if not present:
+        return grads
+    node = _autograd_nodes.DelayedError(b"oops_amd operators have no second derivatives", len(present))
+    wrapped = node(*[g.detach().requires_grad_() for g in present])
+    wrapped = iter(wrapped if isinstance(wrapped, tuple) else (wrapped,))
+    return tuple(None if g is None else next(wrapped) for g in grads)

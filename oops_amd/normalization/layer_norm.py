@@ -24,7 +24,13 @@ from torch import Tensor
 
 from .. import _lib
 from .._errors import unsupported
-from ..attention._runtime import is_nested, needs_custom_op, require_no_forward_mode, require_same_device
+from ..attention._runtime import (
+    is_nested,
+    needs_custom_op,
+    require_no_forward_mode,
+    require_same_device,
+    without_second_derivative,
+)
 
 _OPERATOR = "layer_norm"
 _HALF = (torch.float16, torch.bfloat16)
@@ -265,7 +271,7 @@ class _EagerLayerNorm(torch.autograd.Function):
     def backward(ctx, dy):
         if dy is None:
             return None, None, None, None
-        return _grads(ctx, dy, _backward_impl)
+        return without_second_derivative(_grads(ctx, dy, _backward_impl), ctx, dy)
 
 
 def _apply(x: Tensor, weight: Optional[Tensor], bias: Optional[Tensor], eps: float) -> Tensor:

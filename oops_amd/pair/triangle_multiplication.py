@@ -33,7 +33,13 @@ from torch.nn import functional as F
 from .. import _lib
 from .._errors import unsupported
 from .._partials import PartialSums
-from ..attention._runtime import is_nested, needs_custom_op, require_no_forward_mode, require_same_device
+from ..attention._runtime import (
+    is_nested,
+    needs_custom_op,
+    require_no_forward_mode,
+    require_same_device,
+    without_second_derivative,
+)
 
 _OPERATOR = "triangle_multiplication"
 _KERNEL_DTYPES = (torch.bfloat16, torch.float16)
@@ -599,7 +605,7 @@ class _EagerTrimul(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout):
-        return _grads(ctx, dout, _backward_impl)
+        return without_second_derivative(_grads(ctx, dout, _backward_impl), ctx, dout)
 
 
 def _prepare(grouped: Tensor, mask: Optional[Tensor], weights, biases):

@@ -219,3 +219,31 @@ def test_layer_norm_fake_shapes():
         y = layer_norm(x, 128, w, w)
         assert is_fake(y)
         assert y.shape == x.shape and y.dtype == x.dtype
+
+
+def test_without_second_derivative():
+    """Kernel gradients carry a node that raises when differentiated under create_graph=True, and are
+    returned unchanged (no node) by an ordinary backward."""
+
+    from oops_amd.attention._runtime import without_second_derivative
+
+    class Square(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, x, y):
+            ctx.save_for_backward(x)
+            return x * x
+
+        @staticmethod
+        def backward(ctx, g):
+            (x,) = ctx.saved_tensors
+            with torch.no_grad():
+                gx = 2 * x * g
+            return without_second_derivative((gx, None), ctx, g)
+
+    x = torch.randn(5, requires_grad=True)
+    (plain,) = torch.autograd.grad(Square.apply(x, None).sum(), x)
+    assert plain.grad_fn is None
+    (first,) = torch.autograd.grad(Square.apply(x, None).sum(), x, create_graph=True)
+    torch.testing.assert_close(first, plain, rtol=0, atol=0)
+    with pytest.raises(RuntimeError, match="no second derivatives"):
+        first.sum().backward()
